@@ -1,0 +1,17 @@
+"""alveare_amd -- MI355X-native (gfx950) Q4 decode hot path of Alveare.
+
+HIP kernels behind a C ABI (``include/alveare_q4.h``, ``libalveare_q4.so``)
+for the three quantized matmuls of Alveare's runtime -- ``gemv_q``,
+``ffn_fused`` and ``gemm_q`` -- with torch-facing ops (``alveare_amd.ops``)
+and the ``runtime/py`` dispatch (``alveare_amd.runtime``) on top.
+"""
+from ._lib import LibraryNotBuilt, Q4Error, Q4ValueError, lib
+from .ops import (FfnWeights, dequant_q4, ffn_fused, ffn_fused_npu, gemm_q, gemm_q_npu, gemv_q,
+                  gemv_q_npu, pack_ffn_fused_weights)
+from .runtime import LazyLayerWeights, Q4Dispatch, ResidentWeight
+
+__all__ = [
+    "FfnWeights", "LazyLayerWeights", "LibraryNotBuilt", "Q4Dispatch", "Q4Error", "Q4ValueError",
+    "ResidentWeight", "dequant_q4", "ffn_fused", "ffn_fused_npu", "gemm_q", "gemm_q_npu", "gemv_q",
+    "gemv_q_npu", "lib", "pack_ffn_fused_weights",
+]

@@ -1,0 +1,136 @@
+// Device-side building blocks shared by the gfx950 Q4 kernels.
+//
+// Q4 combined layout (tools/convert/gemv_q_convert.py:53-85): per row, K/32
+// blocks of 20 bytes = 16 bytes of nibbles (byte i holds column 2i in the low
+// nibble and 2i+1 in the high nibble, two's complement), a little-endian bf16
+// scale at bytes 16-17, and 2 zero bytes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/alveare_q4.h"
+
+namespace alv {
+
+typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
+typedef float f32x2 __attribute__((__vector_size__(2 * sizeof(float))));
+typedef uint32_t u32x4 __attribute__((__vector_size__(4 * sizeof(uint32_t))));
+
+constexpr int kBlockBytes = 20;  // bytes per 32 weights
+constexpr int kBlockK = 32;      // weights per block
+
+// Buffer resource over [base, base + bytes): loads past the end return 0
+// instead of faulting. dword3 = 0x00020000 is the raw 32-bit data format on gfx9.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h16) {
+    return __builtin_bit_cast(float, h16 << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (v_cvt_pk_bf16_f32 on gfx950), returned
+// as the fp32 value it represents.
+__device__ __forceinline__ float bf16_round(float v) {
+    __bf16 h = (__bf16)v;
+    return (float)h;
+}
+
+// Per-block scale constants for dequant8: s512 = 512*s, sm8 = -8*s. Both are
+// exact (power-of-two multiples) for |s| < 2^118.
+struct Scale {
+    float s512, sm8;
+};
+
+__device__ __forceinline__ Scale make_scale(float s) { return Scale{s * 512.0f, s * -8.0f}; }
+
+// Eight weights from one dword of nibbles, exactly as the reference dequantizes
+// them: w = bf16_RNE(f32(q) * f32(s)) (tools/ref/gemv_q.py:19-37).
+//
+// XOR 0x8 turns each two's-complement nibble q into q + 8 in [0, 15]. A byte
+// 0x0u read as OCP FP8 E4M3 is exactly u * 2^-9 (exponent field 0 is the
+// subnormal range, 1 the first normal binade, both at step 2^-9), so
+// v_cvt_pk_f32_fp8 yields (q + 8) * 2^-9 for two weights per instruction, and
+// fma((q+8) 2^-9, 512 s, -8 s) is q*s with a single rounding of an exactly
+// representable value, i.e. exact. The bf16 conversion then rounds to nearest
+// even like the reference's astype(bfloat16).
+//
+// Output element e is column 8*t + e of the block when d is the block's
+// dword t (natural column order).
+__device__ __forceinline__ bf16x8 dequant8(uint32_t d, Scale s) {
+    d ^= 0x88888888u;
+    const uint32_t lo = d & 0x0F0F0F0Fu;         // columns 0, 2, 4, 6
+    const uint32_t hi = (d >> 4) & 0x0F0F0F0Fu;  // columns 1, 3, 5, 7
+    const f32x2 l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
+    const f32x2 l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+    const f32x2 h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+    const f32x2 h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+    bf16x8 r;
+    r[0] = (__bf16)__builtin_fmaf(l01[0], s.s512, s.sm8);
+    r[1] = (__bf16)__builtin_fmaf(h01[0], s.s512, s.sm8);
+    r[2] = (__bf16)__builtin_fmaf(l01[1], s.s512, s.sm8);
+    r[3] = (__bf16)__builtin_fmaf(h01[1], s.s512, s.sm8);
+    r[4] = (__bf16)__builtin_fmaf(l23[0], s.s512, s.sm8);
+    r[5] = (__bf16)__builtin_fmaf(h23[0], s.s512, s.sm8);
+    r[6] = (__bf16)__builtin_fmaf(l23[1], s.s512, s.sm8);
+    r[7] = (__bf16)__builtin_fmaf(h23[1], s.s512, s.sm8);
+    return r;
+}
+
+// Exact split of an fp32 value into three bf16 terms, x == p0 + p1 + p2 for
+// every finite x whose low part does not underflow: p0 = RNE(x) leaves a
+// residual with at most 16 significant bits, p1 = RNE(residual) leaves at most
+// 8, which p2 holds exactly. Products p_i * w (bf16 * bf16) are exact in fp32,
+// so an MFMA over the three terms is an fp32 dot product with the exact x.
+struct Split3 {
+    __bf16 p0, p1, p2;
+};
+
+__device__ __forceinline__ Split3 split3(float x) {
+    Split3 s;
+    s.p0 = (__bf16)x;
+    const float r1 = x - (float)s.p0;  // exact
+    s.p1 = (__bf16)r1;
+    const float r2 = r1 - (float)s.p1;  // exact
+    s.p2 = (__bf16)r2;
+    return s;
+}
+
+// D(16x16, fp32) += A(16x32, bf16) * B(32x16, bf16). Lane l supplies row l%16
+// of A and column l%16 of B for k-group l/16 (8 elements each); the result
+// lane l holds D[4*(l/16) + r][l%16], r = 0..3.
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// GeGLU / SwiGLU of one element with the reference CPU path's dtype flow
+// (runtime/py/model.py:800-803 under NumPy >= 2 promotion; :856 for SiLU):
+// the cubic and the inner sum are fp32 (python floats are weak scalars),
+// np.sqrt(2/np.pi) is a float64 scalar so tanh and the two products are
+// float64, and the result reaches bf16 through fp32 (the caller rounds).
+// Contraction is off so every fp32 operation rounds where numpy's does.
+__device__ __forceinline__ float glu_act(float g, float u, int act) {
+#pragma clang fp contract(off)
+    if (act == ALV_ACT_GELU_TANH) {
+        const float g3 = (g * g) * g;
+        const float inner = g + 0.044715f * g3;
+        const double t = tanh(0.7978845608028654 * (double)inner);
+        const double gl = (double)(0.5f * g) * (1.0 + t);
+        return (float)(gl * (double)u);
+    }
+    const float r = 1.0f / (1.0f + expf(-g));
+    return (g * r) * u;
+}
+
+}  // namespace alv

@@ -1,0 +1,246 @@
+"""Torch-facing Q4 ops over the C ABI, mirroring the reference's op interface.
+
+Canonical names and the reference's IRON names (``kernels/*/<name>.py``):
+
+=================  =====================================================
+``gemv_q``         ``gemv_q_npu(W, X, Y, *, N, K, m, k_tile)``
+                   (kernels/gemv_q/gemv_q.py:33-42)
+``gemm_q``         ``gemm_q_npu(W, X, Y, *, B, N, K, m, k_tile)``
+                   (kernels/gemm_q/gemm_q.py:28-39)
+``ffn_fused``      ``ffn_fused_npu(W_fused, X, Y_partial, *, H, I, m_I,
+                   k_tile, activation)`` (kernels/ffn_fused/ffn_fused.py:28-39)
+``pack_ffn_fused_weights``  same name, kernels/ffn_fused/ffn_fused.py:330-395
+                   and runtime/cpp/src/weights.cpp:94-190
+=================  =====================================================
+
+Buffers are torch tensors on the GPU. As in the reference (the
+``_patched_validate`` hook, runtime/py/model.py:12-21) a buffer may be larger
+than the op needs; only a buffer that is too small raises. Activations may be
+float32 or bfloat16; outputs float32 receive the fp32 result before the
+reference's final bf16 cast, outputs bfloat16 receive that cast (round to
+nearest even). ``m``, ``k_tile`` and ``m_I`` are NPU tiling parameters; they
+are accepted for signature compatibility and do not change the result.
+
+Work is enqueued on torch's current stream of the tensors' device.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import ALV_ACT_GELU_TANH, ALV_ACT_SILU, check, lib
+
+_ACTS = {"gelu": ALV_ACT_GELU_TANH, "gelu_tanh": ALV_ACT_GELU_TANH, "silu": ALV_ACT_SILU}
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need_gpu(*ts: torch.Tensor) -> torch.device:
+    dev = None
+    for t in ts:
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"expected a torch.Tensor, got {type(t).__name__}")
+        if t.device.type != "cuda":
+            raise ValueError("alveare_amd ops run on the GPU; got a tensor on " + str(t.device))
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _too_small(name: str, actual: int, expected: int) -> None:
+    if actual < expected:
+        raise RuntimeError(f"Tensor too small. Actual: {actual}, Expected: {expected} ({name})")
+
+
+def _weight(W: torch.Tensor, N: int, K: int, name: str = "W") -> torch.Tensor:
+    if W.dtype != torch.uint8:
+        raise TypeError(f"{name} must be uint8 in the combined Q4 layout, got {W.dtype}")
+    if not W.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    _too_small(name, W.numel(), N * (K // 32) * 20)
+    return W
+
+
+def _act_in(X: torch.Tensor, n: int, name: str) -> torch.Tensor:
+    _too_small(name, X.numel(), n)
+    X = X.reshape(-1)[:n]
+    if X.dtype == torch.bfloat16:
+        X = X.float()
+    elif X.dtype != torch.float32:
+        raise TypeError(f"{name} must be float32 or bfloat16, got {X.dtype}")
+    return X.contiguous()
+
+
+def _check_shape(N: int, K: int) -> None:
+    if N < 1 or K < 32 or K % 32:
+        raise ValueError(f"bad shape N={N} K={K}: K must be a positive multiple of 32")
+
+
+def _store(Y: torch.Tensor, y32: torch.Tensor, n: int) -> None:
+    flat = Y.view(-1)
+    if flat.data_ptr() == y32.data_ptr():
+        return
+    flat[:n].copy_(y32.reshape(-1))  # bf16 targets: round to nearest even
+
+
+def _out_buffer(Y: torch.Tensor, n: int, name: str) -> torch.Tensor:
+    _too_small(name, Y.numel(), n)
+    if Y.dtype == torch.float32 and Y.is_contiguous():
+        return Y.view(-1)[:n]
+    if Y.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"{name} must be float32 or bfloat16, got {Y.dtype}")
+    return torch.empty(n, dtype=torch.float32, device=Y.device)
+
+
+def gemv_q(W: torch.Tensor, X: torch.Tensor, Y: torch.Tensor, *, N: int, K: int,
+           m: int = 32, k_tile: int = 256) -> torch.Tensor:
+    """Y[:N] = dequant(W)[N, K] @ X[:K] (tools/ref/gemv_q.py:73-80)."""
+    _check_shape(N, K)
+    _need_gpu(W, X, Y)
+    _weight(W, N, K)
+    x = _act_in(X, K, "X")
+    y = _out_buffer(Y, N, "Y")
+    with torch.cuda.device(W.device):
+        check(lib().alv_gemv_q(W.data_ptr(), x.data_ptr(), y.data_ptr(), N, K, _stream(W)), "alv_gemv_q")
+    _store(Y, y, N)
+    return Y
+
+
+def gemm_q(W: torch.Tensor, X: torch.Tensor, Y: torch.Tensor, *, B: int, N: int, K: int,
+           m: int = 32, k_tile: int = 256) -> torch.Tensor:
+    """Y[B, N] = X[B, K] @ dequant(W)^T, row-major (runtime/py/model.py:1049-1111)."""
+    _check_shape(N, K)
+    if B < 1:
+        raise ValueError(f"bad batch B={B}")
+    _need_gpu(W, X, Y)
+    _weight(W, N, K)
+    x = _act_in(X, B * K, "X")
+    y = _out_buffer(Y, B * N, "Y")
+    with torch.cuda.device(W.device):
+        check(lib().alv_gemm_q(W.data_ptr(), x.data_ptr(), y.data_ptr(), B, N, K, K, N, _stream(W)),
+              "alv_gemm_q")
+    _store(Y, y, B * N)
+    return Y
+
+
+def dequant_q4(W: torch.Tensor, N: int, K: int) -> torch.Tensor:
+    """bf16 (N, K) = dequant(W) (tools/ref/gemv_q.py:39-62); parity entry point."""
+    _check_shape(N, K)
+    _need_gpu(W)
+    _weight(W, N, K)
+    out = torch.empty((N, K), dtype=torch.bfloat16, device=W.device)
+    with torch.cuda.device(W.device):
+        check(lib().alv_dequant_q4(W.data_ptr(), out.data_ptr(), N, K, _stream(W)), "alv_dequant_q4")
+    return out
+
+
+class FfnWeights:
+    """A registered FFN layer (the device-resident analogue of the reference's
+    fused FFN weight, runtime/cpp/src/npu.cpp:255-267). Owns a device copy of
+    gate/up/down and the activation scratch; released on ``close()`` or
+    garbage collection."""
+
+    def __init__(self, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
+                 H: int, I: int, activation: str = "gelu"):
+        if activation not in _ACTS:
+            raise ValueError(f"unknown activation {activation!r}; expected one of {sorted(_ACTS)}")
+        if H < 32 or I < 32 or H % 32 or I % 32:
+            raise ValueError(f"bad FFN shape H={H} I={I}: both must be positive multiples of 32")
+        dev = _need_gpu(w_gate, w_up, w_down)
+        _weight(w_gate, I, H, "w_gate")
+        _weight(w_up, I, H, "w_up")
+        _weight(w_down, H, I, "w_down")
+        self.H, self.I, self.activation, self.device = H, I, activation, dev
+        self._h = ctypes.c_void_p()
+        with torch.cuda.device(dev):
+            check(lib().alv_ffn_register(w_gate.data_ptr(), w_up.data_ptr(), w_down.data_ptr(), H, I,
+                                         _ACTS[activation], ctypes.byref(self._h), _stream(w_gate)),
+                  "alv_ffn_register")
+        # Lets ffn_fused_npu's caller read .shape like the reference's ResidentWeight.
+        self.shape = (H, I)
+
+    @property
+    def handle(self) -> int:
+        if not self._h:
+            raise ValueError("FFN weights were released")
+        return self._h.value
+
+    def close(self) -> None:
+        if self._h:
+            with torch.cuda.device(self.device):
+                lib().alv_ffn_release(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def last_activation(self, M: int = 1) -> torch.Tensor:
+        """The bf16-valued activation (M, I) of the last call (parity checks)."""
+        out = torch.empty((M, self.I), dtype=torch.float32, device=self.device)
+        with torch.cuda.device(self.device):
+            check(lib().alv_ffn_activation(self.handle, out.data_ptr(), M, _stream(out)),
+                  "alv_ffn_activation")
+        return out
+
+    def __call__(self, X: torch.Tensor, Y: torch.Tensor | None = None, M: int = 1) -> torch.Tensor:
+        x = _act_in(X, M * self.H, "X")
+        if x.device != self.device:
+            raise ValueError(f"X on {x.device}, weights on {self.device}")
+        if Y is None:
+            Y = torch.empty((M, self.H) if M > 1 else (self.H,), dtype=torch.float32, device=self.device)
+        _need_gpu(Y)
+        y = _out_buffer(Y, M * self.H, "Y")
+        with torch.cuda.device(self.device):
+            check(lib().alv_ffn_fused(self.handle, x.data_ptr(), y.data_ptr(), M, self.H, self.H,
+                                      _stream(x)), "alv_ffn_fused")
+        _store(Y, y, M * self.H)
+        return Y
+
+
+def pack_ffn_fused_weights(w_gate, w_up, w_down, H: int, I: int, m_I: int = 32,
+                           k_tile: int = 256, activation: str = "gelu", device=None) -> FfnWeights:
+    """Register gate/up/down (combined Q4 layout, torch uint8 tensors or numpy
+    arrays) as one device-resident FFN. The reference packs an NPU tile stream
+    here; on the GPU the handle keeps its own copy in the kernels' layout."""
+    dev = torch.device(device) if device is not None else None
+
+    def to_dev(w):
+        if isinstance(w, torch.Tensor):
+            return w.contiguous() if dev is None else w.to(dev).contiguous()
+        return torch.from_numpy(w.reshape(w.shape[0], -1).copy()).to(dev or "cuda")
+
+    return FfnWeights(to_dev(w_gate), to_dev(w_up), to_dev(w_down), H, I, activation)
+
+
+def ffn_fused(W_fused: FfnWeights, X: torch.Tensor, Y_partial: torch.Tensor, *, H: int, I: int,
+              m_I: int = 32, k_tile: int = 256, activation: str = "gelu", M: int = 1) -> torch.Tensor:
+    """Y_partial[:H] (or [:M*H]) = down(GLU(gate X, up X)). The reference writes
+    one partial row per NPU core and its caller sums them
+    (runtime/py/model.py:394-395); here the sum is finished on the device, so
+    the result is the single row Y_partial[0] (a sum over axis 0 of a (1, H)
+    view is the identity)."""
+    if not isinstance(W_fused, FfnWeights):
+        raise TypeError("W_fused must come from pack_ffn_fused_weights")
+    if (H, I) != (W_fused.H, W_fused.I):
+        raise ValueError(f"shape mismatch: registered (H={W_fused.H}, I={W_fused.I}), called with (H={H}, I={I})")
+    if activation not in _ACTS or _ACTS[activation] != _ACTS[W_fused.activation]:
+        raise ValueError(f"activation {activation!r} does not match the registered {W_fused.activation!r}")
+    return W_fused(X, Y_partial, M)
+
+
+# The reference's names for the same ops.
+gemv_q_npu = gemv_q
+gemm_q_npu = gemm_q
+ffn_fused_npu = ffn_fused
+
+__all__ = ["gemv_q", "gemm_q", "ffn_fused", "dequant_q4", "FfnWeights", "pack_ffn_fused_weights",
+           "gemv_q_npu", "gemm_q_npu", "ffn_fused_npu"]

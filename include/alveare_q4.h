@@ -1,0 +1,127 @@
+/*
+ * alveare_q4 -- C ABI of the MI355X (gfx950) Q4 decode hot path.
+ *
+ * Drop-in for the three quantized-matmul backends of Alveare's runtime:
+ * gemv_q, ffn_fused and gemm_q. Weights are in the layout `alveare quantize`
+ * emits: per row, K/32 blocks of 20 bytes (16 bytes of two's-complement
+ * nibbles, low nibble = even column; a little-endian bf16 scale; 2 zero
+ * bytes), i.e. uint8 (N, K/32*20) row-major (tools/convert/gemv_q_convert.py:53-85,
+ * kernels/gemv_q/README.md:13-23).
+ *
+ * Numerics are those of the reference's fp32 CPU path
+ * (tools/ref/gemv_q.py:73-80, runtime/py/model.py:797-806):
+ *   w = bf16_RNE(f32(q) * f32(scale)),  y = sum_k w[k] * x[k] in fp32.
+ * Outputs are the fp32 values before the reference's final `.astype(bfloat16)`;
+ * a caller that wants the reference's bf16 result rounds them to nearest even.
+ *
+ * Conventions:
+ *  - All pointers are device pointers (hipMalloc / torch tensors), except where
+ *    noted. `stream` is a hipStream_t (NULL = the null stream). Work is
+ *    enqueued asynchronously on it; nothing blocks the host.
+ *  - Every entry point returns ALV_OK (0) or a negative ALV_ERR_* status and
+ *    never throws. alv_last_error() returns a message for the calling thread's
+ *    last failure.
+ *  - K must be a positive multiple of 32; N, M, H, I positive. Activations are
+ *    dense fp32, row-major, with the given leading dimensions (in elements).
+ *  - Calls on different streams may run concurrently; calls that share an FFN
+ *    handle must be serialised on one stream (the handle owns its scratch).
+ */
+#ifndef ALVEARE_Q4_H
+#define ALVEARE_Q4_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ALV_OK 0
+#define ALV_ERR_ARG (-1)      /* null pointer, bad shape, bad activation id */
+#define ALV_ERR_ALIGN (-2)    /* pointer alignment the kernels need is not met */
+#define ALV_ERR_HANDLE (-3)   /* invalid or mismatched FFN handle */
+#define ALV_ERR_HIP (-4)      /* a HIP runtime call failed */
+#define ALV_ERR_RANGE (-5)    /* a size exceeds what the kernels address */
+
+#define ALV_ACT_GELU_TANH 0   /* Gemma: gelu_pytorch_tanh (runtime/py/model.py:802) */
+#define ALV_ACT_SILU 1        /* Llama: x*sigmoid(x) (runtime/py/model.py:856) */
+
+typedef struct alv_ffn* alv_ffn_t;
+
+/* Message for the calling thread's last failed call ("" if none). */
+const char* alv_last_error(void);
+
+/* Library version, e.g. "alveare_q4 1.0 gfx950". */
+const char* alv_version(void);
+
+/*
+ * y[N] = dequant(W)[N,K] @ x[K].
+ * Replaces the gemv_q NPU op: IRON `gemv_q_npu(W, X, Y, *, N, K, m, k_tile)`
+ * (kernels/gemv_q/gemv_q.py:33-42) and NpuRegistry::run_gemv
+ * (runtime/cpp/include/alveare/npu.h:78-80, runtime/cpp/src/npu.cpp:269-288).
+ * W needs 4-byte alignment; x and y 4-byte alignment.
+ */
+int alv_gemv_q(const uint8_t* W, const float* x, float* y, int N, int K, void* stream);
+
+/*
+ * Y[M,N] = X[M,K] @ dequant(W)^T, rows of X/Y at leading dimensions ldx/ldy.
+ * Replaces IRON `gemm_q_npu(W, X, Y, *, B, N, K, m, k_tile)`
+ * (kernels/gemm_q/gemm_q.py:28-39) and NpuRegistry::run_gemm
+ * (runtime/cpp/include/alveare/npu.h:82-87, runtime/cpp/src/npu.cpp:290-310).
+ * M is any positive token count (the reference's B=16 chunking is not needed).
+ * Small M runs the streaming GEMV kernel, large M the MFMA tiled kernel.
+ */
+int alv_gemm_q(const uint8_t* W, const float* X, float* Y, int M, int N, int K,
+               int ldx, int ldy, void* stream);
+
+/*
+ * Register one FFN layer: Wg, Wu are (I, H/32*20), Wd is (H, I/32*20), all in
+ * the combined Q4 layout, on the device. The handle keeps its own device copy
+ * in the kernels' layout (the caller may free its buffers after the call
+ * returns) plus scratch for the activation. act is ALV_ACT_*.
+ * Replaces NpuRegistry::create_ffn_fused_weight (npu.h:70-71, npu.cpp:255-267)
+ * together with the registration-time repack pack_ffn_fused_weights
+ * (runtime/cpp/src/weights.cpp:94-190; kernels/ffn_fused/ffn_fused.py:330-395).
+ * Synchronises `stream` before returning.
+ */
+int alv_ffn_register(const uint8_t* Wg, const uint8_t* Wu, const uint8_t* Wd, int H, int I,
+                     int act, alv_ffn_t* out, void* stream);
+
+/*
+ * Y[M,H] = down(GLU(gate X, up X)) with the reference CPU path's bf16 rounding
+ * points: g = bf16(Wg x), u = bf16(Wu x), a = bf16(act(g) * u), y = Wd a (fp32).
+ * Replaces IRON `ffn_fused_npu(W_fused, X, Y_partial, *, H, I, m_I, k_tile,
+ * activation)` (kernels/ffn_fused/ffn_fused.py:28-39) plus the host sum of
+ * the per-core partials (runtime/cpp/src/npu.cpp:340-378,
+ * runtime/py/model.py:363-397); the sum is done on the device.
+ * X and Y are (M, H) row-major with leading dimensions ldx, ldy.
+ */
+int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int ldx, int ldy,
+                  void* stream);
+
+/*
+ * out[M, I] = the activation a = bf16(act(g) * u) of the handle's last
+ * alv_ffn_fused call (fp32 holding bf16 values), for M up to that call's
+ * token count (all tokens when it had M <= 16 or M >= 32; otherwise the last
+ * 16-token chunk). Test / parity entry point: lets a checker separate the
+ * bf16 rounding points from the down projection.
+ */
+int alv_ffn_activation(alv_ffn_t w, float* out, int M, void* stream);
+
+/* Shape of a registered FFN (any output pointer may be NULL). */
+int alv_ffn_shape(alv_ffn_t w, int* H, int* I, int* act);
+
+/* Free a handle from alv_ffn_register (NULL is a no-op). Synchronises the
+ * device before freeing. */
+void alv_ffn_release(alv_ffn_t w);
+
+/*
+ * out[N,K] = bf16 bit patterns of dequant(W). Test / parity entry point: the
+ * reference materialises this matrix in dequantize_combined
+ * (tools/ref/gemv_q.py:39-62).
+ */
+int alv_dequant_q4(const uint8_t* W, uint16_t* out, int N, int K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ALVEARE_Q4_H */

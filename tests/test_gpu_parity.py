@@ -1,0 +1,258 @@
+"""GPU parity of the HIP path against the oracle (C ABI through alveare_amd).
+
+Bars (tests/parity.py): dequant bit-exact; GEMV/GEMM max-relative error
+<= 1e-4 against the oracle plus the per-element fp32 bound against fp64; FFN
+flip-aware (down projection <= 1e-4 at the GPU's own activation, every
+activation flip on a bf16 rounding midpoint within the fp32 bound, end to end
+<= 1e-4 plus the flips' exact contribution).
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import parity
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def to_dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def run_gemv(W, x, N, K, dev):
+    import alveare_amd as aa
+
+    y = torch.empty(N, dtype=torch.float32, device=dev)
+    aa.gemv_q(to_dev(W, dev), to_dev(x, dev), y, N=N, K=K)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+# ---- dequant -------------------------------------------------------------------
+
+def test_dequant_exhaustive_scales(orc, dev):
+    import alveare_amd as aa
+
+    _say("dequant: all bf16 scales with |s| < 2^119, 16 codes x 2 nibble positions")
+    W = np.zeros((65536, 20), np.uint8)
+    lo = np.arange(16, dtype=np.uint8)
+    W[:, :16] = lo | ((15 - lo) << 4)
+    s = np.arange(65536, dtype=np.uint32)
+    W[:, 16], W[:, 17] = s & 0xFF, s >> 8
+    got = aa.dequant_q4(to_dev(W, dev), 65536, 32).view(torch.int16).cpu().numpy().view(np.uint16)
+    want = orc.dequant_q4(W, 65536, 32)
+    exp_field = (s >> 7) & 0xFF
+    dom = exp_field <= 127 + 118  # documented domain: |s| < 2^119
+    assert dom.sum() == 2 * 246 * 128
+    assert np.array_equal(got[dom], want[dom])
+
+
+def test_dequant_random_matches_oracle(orc, dev):
+    import alveare_amd as aa
+
+    N, K = 300, 1152
+    W = orc.synth_q4(N, K, 77)
+    got = aa.dequant_q4(to_dev(W, dev), N, K).view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, orc.dequant_q4(W, N, K))
+
+
+# ---- GEMV ------------------------------------------------------------------------
+
+GEMV_SHAPES = [
+    (2048, 2048, "c1"),       # single gemv_q at the reference CPU path's size
+    (256, 256, "ref42"),      # tests/test_gemv_q.py:76-91 style (seed 42, U(-1,1) quantized)
+    (2560, 2560, "ref42"),    # tests/test_gemv_q.py:93-114
+    (1, 32, "syn"), (17, 96, "syn"), (333, 1152, "syn"), (31, 6912, "syn"),
+    (3840, 4096, "syn"),      # O projection
+    (8192, 3840, "syn"),      # fused QKV at the 12B-class shape
+    (3840, 15360, "syn"),     # FFN down shape
+    (100, 480, "syn"),        # K not a multiple of 128 (partial super-steps)
+]
+
+
+@pytest.mark.parametrize("N,K,kind", GEMV_SHAPES)
+def test_gemv_parity(orc, dev, N, K, kind):
+    _say(f"gemv N={N} K={K} {kind}")
+    if kind == "ref42":
+        rng = np.random.default_rng(42)
+        Wf = rng.uniform(-1.0, 1.0, size=(N, K)).astype(np.float32)
+        x = rng.uniform(-1.0, 1.0, size=(K,)).astype(np.float32)
+        W = orc.quantize_q4_0(Wf)
+    else:
+        W = orc.synth_q4(N, K, orc.seed_for(1, 0) + N + K)
+        x = orc.synth_normal(K, orc.seed_for(1, 1) + K)
+    y = run_gemv(W, x, N, K, dev)
+    err = parity.gemv_check(orc, W, x, y, N, K)
+    _say(f"  max-rel {err:.2e}")
+
+
+def test_gemv_one_hot_and_zero(orc, dev):
+    N, K = 4096, 3840
+    W = orc.synth_q4(N, K, 5)
+    Wd = to_dev(W, dev)
+    import alveare_amd as aa
+
+    deq = aa.dequant_q4(Wd, N, K).float().cpu().numpy()
+    for k in (0, 7, 31, 32, 1000, K - 1):
+        x = np.zeros(K, np.float32)
+        x[k] = 1.0
+        assert np.array_equal(run_gemv(W, x, N, K, dev), deq[:, k])
+    assert np.all(run_gemv(W, np.zeros(K, np.float32), N, K, dev) == 0.0)
+
+
+def test_gemv_deterministic_and_linear(orc, dev):
+    N, K = 3840, 15360  # split-K across workgroups
+    W = orc.synth_q4(N, K, 8)
+    x = orc.synth_normal(K, 9)
+    y1 = run_gemv(W, x, N, K, dev)
+    y2 = run_gemv(W, x, N, K, dev)
+    assert np.array_equal(y1, y2)
+    # Scaling x by a power of two scales every product and sum exactly.
+    y4 = run_gemv(W, 4.0 * x, N, K, dev)
+    assert np.array_equal(y4, 4.0 * y1)
+
+
+def test_gemv_bf16_activation_and_padded_buffers(orc, dev):
+    import alveare_amd as aa
+
+    N, K = 1000, 2048
+    W = orc.synth_q4(N, K, 12)
+    x = orc.bf16_round(orc.synth_normal(K, 13))
+    big_w = torch.zeros(W.size + 4096, dtype=torch.uint8, device=dev)  # oversized buffers are allowed
+    big_w[: W.size] = to_dev(W.reshape(-1), dev)
+    xb = to_dev(x, dev).to(torch.bfloat16)
+    y = torch.full((N + 10,), 7.0, device=dev)
+    aa.gemv_q(big_w, xb, y, N=N, K=K)
+    yc = y.cpu().numpy()
+    parity.gemv_check(orc, W, x, yc[:N], N, K)
+    assert np.all(yc[N:] == 7.0)
+    yb = torch.empty(N, dtype=torch.bfloat16, device=dev)
+    aa.gemv_q(big_w, xb, yb, N=N, K=K)
+    assert torch.equal(yb, y[:N].to(torch.bfloat16))
+    with pytest.raises(RuntimeError, match="too small"):
+        aa.gemv_q(big_w[:100], xb, y, N=N, K=K)
+
+
+# ---- GEMM (small M: streaming kernel; M >= 32: MFMA tiled kernel) -------------------
+
+@pytest.mark.parametrize("M,N,K,bf16x", [(2, 3840, 3840, False), (4, 15360, 3840, False),
+                                          (8, 3840, 15360, False), (16, 3840, 3840, False),
+                                          (19, 1000, 1152, False), (32, 512, 1024, False),
+                                          (64, 2048, 3840, True), (100, 777, 2048, False),
+                                          (512, 1024, 3840, True)])
+def test_gemm_parity(orc, dev, M, N, K, bf16x):
+    import alveare_amd as aa
+
+    _say(f"gemm M={M} N={N} K={K} bf16x={bf16x}")
+    W = orc.synth_q4(N, K, 1000 + M)
+    X = orc.synth_normal(M * K, 2000 + M).reshape(M, K)
+    if bf16x:
+        X = orc.bf16_round(X).reshape(M, K)
+    Y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    aa.gemm_q(to_dev(W, dev), to_dev(X, dev), Y, B=M, N=N, K=K)
+    torch.cuda.synchronize()
+    Yc = Y.cpu().numpy()
+    Yr = orc.gemm_q(W, X, M, N, K)
+    err = parity.max_rel(Yc, Yr)
+    _say(f"  max-rel {err:.2e}")
+    assert err <= parity.TOL
+    for m in sorted({0, M // 2, M - 1}):
+        parity.gemv_check(orc, W, X[m], Yc[m], N, K)
+
+
+# ---- FFN ---------------------------------------------------------------------------
+
+def _ffn_inputs(orc, H, I, kind, seed):
+    if kind == "ref":
+        # tests/test_ffn_fused.py:38-58: seed 1726250518, U(-1,1) weights quantized.
+        rng = np.random.default_rng(1726250518)
+        Wg = orc.quantize_q4_0(rng.uniform(-1, 1, size=(I, H)).astype(np.float32))
+        Wu = orc.quantize_q4_0(rng.uniform(-1, 1, size=(I, H)).astype(np.float32))
+        Wd = orc.quantize_q4_0(rng.uniform(-1, 1, size=(H, I)).astype(np.float32))
+        x = rng.uniform(-1, 1, size=(H,)).astype(np.float32)
+        return Wg, Wu, Wd, x[None, :]
+    Wg, Wu, Wd = orc.synth_q4(I, H, seed), orc.synth_q4(I, H, seed + 1), orc.synth_q4(H, I, seed + 2)
+    return Wg, Wu, Wd, None
+
+
+@pytest.mark.parametrize("H,I,M,act,kind", [(256, 512, 1, "gelu", "ref"), (1024, 2048, 1, "gelu", "syn"),
+                                            (1152, 6912, 1, "gelu", "syn"), (1152, 6912, 1, "silu", "syn"),
+                                            (3840, 15360, 1, "gelu", "syn"), (3840, 15360, 4, "gelu", "syn"),
+                                            (1152, 6912, 16, "gelu", "syn"), (1152, 6912, 64, "gelu", "syn")])
+def test_ffn_parity(orc, dev, H, I, M, act, kind):
+    import alveare_amd as aa
+
+    _say(f"ffn H={H} I={I} M={M} {act} {kind}")
+    seed = orc.seed_for(2, 0) + H + M
+    Wg, Wu, Wd, X = _ffn_inputs(orc, H, I, kind, seed)
+    if X is None:
+        X = orc.synth_normal(M * H, seed + 7).reshape(M, H)
+    ffn = aa.pack_ffn_fused_weights(to_dev(Wg, dev), to_dev(Wu, dev), to_dev(Wd, dev), H, I,
+                                    activation=act)
+    Y = torch.empty((M, H), dtype=torch.float32, device=dev)
+    ffn(to_dev(X, dev), Y, M)
+    A = ffn.last_activation(M).cpu().numpy()
+    Yc = Y.cpu().numpy()
+    a_id = 0 if act == "gelu" else 1
+    worst = 0.0
+    for m in range(M):
+        st = parity.ffn_check(orc, Wg, Wu, Wd, X[m], H, I, a_id, Yc[m], A[m])
+        worst = max(worst, st["max_rel"])
+        if m == 0:
+            _say(f"  token0 {st}")
+    _say(f"  worst end-to-end max-rel {worst:.2e}")
+    ffn.close()
+
+
+def test_ffn_deterministic(orc, dev):
+    import alveare_amd as aa
+
+    H, I = 3840, 15360
+    Wg, Wu, Wd = orc.synth_q4(I, H, 1), orc.synth_q4(I, H, 2), orc.synth_q4(H, I, 3)
+    ffn = aa.pack_ffn_fused_weights(Wg, Wu, Wd, H, I, device=dev)
+    x = to_dev(orc.synth_normal(H, 4), dev)
+    y1 = ffn(x).clone()
+    y2 = ffn(x).clone()
+    assert torch.equal(y1, y2)
+    with pytest.raises(ValueError, match="shape mismatch"):
+        aa.ffn_fused(ffn, x, y1, H=H, I=I + 32)
+    ffn.close()
+
+
+# ---- runtime/py dispatch -------------------------------------------------------------
+
+def test_dispatch_entry_points(orc, dev):
+    from alveare_amd.runtime import Q4Dispatch, ResidentWeight
+
+    H, I = 1152, 6912
+    d = Q4Dispatch(H, I, "gemma3", dev)
+    Wg, Wu, Wd = orc.synth_q4(I, H, 51), orc.synth_q4(I, H, 52), orc.synth_q4(H, I, 53)
+    l = d.register_ffn(Wg, Wu, Wd)
+    x = orc.bf16_round(orc.synth_normal(H, 54))
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    y = d.run_ffn_fused_npu(l, xb)
+    assert y.dtype == torch.bfloat16 and y.shape == (H,)
+    st = parity.ffn_check(orc, Wg, Wu, Wd, x, H, I, 0, y.float().cpu().numpy(),
+                          d.layer_ffn_fused_tensors[l].last_activation(1).cpu().numpy()[0], tol=2 ** -8)
+    # gemv with x shorter than K (zero-padded, model.py:343-346), numpy weights
+    N, K = 1024, 2048
+    W = orc.synth_q4(N, K, 55)
+    xs = orc.bf16_round(orc.synth_normal(1152, 56))
+    yg = d.run_gemv_npu(W, torch.from_numpy(xs).to(torch.bfloat16)).float().cpu().numpy()
+    xp = np.zeros(K, np.float32)
+    xp[:1152] = xs
+    ref = orc.bf16_round(orc.gemv_q(W, xp, N, K))
+    assert parity.max_rel(yg, ref) <= 2 ** -8
+    # resident weights and a batch
+    rw = ResidentWeight(to_dev(W.reshape(-1), dev), W.shape)
+    Xb = orc.bf16_round(orc.synth_normal(5 * K, 57)).reshape(5, K)
+    Yb = d.run_gemm_npu(rw, torch.from_numpy(Xb).to(torch.bfloat16)).float().cpu().numpy()
+    assert parity.max_rel(Yb, orc.bf16_round(orc.gemm_q(W, Xb, 5, N, K))) <= 2 ** -8
+    del st

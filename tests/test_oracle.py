@@ -1,0 +1,339 @@
+"""Pins of the CPU oracle (oracle/) -- CPU only.
+
+Each check is independent of the oracle's own code path: the reference's
+compiled bf16.cpp (oracle/_ref), torch's bf16 cast, the AIE kernel's
+shift-based sign extension, numpy evaluating the reference's own expressions
+(oracle/q4_numpy.py), fp64 brute force, exhaustive tables and closed forms.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import q4_numpy
+
+import parity
+
+
+def _bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return bits.astype(np.uint32).view(np.float32)
+
+
+def _torch_bf16_bits(x: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+# ---- bf16 (runtime/cpp/src/bf16.cpp:7-27) -----------------------------------
+
+def test_bf16_exhaustive_vs_reference_bf16_cpp(orc):
+    ref = orc.ref_lib()
+    if ref is None:
+        pytest.skip("oracle/_ref not built (needs the reference tree: make -C oracle ref)")
+    first = ctypes.c_uint32(0)
+    fn = ctypes.cast(ref.ref_bf16_from_f32, ctypes.c_void_p)
+    bad = orc.lib().orc_bf16_sweep(fn, ctypes.byref(first))
+    assert bad == 0, f"{bad} of 2^32 patterns differ from bf16.cpp, first 0x{first.value:08x}"
+
+
+def test_bf16_vs_torch_and_specials(orc):
+    rng = np.random.default_rng(7)
+    bits = rng.integers(0, 2**32, size=1 << 22, dtype=np.uint64).astype(np.uint32)
+    specials = np.array([0, 0x80000000, 0x7F800000, 0xFF800000, 0x7FC00000, 0x7F800001, 0xFFFFFFFF,
+                         0x00000001, 0x007FFFFF, 0x00800000, 0x3F808000, 0x3F818000, 0x3F807FFF,
+                         0x3F808001, 0x7F7FFFFF, 0x7F7F8000, 0x7F7F7FFF], dtype=np.uint32)
+    # Every tie pattern (low 16 bits exactly 0x8000) for a spread of high halves.
+    ties = (np.arange(0, 1 << 16, 7, dtype=np.uint32) << 16) | 0x8000
+    f = _bits_to_f32(np.concatenate([bits, specials, ties]))
+    # NaN payloads are outside the comparison: torch's vectorised cast keeps
+    # them, the reference's bf16.cpp (pinned exhaustively above) makes 0x7FC0.
+    f = f[~np.isnan(f)]
+    assert np.array_equal(orc.bf16_bits(f), _torch_bf16_bits(f))
+    # NaN -> 0x7FC0 (bf16.cpp:9-11), ties to even, overflow to inf.
+    tb = orc.bf16_bits(_bits_to_f32(np.array([0x7FC00000, 0x3F808000, 0x3F818000, 0x7F7FFFFF], np.uint32)))
+    assert tb.tolist() == [0x7FC0, 0x3F80, 0x3F82, 0x7F80]
+
+
+def test_bf16_numpy_restatement_matches(orc):
+    rng = np.random.default_rng(8)
+    f = _bits_to_f32(rng.integers(0, 2**32, size=1 << 20, dtype=np.uint64).astype(np.uint32))
+    a = q4_numpy.bf16_rne(f).view(np.uint32) >> 16
+    assert np.array_equal(a.astype(np.uint16), orc.bf16_bits(f))
+
+
+# ---- unpack (tools/ref/gemv_q.py:19-31) ---------------------------------------
+
+def _all_bytes_matrix() -> np.ndarray:
+    """16 rows x one block: row r holds bytes 16r .. 16r+15, so all 256 byte
+    values appear once; scale 1.0."""
+    W = np.zeros((16, 20), np.uint8)
+    W[:, :16] = np.arange(256, dtype=np.uint8).reshape(16, 16)
+    W[:, 16], W[:, 17] = 0x80, 0x3F
+    return W
+
+
+def test_unpack_exhaustive_vs_aie_shift_form(orc):
+    W = _all_bytes_matrix()
+    q = orc.unpack_q4(W, 16, 32).reshape(256, 2)
+    b = np.arange(256, dtype=np.int32)
+    # kernels/gemv_q/gemv_q.cc:46-47 sign-extends by int16 shifts: (x<<12)>>12, (x<<8)>>12.
+    lo = ((b << 12).astype(np.int16) >> 12).astype(np.int8)
+    hi = ((b << 8).astype(np.int16) >> 12).astype(np.int8)
+    assert np.array_equal(q[:, 0], lo) and np.array_equal(q[:, 1], hi)
+
+
+def test_pack_unpack_round_trip_all_pairs(orc):
+    q0, q1 = np.meshgrid(np.arange(-8, 8), np.arange(-8, 8), indexing="ij")
+    q0, q1 = q0.ravel(), q1.ravel()
+    # tools/convert/gemv_q_convert.py:46-48 packing.
+    byte = ((q0 & 0x0F) | ((q1 & 0x0F) << 4)).astype(np.uint8)
+    W = np.zeros((16, 20), np.uint8)
+    W[:, :16] = byte.reshape(16, 16)
+    q = orc.unpack_q4(W, 16, 32).reshape(256, 2)
+    assert np.array_equal(q[:, 0], q0) and np.array_equal(q[:, 1], q1)
+
+
+# ---- dequant (tools/ref/gemv_q.py:33-37) ----------------------------------------
+
+def exhaustive_scale_matrix() -> np.ndarray:
+    """65536 rows x one block: row s has bf16 scale bits s and codes covering
+    all 16 values in both nibble positions."""
+    W = np.zeros((65536, 20), np.uint8)
+    lo = np.arange(16, dtype=np.uint8)
+    W[:, :16] = lo | ((15 - lo) << 4)
+    s = np.arange(65536, dtype=np.uint32)
+    W[:, 16] = s & 0xFF
+    W[:, 17] = s >> 8
+    return W
+
+
+def test_dequant_exhaustive_vs_torch(orc):
+    W = exhaustive_scale_matrix()
+    got = orc.dequant_q4(W, 65536, 32)
+    q = orc.unpack_q4(W, 65536, 32).astype(np.float32)
+    s = _bits_to_f32(np.arange(65536, dtype=np.uint32) << 16)[:, None]
+    prod32 = torch.from_numpy(q).mul(torch.from_numpy(np.ascontiguousarray(np.broadcast_to(s, q.shape))))
+    want = prod32.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    # NaN products (NaN scales, 0 * inf) become 0x7FC0 as in bf16.cpp:9-11;
+    # torch keeps NaN payloads, so they are compared separately.
+    nan = torch.isnan(prod32).numpy()
+    assert np.array_equal(got[~nan], want[~nan])
+    assert np.all(got[nan] == 0x7FC0) and nan.sum() == 254 * 32 + 2 * 2
+    # Powers of two (|q| in {0,1,2,4,8}) are exact products for finite scales.
+    fin = np.isfinite(s[:, 0])
+    exact = np.isin(np.abs(q), [0, 1, 2, 4, 8])
+    with np.errstate(over="ignore", invalid="ignore"):
+        prod = (q * s)[fin][exact[fin]]
+    deq = _bits_to_f32(got.astype(np.uint32) << 16)[fin][exact[fin]]
+    nz = np.abs(prod) >= np.float32(2.0 ** -126)  # keep normal results
+    assert np.array_equal(deq[nz], prod[nz])
+
+
+def test_dequant_numpy_restatement(orc):
+    W = orc.synth_q4(64, 256, 11)
+    a = orc.dequant_q4(W, 64, 256)
+    b = (q4_numpy.dequantize_combined(W).view(np.uint32) >> 16).astype(np.uint16)
+    assert np.array_equal(a, b)
+
+
+# ---- gemv (tools/ref/gemv_q.py:73-80) --------------------------------------------
+
+@pytest.mark.parametrize("N,K,seed", [(64, 256, 1), (256, 256, 42), (333, 1152, 5), (128, 4096, 9)])
+def test_gemv_fp64_bound_and_numpy(orc, N, K, seed):
+    W = orc.synth_q4(N, K, seed)
+    x = orc.synth_normal(K, seed + 1)
+    y = orc.gemv_q(W, x, N, K)
+    y64 = orc.gemv_q_f64(W, x, N, K)
+    w = _bits_to_f32(orc.dequant_q4(W, N, K).astype(np.uint32) << 16).astype(np.float64)
+    absdot = np.abs(w) @ np.abs(x.astype(np.float64))
+    u = 2.0 ** -24
+    gamma = K * u / (1 - K * u)
+    assert np.all(np.abs(y - y64) <= gamma * absdot + 1e-30)
+    # numpy with the reference's own expression (BLAS order) agrees to fp32 rounding.
+    yn = q4_numpy.gemv_q_combined(W, x)
+    assert np.all(np.abs(y - yn) <= 2 * gamma * absdot + 1e-30)
+
+
+def test_gemv_one_hot_selects_column(orc):
+    N, K = 48, 320
+    W = orc.synth_q4(N, K, 3)
+    deq = _bits_to_f32(orc.dequant_q4(W, N, K).astype(np.uint32) << 16)
+    for k in (0, 1, 31, 32, 100, K - 1):
+        x = np.zeros(K, np.float32)
+        x[k] = 1.0
+        assert np.array_equal(orc.gemv_q(W, x, N, K), deq[:, k])
+
+
+def test_gemv_zero_scale_rows(orc):
+    N, K = 8, 128
+    W = orc.synth_q4(N, K, 4)
+    W.reshape(N, K // 32, 20)[3, :, 16:18] = 0  # row 3: all scales +0
+    y = orc.gemv_q(W, orc.synth_normal(K, 5), N, K)
+    assert y[3] == 0.0 and np.all(y[[0, 1, 2, 4]] != 0.0)
+
+
+def test_dropped_dequant_rounding_fails_tolerance(orc):
+    """A plausible mistake -- factoring the scale out (s * sum q x, no bf16
+    rounding of the dequantized weight, as runtime/cpp/src/generator.cpp:80-101
+    does) -- is caught by the 1e-4 max-relative tolerance."""
+    N, K = 3840, 3840
+    W = orc.synth_q4(N, K, 21)
+    x = orc.synth_normal(K, 22)
+    y = orc.gemv_q(W, x, N, K)
+    q = orc.unpack_q4(W, N, K).astype(np.float64)
+    s = _bits_to_f32(orc.scales_q4(W, N, K).astype(np.uint32) << 16).astype(np.float64)
+    y_bad = ((q.reshape(N, K // 32, 32) * x.reshape(1, K // 32, 32)).sum(-1) * s).sum(-1)
+    err = np.max(np.abs(y_bad - y)) / np.max(np.abs(y))
+    assert err > 1e-4, err
+
+
+# ---- gemm (runtime/py/model.py:1049-1111; runtime/cpp/src/main.cpp:98-108) ----------
+
+def test_gemm_rows_equal_gemv(orc):
+    M, N, K = 5, 96, 512
+    W = orc.synth_q4(N, K, 12)
+    X = orc.synth_normal(M * K, 13).reshape(M, K)
+    Y = orc.gemm_q(W, X, M, N, K)
+    for m in range(M):
+        assert np.array_equal(Y[m], orc.gemv_q(W, X[m], N, K))
+
+
+# ---- GLU and FFN (runtime/py/model.py:797-806, :853-860) ---------------------------
+
+def _numpy_gelu_mul(g, u):
+    # runtime/py/model.py:802-803, evaluated by numpy.
+    gelu_out = 0.5 * g * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (g + 0.044715 * (g ** 3))))
+    return q4_numpy.bf16_rne(np.asarray(gelu_out * u).astype(np.float32))
+
+
+def _numpy_silu_mul(g, u):
+    return q4_numpy.bf16_rne((g * (1.0 / (1.0 + np.exp(-g)))) * u)
+
+
+def test_glu_matches_numpy_expression(orc):
+    rng = np.random.default_rng(3)
+    g = q4_numpy.bf16_rne(rng.standard_normal(1 << 18).astype(np.float32) * 4)
+    u = q4_numpy.bf16_rne(rng.standard_normal(1 << 18).astype(np.float32) * 4)
+    a = orc.glu(g, u, 0)
+    want = _numpy_gelu_mul(g, u)
+    diff = a != want
+    # numpy's float32 g**3 is a SIMD routine, not correctly rounded: at most a
+    # rare one-ulp flip of the bf16 result.
+    assert diff.mean() < 1e-3, diff.mean()
+    # Where 1 + tanh cancels (g < -4.5) the libm tanh ulps are amplified, but
+    # the values are below 1e-9 * |u|; elsewhere the flips are single bf16 ulps.
+    deep = g[diff] < -4.5
+    ulp = np.abs(a[diff].view(np.int32) - want[diff].view(np.int32))
+    assert np.all(ulp[~deep] == 1 << 16)
+    assert np.all(np.abs(a[diff][deep] - want[diff][deep]) <= 1e-9 * np.abs(u[diff][deep]))
+    a_s = orc.glu(g, u, 1)
+    ws = _numpy_silu_mul(g, u)
+    ds = a_s != ws
+    assert ds.mean() < 1e-3
+    deep = g[ds] < -20
+    assert np.all(np.abs(a_s[ds].view(np.int32) - ws[ds].view(np.int32))[~deep] == 1 << 16)
+
+
+def test_glu_vs_longdouble_tanh(orc):
+    rng = np.random.default_rng(4)
+    g = q4_numpy.bf16_rne(rng.standard_normal(1 << 16).astype(np.float32) * 3)
+    u = np.ones_like(g)
+    a = orc.glu(g, u, 0)
+    gl = g.astype(np.longdouble)
+    inner = (g + np.float32(0.044715) * ((g * g) * g)).astype(np.longdouble)
+    c = np.sqrt(np.longdouble(2) / np.pi)
+    ref = np.longdouble(0.5) * gl * (1 + np.tanh(c * inner))
+    want = q4_numpy.bf16_rne(ref.astype(np.float64).astype(np.float32))
+    ok = g > -4.5  # outside the 1 + tanh cancellation, where float64 itself loses digits
+    assert (a[ok] != want[ok]).mean() < 1e-3
+    assert np.all(np.abs(a[~ok] - want[~ok]) <= 1e-9)
+
+
+def test_glu_special_cases(orc):
+    g = np.array([0.0, 0.0, 3.0, -3.0, 40.0, -40.0, 1.0], np.float32)
+    u = np.array([5.0, 0.0, 0.0, 0.0, 2.0, 2.0, 1.0], np.float32)
+    a = orc.glu(g, u, 0)
+    assert a[0] == 0 and a[1] == 0 and a[2] == 0 and a[3] == 0
+    assert a[4] == 80.0 and a[5] == 0.0  # gelu(g) -> g, -> 0
+    # gelu_tanh(1) = 0.841192 -> bf16 0.83984375
+    assert a[6] == np.float32(0.83984375)
+
+
+@pytest.mark.parametrize("H,I,act,seed", [(256, 512, "gelu", 31), (384, 1152, "silu", 31),
+                                         (1152, 6912, "gelu", 31), (1152, 6912, "gelu", 100)])
+def test_ffn_vs_numpy(orc, H, I, act, seed):
+    """The oracle against numpy evaluating the reference's expressions, with
+    the flip-aware criterion of tests/parity.py (numpy's BLAS adds in another
+    order, so a few bf16 rounding points may legitimately differ)."""
+    Wg, Wu, Wd = orc.synth_q4(I, H, seed), orc.synth_q4(I, H, seed + 1), orc.synth_q4(H, I, seed + 2)
+    x = orc.synth_normal(H, seed + 3)
+    yn, an = q4_numpy.ffn_cpu(Wg, Wu, Wd, x, act, return_act=True)
+    st = parity.ffn_check(orc, Wg, Wu, Wd, x, H, I, 0 if act == "gelu" else 1, yn, an)
+    assert st["down_max_rel"] < 1e-5
+
+
+def test_ffn_fp64_accumulation_within_flip_bound(orc):
+    """fp64 accumulation of gate/up is another legitimate order."""
+    H, I = 1152, 6912
+    Wg, Wu, Wd = orc.synth_q4(I, H, 31), orc.synth_q4(I, H, 32), orc.synth_q4(H, I, 33)
+    x = orc.synth_normal(H, 34)
+    g = orc.bf16_round(orc.gemv_q_f64(Wg, x, I, H).astype(np.float32))
+    u = orc.bf16_round(orc.gemv_q_f64(Wu, x, I, H).astype(np.float32))
+    a = orc.glu(g, u, 0)
+    y = orc.gemv_q(Wd, a, H, I)
+    st = parity.ffn_check(orc, Wg, Wu, Wd, x, H, I, 0, y, a)
+    assert st["flips"] >= 1  # this seed does flip, so the flip path is exercised
+
+
+def test_ffn_batch_rows_equal(orc):
+    H, I, M = 128, 256, 3
+    Wg, Wu, Wd = orc.synth_q4(I, H, 41), orc.synth_q4(I, H, 42), orc.synth_q4(H, I, 43)
+    X = orc.synth_normal(M * H, 44).reshape(M, H)
+    Y = orc.ffn(Wg, Wu, Wd, X, H, I, 0)
+    for m in range(M):
+        assert np.array_equal(Y[m], orc.ffn(Wg, Wu, Wd, X[m], H, I, 0))
+
+
+# ---- quantizer (tools/convert/gemv_q_convert.py:5-85) ----------------------------
+
+def test_quantize_hand_block(orc):
+    w = np.zeros((1, 64), np.float32)
+    # block 0: max 7 -> scale 1.0; halves tie to even (np.round).
+    w[0, :10] = [7, -7, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.49, -6.51]
+    # block 1 all zero -> scale 1.0, codes 0.
+    W = orc.quantize_q4_0(w)
+    q = orc.unpack_q4(W, 1, 64)[0]
+    assert q[:10].tolist() == [7, -7, 0, 2, 2, 0, -2, -2, 3, -7]
+    assert np.all(q[10:] == 0)
+    s = orc.scales_q4(W, 1, 64)[0]
+    assert s.tolist() == [0x3F80, 0x3F80]
+    assert W[0, 18:20].tolist() == [0, 0] and W[0, 38:40].tolist() == [0, 0]
+
+
+def test_quantize_round_trip_bound(orc):
+    rng = np.random.default_rng(42)
+    w = rng.uniform(-1.0, 1.0, size=(256, 256)).astype(np.float32)
+    W = orc.quantize_q4_0(w)
+    deq = _bits_to_f32(orc.dequant_q4(W, 256, 256).astype(np.uint32) << 16)
+    s = np.repeat(np.abs(w).reshape(256, 8, 32).max(-1) / np.float32(7), 32, axis=1)
+    # half a step, plus half a bf16 ulp (2^-8 relative) on the scale and on the product
+    assert np.all(np.abs(deq - w) <= s * (0.5 + 2 * 7 * 2.0 ** -8))
+
+
+# ---- synthetic inputs -------------------------------------------------------------
+
+def test_synth_deterministic_and_distributed(orc):
+    a = orc.synth_q4(64, 512, 123)
+    assert np.array_equal(a, orc.synth_q4(64, 512, 123))
+    assert not np.array_equal(a, orc.synth_q4(64, 512, 124))
+    blk = a.reshape(64, 16, 20)
+    assert np.all(blk[:, :, 18:] == 0)
+    s = _bits_to_f32(orc.scales_q4(a, 64, 512).astype(np.uint32) << 16)
+    assert s.min() >= 0.00099 and s.max() <= 0.0201
+    q = orc.unpack_q4(a, 64, 512)
+    hist = np.bincount(q.ravel() + 8, minlength=16)
+    assert hist.min() > 0.8 * q.size / 16
+    x = orc.synth_normal(1 << 16, 5)
+    assert abs(x.mean()) < 0.02 and abs(x.std() - 1) < 0.02
+    # Counter-based SplitMix64 (Steele et al.): first outputs for seed 0.
+    assert orc.lib().orc_splitmix64_at(0, 0) == 0xE220A8397B1DCDAF
