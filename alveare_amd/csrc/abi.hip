@@ -38,6 +38,12 @@ int get_workspace(hipStream_t s, size_t partial_floats, size_t counters, Workspa
     std::lock_guard<std::mutex> lk(g_ws_mu);
     Workspace& w = g_ws[{dev, s}];
     if (w.partial_floats < partial_floats || w.counter_count < counters) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (int rc = hip_check(hipStreamIsCapturing(s, &cs), "hipStreamIsCapturing")) return rc;
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(ALV_ERR_ARG,
+                        "split-K workspace of this stream must grow, which cannot happen during graph "
+                        "capture: run the same call once on this stream before capturing");
         // The old buffers may still be read by queued kernels.
         if (int rc = hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize")) return rc;
         size_t pf = w.partial_floats > partial_floats ? w.partial_floats : partial_floats;

@@ -6,8 +6,8 @@
 //      waves against the same activation operands; the epilogue rounds both to
 //      bf16, applies the GLU and rounds the activation to bf16 -- the
 //      reference CPU path's three rounding points (runtime/py/model.py:798-803).
-//      The activation (M x I fp32, bf16-valued) stays in the handle's scratch,
-//      which is L2/MALL-resident at these sizes.
+//      The activation (M x I bf16) stays in the handle's scratch, which is
+//      L2/MALL-resident at these sizes.
 //   2. down = Wd * a, with a single bf16 term per activation value (it is
 //      bf16 by construction), summed entirely on the device -- the reference
 //      sums per-core partials on the host (runtime/cpp/src/npu.cpp:360-377).
@@ -23,9 +23,9 @@ struct alv_ffn {
     uint32_t magic;
     int device;
     int H, I, act;
-    uint8_t* w;  // one allocation: gate | up | down, combined layout
+    uint8_t* w;  // one allocation: gate | up | down, tiled layout (q4_device.h)
     size_t gate_bytes, down_bytes;
-    float* a;  // activation scratch, a_cap floats
+    uint16_t* a;  // activation scratch (bf16 bit patterns), a_cap elements
     size_t a_cap;
     int a_rows;  // tokens held in `a` after the last call
 };
@@ -48,12 +48,14 @@ extern "C" int alv_ffn_register(const uint8_t* Wg, const uint8_t* Wu, const uint
     if (!out) return fail(ALV_ERR_ARG, "null output handle pointer");
     *out = nullptr;
     if (!Wg || !Wu || !Wd) return fail(ALV_ERR_ARG, "null weight pointer");
+    if ((reinterpret_cast<uintptr_t>(Wg) | reinterpret_cast<uintptr_t>(Wu) | reinterpret_cast<uintptr_t>(Wd)) % 4)
+        return fail(ALV_ERR_ALIGN, "FFN weights need 4-byte alignment");
     if (H < 32 || I < 32 || H % 32 || I % 32)
         return fail(ALV_ERR_ARG, "bad FFN shape H=%d I=%d (both must be positive multiples of 32)", H, I);
     if (act != ALV_ACT_GELU_TANH && act != ALV_ACT_SILU) return fail(ALV_ERR_ARG, "bad activation id %d", act);
-    const size_t gate_bytes = (size_t)I * (H / 32) * kBlockBytes;
-    const size_t down_bytes = (size_t)H * (I / 32) * kBlockBytes;
-    if (gate_bytes >= 0xFFFFFF00ull || down_bytes >= 0xFFFFFF00ull)
+    const size_t gate_bytes = tile_bytes(I, H);
+    const size_t down_bytes = tile_bytes(H, I);
+    if (gate_bytes >= 0xFFFFE000ull || down_bytes >= 0xFFFFE000ull)
         return fail(ALV_ERR_RANGE, "FFN matrices exceed the 4 GiB buffer range");
     hipStream_t s = (hipStream_t)stream;
     alv_ffn* h = new alv_ffn{};
@@ -65,11 +67,11 @@ extern "C" int alv_ffn_register(const uint8_t* Wg, const uint8_t* Wu, const uint
     h->down_bytes = down_bytes;
     int rc = hip_check(hipGetDevice(&h->device), "hipGetDevice");
     if (!rc) rc = hip_check(hipMalloc(&h->w, 2 * gate_bytes + down_bytes), "hipMalloc(FFN weights)");
-    if (!rc) rc = hip_check(hipMemcpyAsync(h->w, Wg, gate_bytes, hipMemcpyDeviceToDevice, s), "copy gate");
-    if (!rc) rc = hip_check(hipMemcpyAsync(h->w + gate_bytes, Wu, gate_bytes, hipMemcpyDeviceToDevice, s), "copy up");
-    if (!rc) rc = hip_check(hipMemcpyAsync(h->w + 2 * gate_bytes, Wd, down_bytes, hipMemcpyDeviceToDevice, s), "copy down");
+    if (!rc) rc = launch_tile(Wg, h->w, I, H, s);
+    if (!rc) rc = launch_tile(Wu, h->w + gate_bytes, I, H, s);
+    if (!rc) rc = launch_tile(Wd, h->w + 2 * gate_bytes, H, I, s);
     h->a_cap = (size_t)I * kGemvMaxM;
-    if (!rc) rc = hip_check(hipMalloc(&h->a, h->a_cap * sizeof(float)), "hipMalloc(FFN activation)");
+    if (!rc) rc = hip_check(hipMalloc(&h->a, h->a_cap * sizeof(uint16_t)), "hipMalloc(FFN activation)");
     if (!rc) rc = hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
     if (rc) {
         if (h->w) (void)hipFree(h->w);
@@ -107,7 +109,7 @@ extern "C" int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int l
         (void)hipFree(w->a);
         w->a = nullptr;
         w->a_cap = 0;
-        if (int rc = hip_check(hipMalloc(&w->a, need * sizeof(float)), "hipMalloc(FFN activation)")) return rc;
+        if (int rc = hip_check(hipMalloc(&w->a, need * sizeof(uint16_t)), "hipMalloc(FFN activation)")) return rc;
         w->a_cap = need;
     }
     const uint8_t* wg = w->w;
@@ -120,17 +122,18 @@ extern "C" int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int l
         up.W1 = wu;
         up.X = X + (size_t)m0 * ldx;
         up.ldx = ldx;
-        up.Y = w->a;
+        up.Yb = w->a;
         up.ldy = w->I;
         up.M = mc;
         up.N = w->I;
         up.K = w->H;
         up.parts = 3;
         up.glu = true;
+        up.tiled = true;
         up.act = w->act;
         GemvLaunch down;
         down.W0 = wd;
-        down.X = w->a;
+        down.Xb = w->a;
         down.ldx = w->I;
         down.Y = Y + (size_t)m0 * ldy;
         down.ldy = ldy;
@@ -138,6 +141,7 @@ extern "C" int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int l
         down.N = w->H;
         down.K = w->I;
         down.parts = 1;
+        down.tiled = true;
         const bool tiled = mc >= kTiledMinM;
         if (int rc = tiled ? launch_gemm_tiled(up, s) : launch_gemv(up, s)) return rc;
         if (int rc = tiled ? launch_gemm_tiled(down, s) : launch_gemv(down, s)) return rc;
@@ -146,13 +150,23 @@ extern "C" int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int l
     return ALV_OK;
 }
 
+namespace {
+
+__global__ void __launch_bounds__(256) bf16_to_f32_kernel(const uint16_t* in, float* out, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = bf16_bits_to_f32(in[i]);
+}
+
+}  // namespace
+
 extern "C" int alv_ffn_activation(alv_ffn_t w, float* out, int M, void* stream) {
     if (int rc = check_handle(w)) return rc;
     if (!out) return fail(ALV_ERR_ARG, "null output pointer");
     if (M < 1 || M > w->a_rows) return fail(ALV_ERR_ARG, "M=%d outside the %d tokens of the last call", M, w->a_rows);
-    return hip_check(hipMemcpyAsync(out, w->a, (size_t)M * w->I * sizeof(float), hipMemcpyDeviceToDevice,
-                                    (hipStream_t)stream),
-                     "copy activation");
+    const int64_t n = (int64_t)M * w->I;
+    const int grid = (int)std::min<int64_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, w->a, out, n);
+    return hip_check(hipGetLastError(), "bf16_to_f32_kernel launch");
 }
 
 extern "C" void alv_ffn_release(alv_ffn_t w) {

@@ -30,10 +30,14 @@ constexpr int LDR = 40;  // padded LDS row length in bf16
 struct TiledArgs {
     const uint8_t* W0;
     const uint8_t* W1;
-    const float* X;
-    float* Y;
+    const float* X;       // fp32 activations, or
+    const uint16_t* Xb;   // bf16 activations (bit patterns)
+    float* Y;             // fp32 output, or
+    uint16_t* Yb;         // bf16 output (bit patterns)
     uint32_t wbytes;
     int ldx, ldy, M, N, K, parts, act;
+    bool tiled;   // weights in the tiled layout (q4_device.h) instead of the combined one
+    TileGeom tg;
 };
 
 template <bool GLU>
@@ -72,13 +76,25 @@ __global__ void __launch_bounds__(256) gemm_tiled_kernel(TiledArgs a) {
     for (int kb = 0; kb < nb; ++kb) {
         // ---- stage the weight tile (dequantized) --------------------------
         {
-            const uint32_t off = wrow_ok ? (uint32_t)wrow * rs + (uint32_t)kb * kBlockBytes : a.wbytes;
+            uint32_t o0, o1, os;  // nibble dwords 2*half, 2*half+1 and the scale dword
+            if (!wrow_ok) {
+                o0 = o1 = os = a.wbytes;
+            } else if (a.tiled) {
+                o0 = tiled_offset(a.tg, wrow, kb, 8 * half);
+                o1 = tiled_offset(a.tg, wrow, kb, 8 * half + 4);
+                os = tiled_offset(a.tg, wrow, kb, 16);
+            } else {
+                const uint32_t off = (uint32_t)wrow * rs + (uint32_t)kb * kBlockBytes;
+                o0 = off + 8 * half;
+                o1 = off + 8 * half + 4;
+                os = off + 16;
+            }
 #pragma unroll
             for (int n = 0; n < NT; ++n) {
                 const __amdgpu_buffer_rsrc_t r = n ? r1 : r0;
-                const uint32_t d0 = buf_load4(r, off + 8 * half);
-                const uint32_t d1 = buf_load4(r, off + 8 * half + 4);
-                const uint32_t ds = buf_load4(r, off + 16);
+                const uint32_t d0 = buf_load4(r, o0);
+                const uint32_t d1 = buf_load4(r, o1);
+                const uint32_t ds = buf_load4(r, os);
                 const Scale sc = make_scale(bf16_bits_to_f32(ds & 0xFFFFu));
                 __bf16* dst = &ws[n][srow * LDR + 16 * half];
                 *reinterpret_cast<bf16x8*>(dst) = dequant8(d0, sc);
@@ -93,7 +109,8 @@ __global__ void __launch_bounds__(256) gemm_tiled_kernel(TiledArgs a) {
             for (int h = 0; h < 2; ++h) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float v = xrow_ok ? a.X[(size_t)xrow * a.ldx + kb * 32 + 16 * half + 8 * h + e] : 0.0f;
+                    const size_t xi = (size_t)xrow * a.ldx + kb * 32 + 16 * half + 8 * h + e;
+                    const float v = !xrow_ok ? 0.0f : a.Xb ? bf16_bits_to_f32(a.Xb[xi]) : a.X[xi];
                     if (a.parts == 3) {
                         const Split3 s = split3(v);
                         p[0][h][e] = s.p0;
@@ -153,21 +170,26 @@ __global__ void __launch_bounds__(256) gemm_tiled_kernel(TiledArgs a) {
                 float out = acc[0][i][jj][r];
                 if constexpr (GLU)
                     out = bf16_round(glu_act(bf16_round(acc[0][i][jj][r]), bf16_round(acc[NT - 1][i][jj][r]), a.act));
-                a.Y[(size_t)m * a.ldy + n] = out;
+                if (a.Yb)
+                    a.Yb[(size_t)m * a.ldy + n] = __builtin_bit_cast(uint16_t, (__bf16)out);
+                else
+                    a.Y[(size_t)m * a.ldy + n] = out;
             }
 }
 
 }  // namespace
 
 int launch_gemm_tiled(const GemvLaunch& L, hipStream_t s) {
-    const uint64_t wbytes = (uint64_t)L.N * (uint64_t)(L.K / 32) * kBlockBytes;
+    const uint64_t wbytes = L.tiled ? tile_bytes(L.N, L.K) : (uint64_t)L.N * (uint64_t)(L.K / 32) * kBlockBytes;
     if (wbytes >= 0xFFFFFF00ull) return fail(ALV_ERR_RANGE, "weight matrix of %llu bytes exceeds the 4 GiB buffer range", (unsigned long long)wbytes);
     if (L.parts != 1 && L.parts != 3) return fail(ALV_ERR_ARG, "parts must be 1 or 3");
     TiledArgs a{};
     a.W0 = L.W0;
     a.W1 = L.W1;
     a.X = L.X;
+    a.Xb = L.Xb;
     a.Y = L.Y;
+    a.Yb = L.Yb;
     a.wbytes = (uint32_t)wbytes;
     a.ldx = L.ldx;
     a.ldy = L.ldy;
@@ -176,6 +198,8 @@ int launch_gemm_tiled(const GemvLaunch& L, hipStream_t s) {
     a.K = L.K;
     a.parts = L.parts;
     a.act = L.act;
+    a.tiled = L.tiled;
+    a.tg = tile_geom(L.K);
     const dim3 grid((L.N + TN - 1) / TN, (L.M + TM - 1) / TM);
     if (L.glu)
         hipLaunchKernelGGL(gemm_tiled_kernel<true>, grid, dim3(256), 0, s, a);

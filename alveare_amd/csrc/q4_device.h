@@ -21,6 +21,43 @@ typedef uint32_t u32x4 __attribute__((__vector_size__(4 * sizeof(uint32_t))));
 constexpr int kBlockBytes = 20;  // bytes per 32 weights
 constexpr int kBlockK = 32;      // weights per block
 
+// Tiled Q4 layout (the kernels' registration-time layout; a byte permutation
+// of the combined layout, zero-padded to whole 128-column runs):
+//   row tile rt = 16 rows; super-step ss = 16 blocks (512 columns); within a
+//   row tile, lane (g, j), g = 0..3, j = 0..15, owns the 80-byte run of row
+//   16 rt + j covering blocks 16 ss + 4 g .. 16 ss + 4 g + 3.
+//   Tile (rt, ss) stores those runs as 5 planes of 16-byte pieces: piece i of
+//   lane l = 16 g + j sits at tile + i * 256 * ng + 16 * l, where ng = 4 for
+//   every super-step but the last, which holds ng = ceil(blocks left / 4)
+//   lanes of g. Tiles follow each other in (rt, ss) order, so row tile rt
+//   starts at rt * tile_row_bytes(K) and super-step ss at + ss * 5120.
+//   Blocks past K and rows past N are zero (they dequantize to zero).
+// A wave reading piece i of every lane reads 1 KiB of contiguous memory.
+struct TileGeom {
+    int nb;           // blocks per row
+    int nss;          // super-steps per row
+    int ng_last;      // lanes of g in the last super-step
+    uint32_t rtb;     // bytes per row tile
+};
+
+// Byte offset in the tiled layout of byte x (0..19) of block kb of row `row`.
+__host__ __device__ inline uint32_t tiled_offset(const TileGeom& t, int row, int kb, int x) {
+    const int ss = kb >> 4, g = (kb >> 2) & 3, bl = kb & 3;
+    const int rb = 20 * bl + x;
+    const uint32_t ng = ss == t.nss - 1 ? (uint32_t)t.ng_last : 4u;
+    return (uint32_t)(row >> 4) * t.rtb + (uint32_t)ss * 5120u + (uint32_t)(rb >> 4) * 256u * ng +
+           (uint32_t)(g * 16 + (row & 15)) * 16u + (uint32_t)(rb & 15);
+}
+
+__host__ __device__ inline TileGeom tile_geom(int K) {
+    TileGeom t;
+    t.nb = K / kBlockK;
+    t.nss = (t.nb + 15) / 16;
+    t.ng_last = (t.nb - 16 * (t.nss - 1) + 3) / 4;
+    t.rtb = (uint32_t)(t.nss - 1) * 5120u + 1280u * (uint32_t)t.ng_last;
+    return t;
+}
+
 // Buffer resource over [base, base + bytes): loads past the end return 0
 // instead of faulting. dword3 = 0x00020000 is the raw 32-bit data format on gfx9.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -30,6 +67,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 
 __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+// Streaming (nontemporal) variant for weights, which are read exactly once:
+// aux bit 1 sets the `nt` cache policy on gfx950.
+__device__ __forceinline__ u32x4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
+}
+
+// Loads addressed by a per-lane voffset that stays fixed and a wave-uniform
+// soffset (an SGPR) that carries the moving part of the address, so a
+// prefetch never writes a VGPR that an in-flight load may still target.
+template <bool NT>
+__device__ __forceinline__ u32x4 buf_load16_so(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, NT ? 2 : 0);
 }
 
 __device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
@@ -55,6 +106,12 @@ struct Scale {
 
 __device__ __forceinline__ Scale make_scale(float s) { return Scale{s * 512.0f, s * -8.0f}; }
 
+// The block scale from the dword holding block bytes 16..19: the bf16 at bytes
+// 16-17 moved to the high half (one byte permute; bytes 18-19 are dropped).
+__device__ __forceinline__ float scale_of(uint32_t d) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_perm(d, d, 0x01000C0Cu));
+}
+
 // Eight weights from one dword of nibbles, exactly as the reference dequantizes
 // them: w = bf16_RNE(f32(q) * f32(s)) (tools/ref/gemv_q.py:19-37).
 //
@@ -66,12 +123,14 @@ __device__ __forceinline__ Scale make_scale(float s) { return Scale{s * 512.0f, 
 // representable value, i.e. exact. The bf16 conversion then rounds to nearest
 // even like the reference's astype(bfloat16).
 //
+// The nibble split is one v_bitop3 per half: (d & 0x0F0F0F0F) ^ 0x08080808
+// (truth table 0x6A for S0 & S1 ^ S2).
+//
 // Output element e is column 8*t + e of the block when d is the block's
 // dword t (natural column order).
 __device__ __forceinline__ bf16x8 dequant8(uint32_t d, Scale s) {
-    d ^= 0x88888888u;
-    const uint32_t lo = d & 0x0F0F0F0Fu;         // columns 0, 2, 4, 6
-    const uint32_t hi = (d >> 4) & 0x0F0F0F0Fu;  // columns 1, 3, 5, 7
+    const uint32_t lo = __builtin_amdgcn_bitop3_b32(d, 0x0F0F0F0Fu, 0x08080808u, 0x6A);       // cols 0,2,4,6
+    const uint32_t hi = __builtin_amdgcn_bitop3_b32(d >> 4, 0x0F0F0F0Fu, 0x08080808u, 0x6A);  // cols 1,3,5,7
     const f32x2 l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
     const f32x2 l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
     const f32x2 h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);

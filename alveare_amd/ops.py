@@ -140,6 +140,68 @@ def dequant_q4(W: torch.Tensor, N: int, K: int) -> torch.Tensor:
     return out
 
 
+def q4_tile(W: torch.Tensor, N: int, K: int) -> torch.Tensor:
+    """The kernels' tiled layout of W (uint8, alv_q4_tiled_bytes(N, K) bytes);
+    parity entry point for the registration-time repack."""
+    _check_shape(N, K)
+    _need_gpu(W)
+    _weight(W, N, K)
+    out = torch.empty(int(lib().alv_q4_tiled_bytes(N, K)), dtype=torch.uint8, device=W.device)
+    with torch.cuda.device(W.device):
+        check(lib().alv_q4_tile(W.data_ptr(), out.data_ptr(), N, K, _stream(W)), "alv_q4_tile")
+    return out
+
+
+class Q4Weight:
+    """A registered projection (runtime/cpp/src/npu.cpp:241-253
+    create_gemv_weight): a device copy in the kernels' tiled layout, used by
+    ``gemv``/``__call__``. Released on ``close()`` or garbage collection."""
+
+    def __init__(self, W: torch.Tensor, N: int, K: int):
+        _check_shape(N, K)
+        dev = _need_gpu(W)
+        _weight(W, N, K)
+        self.N, self.K, self.device = N, K, dev
+        self._h = ctypes.c_void_p()
+        with torch.cuda.device(dev):
+            check(lib().alv_weight_register(W.data_ptr(), N, K, ctypes.byref(self._h), _stream(W)),
+                  "alv_weight_register")
+        self.shape = (N, K // 32 * 20)
+
+    @property
+    def handle(self) -> int:
+        if not self._h:
+            raise ValueError("weights were released")
+        return self._h.value
+
+    def close(self) -> None:
+        if self._h:
+            with torch.cuda.device(self.device):
+                lib().alv_weight_release(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __call__(self, X: torch.Tensor, Y: torch.Tensor | None = None, M: int = 1) -> torch.Tensor:
+        """Y[M, N] = X[M, K] @ dequant(W)^T (M = 1: the decode GEMV)."""
+        x = _act_in(X, M * self.K, "X")
+        if x.device != self.device:
+            raise ValueError(f"X on {x.device}, weights on {self.device}")
+        if Y is None:
+            Y = torch.empty((M, self.N) if M > 1 else (self.N,), dtype=torch.float32, device=self.device)
+        _need_gpu(Y)
+        y = _out_buffer(Y, M * self.N, "Y")
+        with torch.cuda.device(self.device):
+            check(lib().alv_gemv(self.handle, x.data_ptr(), y.data_ptr(), M, self.K, self.N, _stream(x)),
+                  "alv_gemv")
+        _store(Y, y, M * self.N)
+        return Y
+
+
 class FfnWeights:
     """A registered FFN layer (the device-resident analogue of the reference's
     fused FFN weight, runtime/cpp/src/npu.cpp:255-267). Owns a device copy of
@@ -242,5 +304,5 @@ gemv_q_npu = gemv_q
 gemm_q_npu = gemm_q
 ffn_fused_npu = ffn_fused
 
-__all__ = ["gemv_q", "gemm_q", "ffn_fused", "dequant_q4", "FfnWeights", "pack_ffn_fused_weights",
-           "gemv_q_npu", "gemm_q_npu", "ffn_fused_npu"]
+__all__ = ["gemv_q", "gemm_q", "ffn_fused", "dequant_q4", "q4_tile", "Q4Weight", "FfnWeights",
+           "pack_ffn_fused_weights", "gemv_q_npu", "gemm_q_npu", "ffn_fused_npu"]

@@ -25,6 +25,11 @@
  *    dense fp32, row-major, with the given leading dimensions (in elements).
  *  - Calls on different streams may run concurrently; calls that share an FFN
  *    handle must be serialised on one stream (the handle owns its scratch).
+ *  - Shapes whose K is split across workgroups use a split-K workspace the
+ *    library keeps per (device, stream). It grows on first need (that growth
+ *    synchronises the device), so a stream that will be captured into a HIP
+ *    graph must run the same calls once before capture; growth during capture
+ *    fails with ALV_ERR_ARG.
  */
 #ifndef ALVEARE_Q4_H
 #define ALVEARE_Q4_H
@@ -46,6 +51,7 @@ extern "C" {
 #define ALV_ACT_SILU 1        /* Llama: x*sigmoid(x) (runtime/py/model.py:856) */
 
 typedef struct alv_ffn* alv_ffn_t;
+typedef struct alv_weight* alv_weight_t;
 
 /* Message for the calling thread's last failed call ("" if none). */
 const char* alv_last_error(void);
@@ -72,6 +78,42 @@ int alv_gemv_q(const uint8_t* W, const float* x, float* y, int N, int K, void* s
  */
 int alv_gemm_q(const uint8_t* W, const float* X, float* Y, int M, int N, int K,
                int ldx, int ldy, void* stream);
+
+/*
+ * Register one projection: W is (N, K/32*20) in the combined Q4 layout on the
+ * device. The handle keeps its own device copy in the kernels' tiled layout
+ * (the caller may free W after the call returns). Synchronises `stream`.
+ * Replaces NpuRegistry::create_gemv_weight (runtime/cpp/include/alveare/npu.h:68-69,
+ * runtime/cpp/src/npu.cpp:241-253); the reference also registers weights once
+ * and keeps them device-resident (runtime/py/model.py:31-35 ResidentWeight).
+ */
+int alv_weight_register(const uint8_t* W, int N, int K, alv_weight_t* out, void* stream);
+
+/* Shape of a registered projection (either output pointer may be NULL). */
+int alv_weight_shape(alv_weight_t w, int* N, int* K);
+
+/*
+ * Y[M,N] = X[M,K] @ dequant(W)^T with W registered; rows of X/Y at leading
+ * dimensions ldx/ldy. M = 1 is the decode GEMV, small M the streaming kernel,
+ * M >= 32 the MFMA tiled kernel.
+ * Replaces NpuRegistry::run_gemv / run_gemm (runtime/cpp/include/alveare/npu.h:78-87,
+ * runtime/cpp/src/npu.cpp:269-310).
+ */
+int alv_gemv(alv_weight_t w, const float* X, float* Y, int M, int ldx, int ldy, void* stream);
+
+/* Free a handle from alv_weight_register (NULL is a no-op). Synchronises the
+ * device before freeing. */
+void alv_weight_release(alv_weight_t w);
+
+/*
+ * The kernels' tiled layout of a combined-layout matrix: byte size (0 for a
+ * bad shape) and the repack itself into `out` (device, alv_q4_tiled_bytes
+ * bytes). Test / parity entry points: registration performs this repack, the
+ * counterpart of the reference's registration-time repack of FFN weights
+ * (runtime/cpp/src/weights.cpp:94-190). W and out need 4-byte alignment.
+ */
+uint64_t alv_q4_tiled_bytes(int N, int K);
+int alv_q4_tile(const uint8_t* W, uint8_t* out, int N, int K, void* stream);
 
 /*
  * Register one FFN layer: Wg, Wu are (I, H/32*20), Wd is (H, I/32*20), all in

@@ -116,3 +116,29 @@ def ffn_check(orc, Wg, Wu, Wd, x, H, I, act, y_test, a_test=None, tol=TOL):
     bad = np.abs(y_test - y_ref) > tol * scale + budget
     assert not bad.any(), f"{bad.sum()} outputs outside tolerance + flip budget"
     return {"max_rel": max_rel(y_test, y_ref), "flips": int(len(flips)), "down_max_rel": e1}
+
+
+def tile_layout_np(W: np.ndarray, N: int, K: int) -> np.ndarray:
+    """The kernels' tiled layout, restated from its definition: per 16-row tile
+    and 512-column super-step, lane (g, j) owns the 80-byte run of row j over
+    blocks 4g..4g+3; its five 16-byte pieces go to planes i at
+    tile + i*256*ng + 16*(16g + j). ng = 4 except the last super-step
+    (ceil(blocks left / 4)); bytes past the row or past N are zero."""
+    nb = K // 32
+    nss = (nb + 15) // 16
+    ngl = (nb - 16 * (nss - 1) + 3) // 4
+    rtb = (nss - 1) * 5120 + 1280 * ngl
+    RT = (N + 15) // 16
+    rs = nb * 20
+    Wp = np.zeros((RT * 16, nss * 320), np.uint8)
+    Wp[:N, :rs] = np.asarray(W).reshape(N, rs)
+    out = np.zeros(RT * rtb, np.uint8)
+    for rt in range(RT):
+        for ss in range(nss):
+            ng = 4 if ss < nss - 1 else ngl
+            for g in range(ng):
+                runs = Wp[rt * 16:(rt + 1) * 16, (ss * 16 + g * 4) * 20:(ss * 16 + g * 4) * 20 + 80]
+                for i in range(5):
+                    dst = rt * rtb + ss * 5120 + i * 256 * ng + g * 256
+                    out[dst:dst + 256] = runs[:, 16 * i:16 * i + 16].reshape(-1)
+    return out

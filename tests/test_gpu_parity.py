@@ -140,6 +140,70 @@ def test_gemv_bf16_activation_and_padded_buffers(orc, dev):
         aa.gemv_q(big_w[:100], xb, y, N=N, K=K)
 
 
+# ---- tiled layout and registered weights ---------------------------------------------
+
+@pytest.mark.parametrize("N,K", [(37, 1152), (16, 96), (300, 3840), (5, 32), (64, 15360)])
+def test_tile_layout_matches_definition(orc, dev, N, K):
+    import alveare_amd as aa
+
+    _say(f"tile N={N} K={K}")
+    W = orc.synth_q4(N, K, 4000 + N + K)
+    got = aa.q4_tile(to_dev(W, dev), N, K).cpu().numpy()
+    assert np.array_equal(got, parity.tile_layout_np(W, N, K))
+
+
+REG_SHAPES = [(2048, 2048), (8192, 3840), (3840, 4096), (3840, 15360), (333, 1152), (17, 96), (1, 32),
+              (100, 480)]
+
+
+@pytest.mark.parametrize("N,K", REG_SHAPES)
+def test_registered_gemv_parity(orc, dev, N, K):
+    import alveare_amd as aa
+
+    _say(f"registered gemv N={N} K={K}")
+    W = orc.synth_q4(N, K, orc.seed_for(1, 2) + N + K)
+    x = orc.synth_normal(K, orc.seed_for(1, 3) + K)
+    w = aa.Q4Weight(to_dev(W, dev), N, K)
+    y = w(to_dev(x, dev))
+    torch.cuda.synchronize()
+    err = parity.gemv_check(orc, W, x, y.cpu().numpy(), N, K)
+    _say(f"  max-rel {err:.2e}")
+    w.close()
+
+
+@pytest.mark.parametrize("M,N,K", [(3, 3840, 3840), (16, 1000, 1152), (40, 700, 3840)])
+def test_registered_gemm_parity(orc, dev, M, N, K):
+    import alveare_amd as aa
+
+    _say(f"registered gemm M={M} N={N} K={K}")
+    W = orc.synth_q4(N, K, 5000 + M)
+    X = orc.synth_normal(M * K, 6000 + M).reshape(M, K)
+    w = aa.Q4Weight(to_dev(W, dev), N, K)
+    Y = w(to_dev(X, dev), M=M).cpu().numpy()
+    err = parity.max_rel(Y, orc.gemm_q(W, X, M, N, K))
+    _say(f"  max-rel {err:.2e}")
+    assert err <= parity.TOL
+    for m in sorted({0, M - 1}):
+        parity.gemv_check(orc, W, X[m], Y[m], N, K)
+    w.close()
+
+
+def test_registered_matches_raw_path(orc, dev):
+    """Same products through the combined-layout entry point and the registered
+    one: equal up to summation order (both within the fp32 bound)."""
+    import alveare_amd as aa
+
+    N, K = 3840, 4096
+    W = orc.synth_q4(N, K, 77)
+    x = orc.synth_normal(K, 78)
+    Wd = to_dev(W, dev)
+    y_raw = run_gemv(W, x, N, K, dev)
+    w = aa.Q4Weight(Wd, N, K)
+    y_reg = w(to_dev(x, dev)).cpu().numpy()
+    assert parity.max_rel(y_reg, y_raw) <= 1e-6
+    w.close()
+
+
 # ---- GEMM (small M: streaming kernel; M >= 32: MFMA tiled kernel) -------------------
 
 @pytest.mark.parametrize("M,N,K,bf16x", [(2, 3840, 3840, False), (4, 15360, 3840, False),
