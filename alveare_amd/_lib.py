@@ -42,7 +42,16 @@ SIGNATURES: dict[str, tuple] = {
     "alv_weight_release": (None, [_vp]),
     "alv_q4_tiled_bytes": (ctypes.c_uint64, [_i, _i]),
     "alv_q4_tile": (_i, [_vp, _vp, _i, _i, _vp]),
+    "alv_chain_run": (_i, [_vp, _i, _i, _vp]),
+    "alv_check_async": (_i, [_vp]),
 }
+
+
+class ChainOp(ctypes.Structure):
+    """alv_chain_op (include/alveare_q4.h)."""
+
+    _fields_ = [("weight", ctypes.c_void_p), ("ffn", ctypes.c_void_p), ("x", ctypes.c_void_p),
+                ("y", ctypes.c_void_p), ("dep", ctypes.c_int)]
 
 
 class LibraryNotBuilt(RuntimeError):

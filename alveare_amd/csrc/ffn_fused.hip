@@ -19,29 +19,55 @@
 #include "q4_device.h"
 #include "q4_host.h"
 
-struct alv_ffn {
-    uint32_t magic;
-    int device;
-    int H, I, act;
-    uint8_t* w;  // one allocation: gate | up | down, tiled layout (q4_device.h)
-    size_t gate_bytes, down_bytes;
-    uint16_t* a;  // activation scratch (bf16 bit patterns), a_cap elements
-    size_t a_cap;
-    int a_rows;  // tokens held in `a` after the last call
-};
 
 namespace {
 
-constexpr uint32_t kFfnMagic = 0xA1FEED42u;
-
 int check_handle(alv_ffn_t w) {
-    if (!w || w->magic != kFfnMagic) return alv::fail(ALV_ERR_HANDLE, "invalid FFN handle");
+    if (!w || w->magic != alv::kFfnMagic) return alv::fail(ALV_ERR_HANDLE, "invalid FFN handle");
     return ALV_OK;
 }
 
 }  // namespace
 
 using namespace alv;
+
+namespace alv {
+
+// The two ops of one FFN call: gate/up with the GLU epilogue into the handle's
+// bf16 activation, then down from it (op 1 waits for op 0 inside a chain).
+void ffn_ops(alv_ffn_t w, const float* X, int ldx, float* Y, int ldy, int M, ExecOp (&op)[2]) {
+    ExecOp& up = op[0];
+    up = ExecOp{};
+    up.W0 = w->w;
+    up.W1 = w->w + w->gate_bytes;
+    up.X = X;
+    up.ldx = ldx;
+    up.Yb = w->a;
+    up.ldy = w->I;
+    up.M = M;
+    up.N = w->I;
+    up.K = w->H;
+    up.parts = 3;
+    up.glu = true;
+    up.tiled = true;
+    up.act = w->act;
+    up.dep = -1;
+    ExecOp& down = op[1];
+    down = ExecOp{};
+    down.W0 = w->w + 2 * w->gate_bytes;
+    down.Xb = w->a;
+    down.ldx = w->I;
+    down.Y = Y;
+    down.ldy = ldy;
+    down.M = M;
+    down.N = w->H;
+    down.K = w->I;
+    down.parts = 1;
+    down.tiled = true;
+    down.dep = 0;
+}
+
+}  // namespace alv
 
 extern "C" int alv_ffn_register(const uint8_t* Wg, const uint8_t* Wu, const uint8_t* Wd, int H, int I,
                                 int act, alv_ffn_t* out, void* stream) {
@@ -112,39 +138,16 @@ extern "C" int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int l
         if (int rc = hip_check(hipMalloc(&w->a, need * sizeof(uint16_t)), "hipMalloc(FFN activation)")) return rc;
         w->a_cap = need;
     }
-    const uint8_t* wg = w->w;
-    const uint8_t* wu = w->w + w->gate_bytes;
-    const uint8_t* wd = w->w + 2 * w->gate_bytes;
     for (int m0 = 0; m0 < M; m0 += chunk) {
         const int mc = std::min(chunk, M - m0);
-        GemvLaunch up;
-        up.W0 = wg;
-        up.W1 = wu;
-        up.X = X + (size_t)m0 * ldx;
-        up.ldx = ldx;
-        up.Yb = w->a;
-        up.ldy = w->I;
-        up.M = mc;
-        up.N = w->I;
-        up.K = w->H;
-        up.parts = 3;
-        up.glu = true;
-        up.tiled = true;
-        up.act = w->act;
-        GemvLaunch down;
-        down.W0 = wd;
-        down.Xb = w->a;
-        down.ldx = w->I;
-        down.Y = Y + (size_t)m0 * ldy;
-        down.ldy = ldy;
-        down.M = mc;
-        down.N = w->H;
-        down.K = w->I;
-        down.parts = 1;
-        down.tiled = true;
-        const bool tiled = mc >= kTiledMinM;
-        if (int rc = tiled ? launch_gemm_tiled(up, s) : launch_gemv(up, s)) return rc;
-        if (int rc = tiled ? launch_gemm_tiled(down, s) : launch_gemv(down, s)) return rc;
+        ExecOp op[2];
+        ffn_ops(w, X + (size_t)m0 * ldx, ldx, Y + (size_t)m0 * ldy, ldy, mc, op);
+        if (mc >= kTiledMinM) {
+            if (int rc = launch_gemm_tiled(op[0], s)) return rc;
+            if (int rc = launch_gemm_tiled(op[1], s)) return rc;
+        } else {
+            if (int rc = exec_chain(op, 2, true, s)) return rc;
+        }
         w->a_rows = mc;
     }
     return ALV_OK;

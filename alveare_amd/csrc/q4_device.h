@@ -83,6 +83,12 @@ __device__ __forceinline__ u32x4 buf_load16_so(__amdgpu_buffer_rsrc_t r, uint32_
     return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, NT ? 2 : 0);
 }
 
+// Load that bypasses this XCD's L2 (sc1): sees data another workgroup wrote
+// through with agent-scope stores.
+__device__ __forceinline__ u32x4 buf_load16_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16);
+}
+
 __device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }

@@ -15,17 +15,15 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 void clear_error();
 int hip_check(hipError_t e, const char* what);
 
-// Per-(device, stream) scratch for cross-workgroup split-K reduction:
-// fp32 partial sums and per-row-tile arrival counters. Counters are zero when
-// a kernel starts and every kernel leaves them zero. Grown on demand (the
-// growth synchronises the device); steady-state calls allocate nothing.
+// Per-(device, stream) synchronisation words of the op-chain executor. They
+// are zero when a launch starts and every launch leaves them zero. Allocated
+// on first use on a stream (which synchronises the device); steady-state calls
+// allocate nothing.
 struct Workspace {
-    float* partial = nullptr;
-    size_t partial_floats = 0;
     uint32_t* counters = nullptr;
     size_t counter_count = 0;
 };
-int get_workspace(hipStream_t s, size_t partial_floats, size_t counters, Workspace* out);
+int get_workspace(hipStream_t s, size_t counters, Workspace* out);
 
 // One launch of the streaming kernel (stream_q.hip):
 //   out[m, n] = sum_k X[m, k] * dequant(W0)[n, k]            (glu == false)
@@ -51,6 +49,59 @@ struct GemvLaunch {
 };
 int launch_gemv(const GemvLaunch& L, hipStream_t s);
 
+// ---- op chains (stream_q.hip) --------------------------------------------------
+// One op of a chain: a GemvLaunch plus the index of the earlier op whose output
+// is its input (-1: the input is ready when the launch starts).
+struct ExecOp : GemvLaunch {
+    int dep = -1;
+};
+constexpr int kMaxOps = 16;
+// Synchronisation words of a chain launch. Same-address device atomics
+// serialise (~8 ns each), so counters that many workgroups bump are spread over
+// kSyncSlots words: per op, "row tiles done" (workgroup b counts into slot
+// b % kSyncSlots); a two-level exit count (workgroup b into slot
+// b % kSyncSlots, the slot that completes into one word); and a sticky error
+// flag set when a wait timed out.
+constexpr int kSyncSlots = 64;
+constexpr int kSyncExit1 = kMaxOps * kSyncSlots;
+constexpr int kSyncExit2 = kSyncExit1 + kSyncSlots;
+constexpr int kSyncError = kSyncExit2 + 1;
+constexpr int kSyncWords = kSyncError + 1;
+
+// Device-side descriptor of one op (kernel argument; every field is
+// wave-uniform). A row tile is 16 output rows; its work is U = nss * (glu ? 2 : 1)
+// units (one super-step of 512 k of one matrix), split over the `gw` waves of
+// one of the r wave groups of a workgroup.
+struct OpDesc {
+    const uint8_t* W0;
+    const uint8_t* W1;
+    const void* X;
+    float* Y;
+    uint16_t* Yb;
+    uint32_t wbytes, xbytes, rstride;
+    int ldx, ldy, M, N, K, parts, R, nb, nss, ng_last, RT, U, r, act;
+    int glu, xb, dep, signal;
+    // Work split, precomputed: waves per group = 1 << gw_shift, steps per
+    // round numax, row-tile stride of a group wstride = grid * r; workgroup b
+    // runs nr_full + (b < nr_rem) rounds.
+    int gw_shift, numax, wstride, nr_full, nr_rem;
+};
+struct ExecArgs {
+    OpDesc op[kMaxOps];
+    int nops;
+    uint32_t xs_bytes;  // LDS bytes of the staged activations (the reduction scratch follows)
+    uint32_t spin_limit;
+    int last_wait;  // the last op that waits for an earlier one (-1: none, no counters are used)
+    int flags;
+    uint32_t* sync;
+};
+// Run ops[0..nops) on `s`: one launch per group of tokens that fits the LDS
+// (every op of a launch sees the same tokens). tiled: weights in the tiled
+// layout (required for chains longer than one op).
+int exec_chain(const ExecOp* ops, int nops, bool tiled, hipStream_t s);
+// Report (and clear) a timed-out chain wait on stream `s` (synchronises it).
+int check_async(hipStream_t s);
+
 // Repack W (combined layout, N x K) into the tiled layout at `out`
 // (tile_bytes(N, K) bytes), on `s` (tile_q.hip).
 int launch_tile(const uint8_t* W, uint8_t* out, int N, int K, hipStream_t s);
@@ -66,4 +117,33 @@ int launch_gemm_tiled(const GemvLaunch& L, hipStream_t s);
 // M at and above which alv_gemm_q uses the tiled kernel.
 constexpr int kTiledMinM = 32;
 
+// The two ops of one FFN call on handle w (ffn_fused.hip).
+void ffn_ops(alv_ffn_t w, const float* X, int ldx, float* Y, int ldy, int M, ExecOp (&op)[2]);
+
 }  // namespace alv
+
+namespace alv {
+constexpr uint32_t kWeightMagic = 0xA1E4B0B5u;  // live alv_weight
+constexpr uint32_t kFfnMagic = 0xA1FEED42u;     // live alv_ffn
+}  // namespace alv
+
+// Registered projection (tile_q.hip).
+struct alv_weight {
+    uint32_t magic;
+    int device;
+    int N, K;
+    uint8_t* w;  // tiled copy, tile_bytes(N, K)
+};
+
+// Registered FFN layer (ffn_fused.hip).
+struct alv_ffn {
+    uint32_t magic;
+    int device;
+    int H, I, act;
+    uint8_t* w;  // one allocation: gate | up | down, tiled layout (q4_device.h)
+    size_t gate_bytes, down_bytes;
+    uint16_t* a;  // activation scratch (bf16 bit patterns), a_cap elements
+    size_t a_cap;
+    int a_rows;  // tokens held in `a` after the last call
+};
+

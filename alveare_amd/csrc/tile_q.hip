@@ -60,16 +60,9 @@ int launch_tile(const uint8_t* W, uint8_t* out, int N, int K, hipStream_t s) {
 
 using namespace alv;
 
-struct alv_weight {
-    uint32_t magic;
-    int device;
-    int N, K;
-    uint8_t* w;  // tiled copy, tile_bytes(N, K)
-};
 
 namespace {
 
-constexpr uint32_t kWeightMagic = 0xA1E4B0B5u;
 
 int check_weight(alv_weight_t w) {
     if (!w || w->magic != kWeightMagic) return fail(ALV_ERR_HANDLE, "invalid weight handle");

@@ -299,10 +299,47 @@ def ffn_fused(W_fused: FfnWeights, X: torch.Tensor, Y_partial: torch.Tensor, *, 
     return W_fused(X, Y_partial, M)
 
 
+def chain_run(ops, M: int = 1) -> None:
+    """Run a chain of registered ops on the device with as few launches as
+    possible (alv_chain_run). ``ops`` is a list of ``(handle, x, y, dep)`` with
+    handle a Q4Weight or FfnWeights, x/y float32 GPU tensors (x may be a view
+    into an earlier op's y) and dep the index of the op whose output x reads
+    (or -1). Equivalent to calling the ops one after another."""
+    from ._lib import ChainOp
+
+    arr = (ChainOp * len(ops))()
+    dev = None
+    for i, (h, x, y, dep) in enumerate(ops):
+        if not isinstance(h, (Q4Weight, FfnWeights)):
+            raise TypeError("chain ops take Q4Weight or FfnWeights handles")
+        d = _need_gpu(x, y)
+        dev = dev or d
+        if x.dtype != torch.float32 or y.dtype != torch.float32 or not x.is_contiguous() or not y.is_contiguous():
+            raise TypeError("chain activations are contiguous float32 tensors")
+        K, N = (h.K, h.N) if isinstance(h, Q4Weight) else (h.H, h.H)
+        _too_small("x", x.numel(), M * K)
+        _too_small("y", y.numel(), M * N)
+        arr[i].weight = h.handle if isinstance(h, Q4Weight) else None
+        arr[i].ffn = h.handle if isinstance(h, FfnWeights) else None
+        arr[i].x = x.data_ptr()
+        arr[i].y = y.data_ptr()
+        arr[i].dep = int(dep)
+    with torch.cuda.device(dev):
+        check(lib().alv_chain_run(arr, len(ops), M, torch.cuda.current_stream(dev).cuda_stream), "alv_chain_run")
+
+
+def check_async(device=None) -> None:
+    """Synchronise the current stream and raise if a chained op timed out."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    with torch.cuda.device(dev):
+        check(lib().alv_check_async(torch.cuda.current_stream(dev).cuda_stream), "alv_check_async")
+
+
 # The reference's names for the same ops.
 gemv_q_npu = gemv_q
 gemm_q_npu = gemm_q
 ffn_fused_npu = ffn_fused
 
-__all__ = ["gemv_q", "gemm_q", "ffn_fused", "dequant_q4", "q4_tile", "Q4Weight", "FfnWeights",
+__all__ = ["gemv_q", "gemm_q", "ffn_fused", "dequant_q4", "q4_tile", "Q4Weight", "FfnWeights", "chain_run",
+           "check_async",
            "pack_ffn_fused_weights", "gemv_q_npu", "gemm_q_npu", "ffn_fused_npu"]

@@ -157,6 +157,40 @@ int alv_ffn_shape(alv_ffn_t w, int* H, int* I, int* act);
 void alv_ffn_release(alv_ffn_t w);
 
 /*
+ * One op of a chain: a registered projection (y = W x) or a registered FFN
+ * layer (y = ffn(x)); exactly one of `weight` and `ffn` is set. x and y are
+ * device fp32 buffers of M rows (leading dimension K, resp. N or H). dep is
+ * the index of an earlier op whose output this op reads (its x points into
+ * that op's y), or -1 when x is ready before the call.
+ */
+typedef struct {
+    alv_weight_t weight;
+    alv_ffn_t ffn;
+    const float* x;
+    float* y;
+    int dep;
+} alv_chain_op;
+
+/*
+ * Run ops[0..n) in order on `stream` with as few launches as possible: each op
+ * waits on the device for its dep instead of the host waiting between calls.
+ * Results equal running the ops one after another through alv_gemv /
+ * alv_ffn_fused. M is the token count (1..16). An FFN handle may appear more
+ * than once (each use starts a new launch).
+ * Device-side counterpart of the reference's per-layer dispatch, which calls
+ * NpuRegistry::run_gemv / run_ffn_fused one after another
+ * (runtime/cpp/src/model.cpp:265-420, runtime/py/model.py:632-818).
+ */
+int alv_chain_run(const alv_chain_op* ops, int n, int M, void* stream);
+
+/*
+ * Synchronise `stream` and report whether a chained op on it timed out
+ * waiting for its input (ALV_ERR_HIP; only possible when other work kept
+ * part of the chain's grid from being resident). Clears the condition.
+ */
+int alv_check_async(void* stream);
+
+/*
  * out[N,K] = bf16 bit patterns of dequant(W). Test / parity entry point: the
  * reference materialises this matrix in dequantize_combined
  * (tools/ref/gemv_q.py:39-62).

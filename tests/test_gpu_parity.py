@@ -204,6 +204,81 @@ def test_registered_matches_raw_path(orc, dev):
     w.close()
 
 
+# ---- op chains ------------------------------------------------------------------------
+
+def test_chain_matches_separate_calls(orc, dev):
+    """A layer-shaped chain -- projection, projection reading a slice of the
+    first output, FFN reading the second, projection reading the FFN output --
+    run as one device-side chain equals the same ops called one by one, and
+    each op passes the oracle on the inputs it actually saw."""
+    import alveare_amd as aa
+
+    H, I, NQ, KO = 1152, 3456, 2048, 1024
+    Wq, Wo = orc.synth_q4(NQ, H, 61), orc.synth_q4(H, KO, 62)
+    Wg, Wu, Wd = orc.synth_q4(I, H, 63), orc.synth_q4(I, H, 64), orc.synth_q4(H, I, 65)
+    Wn = orc.synth_q4(NQ, H, 66)
+    q = aa.Q4Weight(to_dev(Wq, dev), NQ, H)
+    o = aa.Q4Weight(to_dev(Wo, dev), H, KO)
+    f = aa.pack_ffn_fused_weights(to_dev(Wg, dev), to_dev(Wu, dev), to_dev(Wd, dev), H, I)
+    n = aa.Q4Weight(to_dev(Wn, dev), NQ, H)
+    x = to_dev(orc.synth_normal(H, 67), dev)
+    yq, yo, yf, yn = (torch.empty(NQ, device=dev), torch.empty(H, device=dev), torch.empty(H, device=dev),
+                      torch.empty(NQ, device=dev))
+    for rep in range(3):  # repeated launches reuse (and must reset) the chain counters
+        yq.fill_(float("nan")); yo.fill_(float("nan")); yf.fill_(float("nan")); yn.fill_(float("nan"))
+        aa.chain_run([(q, x, yq, -1), (o, yq[:KO], yo, 0), (f, yo, yf, 1), (n, yf, yn, 2)])
+        aa.check_async()
+        got = [t.cpu().numpy().copy() for t in (yq, yo, yf, yn)]
+        if rep == 0:
+            first = got
+        else:
+            for a_, b_ in zip(first, got):
+                assert np.array_equal(a_, b_), "chain results differ between launches"
+    sq = q(x).cpu().numpy()
+    so = o(torch.from_numpy(got[0][:KO]).to(dev)).cpu().numpy()
+    sf = f(torch.from_numpy(got[1]).to(dev)).cpu().numpy()
+    sn = n(torch.from_numpy(got[2]).to(dev)).cpu().numpy()
+    # Projections differ from separate calls by summation order only; the FFN
+    # may also flip a bf16 rounding of its activation (checked below).
+    for a_, b_, tol in zip(got, (sq, so, sf, sn), (1e-6, 1e-6, 2e-3, 1e-6)):
+        assert parity.max_rel(a_, b_) <= tol
+    parity.gemv_check(orc, Wq, x.cpu().numpy(), got[0], NQ, H)
+    parity.gemv_check(orc, Wo, got[0][:KO], got[1], H, KO)
+    parity.ffn_check(orc, Wg, Wu, Wd, got[1], H, I, 0, got[2], f.last_activation(1).cpu().numpy()[0])
+    parity.gemv_check(orc, Wn, got[2], got[3], NQ, H)
+    for h in (q, o, n, f):
+        h.close()
+
+
+def test_chain_long_and_repeated_ffn(orc, dev):
+    """A chain longer than one launch holds (the split is transparent) and an
+    FFN handle used twice in a row."""
+    import alveare_amd as aa
+
+    H, I = 512, 1024
+    Wg, Wu, Wd = orc.synth_q4(I, H, 71), orc.synth_q4(I, H, 72), orc.synth_q4(H, I, 73)
+    f = aa.pack_ffn_fused_weights(to_dev(Wg, dev), to_dev(Wu, dev), to_dev(Wd, dev), H, I)
+    p = aa.Q4Weight(to_dev(orc.synth_q4(H, H, 74), dev), H, H)
+    x = to_dev(orc.bf16_round(orc.synth_normal(H, 75)) * 0.25, dev)
+    steps = 12
+    ys = [torch.empty(H, device=dev) for _ in range(steps)]
+    ops = []
+    for i in range(steps):
+        h = f if i % 3 else p
+        ops.append((h, x if i == 0 else ys[i - 1], ys[i], i - 1))
+    aa.chain_run(ops)
+    aa.check_async()
+    cur = x
+    for i in range(steps):
+        h = f if i % 3 else p
+        ref = h(cur).clone()
+        tol = 2e-3 if h is f else 1e-6  # the FFN may flip a bf16 rounding of its activation
+        assert parity.max_rel(ys[i].cpu().numpy(), ref.cpu().numpy()) <= tol, f"step {i}"
+        cur = ys[i]
+    f.close()
+    p.close()
+
+
 # ---- GEMM (small M: streaming kernel; M >= 32: MFMA tiled kernel) -------------------
 
 @pytest.mark.parametrize("M,N,K,bf16x", [(2, 3840, 3840, False), (4, 15360, 3840, False),
