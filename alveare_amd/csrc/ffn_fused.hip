@@ -1,7 +1,7 @@
 // Fused FFN (gate/up projection, GLU activation, down projection) on gfx950:
 // alv_ffn_register / alv_ffn_fused / alv_ffn_shape / alv_ffn_release.
 //
-// Decode (M <= 16): two launches of the streaming kernel (gemv_q.hip).
+// Decode (M <= 16): two launches of the one-shot kernel (oneshot_q.hip).
 //   1. gate and up rows of one 16-row I-tile are streamed together by the same
 //      waves against the same activation operands; the epilogue rounds both to
 //      bf16, applies the GLU and rounds the activation to bf16 -- the
@@ -146,7 +146,8 @@ extern "C" int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int l
             if (int rc = launch_gemm_tiled(op[0], s)) return rc;
             if (int rc = launch_gemm_tiled(op[1], s)) return rc;
         } else {
-            if (int rc = exec_chain(op, 2, true, s)) return rc;
+            if (int rc = launch_gemv(op[0], s)) return rc;
+            if (int rc = launch_gemv(op[1], s)) return rc;
         }
         w->a_rows = mc;
     }

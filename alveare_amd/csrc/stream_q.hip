@@ -1,9 +1,8 @@
 // Streaming Q4 executor for decode and small-M batches (gfx950): one launch
 // runs a chain of up to kMaxOps matrix-vector ops -- a projection, or a
 // gate/up pair with the GLU activation -- where an op may take its input from
-// an earlier op of the chain. alv_gemv_q / alv_gemv / alv_gemm_q (M <= 16) are
-// one-op chains, alv_ffn_fused (M <= 16) is the two-op chain gate/up -> down,
-// alv_chain_run runs longer chains.
+// an earlier op of the chain: the kernel behind alv_chain_run, and behind
+// single ops whose shape the one-shot kernel (oneshot_q.hip) does not cover.
 //
 // The kernel is HBM-bound by design: weights are read once with 16-byte
 // loads, dequantized in registers (q4_device.h::dequant8, ~2.4 VALU ops per
@@ -693,13 +692,6 @@ int exec_chain(const ExecOp* ops, int nops, bool tiled, hipStream_t s) {
     for (int m0 = 0; m0 < M; m0 += mc)
         if (int rc = launch_chunk(ops, nops, tiled, m0, std::min(mc, M - m0), s)) return rc;
     return ALV_OK;
-}
-
-int launch_gemv(const GemvLaunch& L, hipStream_t s) {
-    ExecOp op;
-    static_cast<GemvLaunch&>(op) = L;
-    op.dep = -1;
-    return exec_chain(&op, 1, L.tiled, s);
 }
 
 int check_async(hipStream_t s) {

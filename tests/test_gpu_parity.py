@@ -206,13 +206,22 @@ def test_registered_matches_raw_path(orc, dev):
 
 # ---- op chains ------------------------------------------------------------------------
 
-def test_chain_matches_separate_calls(orc, dev):
+@pytest.fixture(params=["separate", "fused"])
+def chain_mode(request, monkeypatch):
+    """alv_chain_run in its default mode (one launch per op) and with the fused
+    op-chain executor (ALV_CHAIN_FUSED=1, read on every call)."""
+    monkeypatch.setenv("ALV_CHAIN_FUSED", "1" if request.param == "fused" else "0")
+    return request.param
+
+
+def test_chain_matches_separate_calls(orc, dev, chain_mode):
     """A layer-shaped chain -- projection, projection reading a slice of the
     first output, FFN reading the second, projection reading the FFN output --
-    run as one device-side chain equals the same ops called one by one, and
-    each op passes the oracle on the inputs it actually saw."""
+    run as one chain equals the same ops called one by one, and each op passes
+    the oracle on the inputs it actually saw."""
     import alveare_amd as aa
 
+    _say(f"chain layer mode={chain_mode}")
     H, I, NQ, KO = 1152, 3456, 2048, 1024
     Wq, Wo = orc.synth_q4(NQ, H, 61), orc.synth_q4(H, KO, 62)
     Wg, Wu, Wd = orc.synth_q4(I, H, 63), orc.synth_q4(I, H, 64), orc.synth_q4(H, I, 65)
@@ -250,11 +259,12 @@ def test_chain_matches_separate_calls(orc, dev):
         h.close()
 
 
-def test_chain_long_and_repeated_ffn(orc, dev):
+def test_chain_long_and_repeated_ffn(orc, dev, chain_mode):
     """A chain longer than one launch holds (the split is transparent) and an
     FFN handle used twice in a row."""
     import alveare_amd as aa
 
+    _say(f"chain long mode={chain_mode}")
     H, I = 512, 1024
     Wg, Wu, Wd = orc.synth_q4(I, H, 71), orc.synth_q4(I, H, 72), orc.synth_q4(H, I, 73)
     f = aa.pack_ffn_fused_weights(to_dev(Wg, dev), to_dev(Wu, dev), to_dev(Wd, dev), H, I)
