@@ -154,6 +154,21 @@ extern "C" int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int l
     return ALV_OK;
 }
 
+extern "C" int alv_ffn_gate_up(alv_ffn_t w, const float* X, int M, int ldx, void* stream) {
+    if (int rc = check_handle(w)) return rc;
+    if (!X) return fail(ALV_ERR_ARG, "null activation pointer");
+    if (M < 1 || M > kGemvMaxM || ldx < w->H) return fail(ALV_ERR_ARG, "bad M=%d ldx=%d for H=%d (1 <= M <= %d)", M, ldx, w->H, kGemvMaxM);
+    if (reinterpret_cast<uintptr_t>(X) % 4) return fail(ALV_ERR_ALIGN, "X needs 4-byte alignment");
+    int dev = -1;
+    if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    if (dev != w->device) return fail(ALV_ERR_HANDLE, "FFN handle belongs to device %d, current device is %d", w->device, dev);
+    ExecOp op[2];
+    ffn_ops(w, X, ldx, nullptr, w->H, M, op);
+    if (int rc = launch_gemv(op[0], (hipStream_t)stream)) return rc;
+    w->a_rows = M;
+    return ALV_OK;
+}
+
 namespace {
 
 __global__ void __launch_bounds__(256) bf16_to_f32_kernel(const uint16_t* in, float* out, int64_t n) {

@@ -253,6 +253,15 @@ class FfnWeights:
                   "alv_ffn_activation")
         return out
 
+    def gate_up(self, X: torch.Tensor, M: int = 1) -> None:
+        """Only the gate/up launch of a call (alv_ffn_gate_up): the activation
+        lands in the handle's scratch (``last_activation``)."""
+        x = _act_in(X, M * self.H, "X")
+        if x.device != self.device:
+            raise ValueError(f"X on {x.device}, weights on {self.device}")
+        with torch.cuda.device(self.device):
+            check(lib().alv_ffn_gate_up(self.handle, x.data_ptr(), M, self.H, _stream(x)), "alv_ffn_gate_up")
+
     def __call__(self, X: torch.Tensor, Y: torch.Tensor | None = None, M: int = 1) -> torch.Tensor:
         x = _act_in(X, M * self.H, "X")
         if x.device != self.device:

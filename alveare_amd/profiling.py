@@ -1,0 +1,106 @@
+"""Summaries of rocprofv3 output for the Q4 decode kernels.
+
+    python -m alveare_amd.profiling stats <dir>
+        per-kernel calls / average / min / max duration from a
+        ``rocprofv3 --kernel-trace --stats`` output directory.
+    python -m alveare_amd.profiling traffic <fetch_dir> <write_dir> <copy_bytes>
+        HBM bytes per dispatch of every q4 kernel from one ``--pmc FETCH_SIZE``
+        and one ``--pmc WRITE_SIZE`` run of ``bench.py --profile-pass``, each
+        scaled by what the counter reads for the pass's calibration copy (an
+        elementwise kernel that reads and writes ``copy_bytes`` bytes).
+
+Both print short text meant for ``profiles/``.
+"""
+from __future__ import annotations
+
+import csv
+import glob
+import os
+import statistics
+import sys
+from collections import defaultdict
+
+Q4_KERNELS = ("q4_oneshot_kernel", "q4_exec_kernel", "gemm_tiled", "tile_kernel")
+CALIBRATION = "MulFunctor"  # the profile pass's copy: torch.mul(src, 1.0, out=dst)
+
+
+def _short(name: str) -> str:
+    name = name.replace("void ", "").replace("(anonymous namespace)::", "").replace("alv::", "")
+    if "(" in name:
+        name = name[: name.index("(")]
+    return name
+
+
+def _find(d: str, suffix: str) -> str:
+    files = sorted(glob.glob(os.path.join(d, "**", f"*{suffix}"), recursive=True))
+    if not files:
+        raise FileNotFoundError(f"no *{suffix} under {d}")
+    return files[0]
+
+
+def stats(d: str) -> str:
+    """Kernel statistics of a --kernel-trace --stats run (all kernels, by time)."""
+    rows = list(csv.DictReader(open(_find(d, "kernel_stats.csv"))))
+    out = ["kernel | calls | avg us | min us | max us | total %"]
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+        out.append(f"{_short(r['Name'])} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.3f} | "
+                   f"{float(r['MinNs']) / 1e3:.3f} | {float(r['MaxNs']) / 1e3:.3f} | {float(r['Percentage']):.2f}")
+    return "\n".join(out)
+
+
+def _counter_means(d: str, counter: str) -> dict:
+    """Mean of `counter` per dispatch, per kernel name."""
+    per = defaultdict(lambda: defaultdict(float))
+    for r in csv.DictReader(open(_find(d, "counter_collection.csv"))):
+        if r["Counter_Name"] != counter:
+            continue
+        # one row per (dispatch, counter): sum the dimension instances of a dispatch
+        per[_short(r["Kernel_Name"])][r.get("Dispatch_Id", r.get("Correlation_Id", ""))] += float(r["Counter_Value"])
+    return {k: statistics.mean(v.values()) for k, v in per.items()}
+
+
+def traffic(fetch_dir: str, write_dir: str, copy_bytes: int) -> str:
+    fetch = _counter_means(fetch_dir, "FETCH_SIZE")
+    write = _counter_means(write_dir, "WRITE_SIZE")
+    cal = [k for k in fetch if CALIBRATION in k]
+    if not cal:
+        raise RuntimeError("calibration copy kernel not found in the FETCH_SIZE run")
+    f_cal = fetch[cal[0]] * 1024.0
+    w_cal = write[[k for k in write if CALIBRATION in k][0]] * 1024.0
+    f_scale, w_scale = copy_bytes / f_cal, copy_bytes / w_cal
+    out = [f"calibration: {cal[0]} reads and writes {copy_bytes} B; FETCH_SIZE reads {f_cal:.0f} B "
+           f"(scale {f_scale:.4f}), WRITE_SIZE reads {w_cal:.0f} B (scale {w_scale:.4f})",
+           "kernel | FETCH_SIZE KiB/dispatch | WRITE_SIZE KiB/dispatch | traffic B/dispatch (scaled)"]
+    for k in sorted(fetch):
+        if not any(q in k for q in Q4_KERNELS):
+            continue
+        t = fetch[k] * 1024.0 * f_scale + write.get(k, 0.0) * 1024.0 * w_scale
+        out.append(f"{k} | {fetch[k]:.1f} | {write.get(k, 0.0):.1f} | {t:.0f}")
+        out.append(f"traffic_bytes_per_launch[{k}]: {t:.0f}")
+    return "\n".join(out)
+
+
+def read_traffic(path: str, kernel: str):
+    """The scaled traffic of `kernel` from a committed traffic summary, or None."""
+    if not os.path.exists(path):
+        return None
+    key = f"traffic_bytes_per_launch[{kernel}]:"
+    for line in open(path):
+        if line.startswith(key):
+            return int(float(line[len(key):]))
+    return None
+
+
+def main(argv) -> int:
+    if len(argv) >= 2 and argv[0] == "stats":
+        print(stats(argv[1]))
+        return 0
+    if len(argv) >= 4 and argv[0] == "traffic":
+        print(traffic(argv[1], argv[2], int(argv[3])))
+        return 0
+    print(__doc__, file=sys.stderr)
+    return 2
+
+
+if __name__ == "__main__":
+    sys.exit(main(sys.argv[1:]))

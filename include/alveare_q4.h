@@ -149,6 +149,15 @@ int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int ldx, int ldy
  */
 int alv_ffn_activation(alv_ffn_t w, float* out, int M, void* stream);
 
+/*
+ * The first of alv_ffn_fused's two launches alone: a = bf16(act(g) * u) for
+ * M <= 16 tokens into the handle's scratch (read it with alv_ffn_activation).
+ * Measurement / parity entry point: it times and checks the gate/up kernel by
+ * itself. The reference runs both phases inside one NPU kernel
+ * (kernels/ffn_fused/ffn_fused.py:28-39).
+ */
+int alv_ffn_gate_up(alv_ffn_t w, const float* X, int M, int ldx, void* stream);
+
 /* Shape of a registered FFN (any output pointer may be NULL). */
 int alv_ffn_shape(alv_ffn_t w, int* H, int* I, int* act);
 

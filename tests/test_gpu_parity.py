@@ -204,6 +204,24 @@ def test_registered_matches_raw_path(orc, dev):
     w.close()
 
 
+def test_ffn_gate_up_alone(orc, dev):
+    """alv_ffn_gate_up leaves the same activation as the full FFN call."""
+    import alveare_amd as aa
+
+    H, I = 1152, 3456
+    Wg, Wu, Wd = orc.synth_q4(I, H, 81), orc.synth_q4(I, H, 82), orc.synth_q4(H, I, 83)
+    f = aa.pack_ffn_fused_weights(to_dev(Wg, dev), to_dev(Wu, dev), to_dev(Wd, dev), H, I)
+    for M in (1, 3):
+        _say(f"ffn gate_up M={M}")
+        x = to_dev(orc.synth_normal(M * H, 84 + M), dev)
+        f(x, M=M)
+        full = f.last_activation(M).cpu().numpy()
+        f.gate_up(x, M=M)
+        alone = f.last_activation(M).cpu().numpy()
+        assert np.array_equal(full, alone)
+    f.close()
+
+
 # ---- op chains ------------------------------------------------------------------------
 
 @pytest.fixture(params=["separate", "fused"])
