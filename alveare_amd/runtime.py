@@ -24,18 +24,27 @@ from pathlib import Path
 import numpy as np
 import torch
 
-from .ops import FfnWeights, gemm_q, gemv_q, pack_ffn_fused_weights
+from .ops import FfnWeights, Q4Weight, gemm_q, gemv_q, pack_ffn_fused_weights
 
 PROJECTIONS = ["attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"]
 
 
 class ResidentWeight:
-    """A device-resident combined-Q4 matrix (model.py:31-35)."""
+    """A device-resident combined-Q4 matrix (model.py:31-35). The first call
+    through Q4Dispatch also registers it (the kernels' tiled copy, kept next to
+    ``tensor``), so resident weights take the registered-weight kernels."""
 
     def __init__(self, tensor: torch.Tensor, shape):
         self.tensor = tensor
         self.shape = tuple(int(s) for s in shape)
         self.size = int(np.prod(self.shape))
+        self.registered: Q4Weight | None = None
+
+    def q4(self) -> Q4Weight:
+        if self.registered is None:
+            N, K = _shape_of(self)
+            self.registered = Q4Weight(self.tensor.view(self.shape), N, K)
+        return self.registered
 
 
 def _to_device_u8(data, device) -> torch.Tensor:
@@ -124,7 +133,10 @@ class Q4Dispatch:
         N, K = _shape_of(rw)
         x = self._x(x_bf16, K)
         y = torch.empty(N, dtype=torch.float32, device=self.device)
-        gemv_q(rw.tensor, x, y, N=N, K=K)
+        if isinstance(W_combined, ResidentWeight):
+            rw.q4()(x.float(), y)
+        else:  # a per-call array, as the reference's non-resident path uploads per call
+            gemv_q(rw.tensor, x, y, N=N, K=K)
         return y.to(torch.bfloat16)
 
     def run_ffn_fused_npu(self, l: int, x_bf16) -> torch.Tensor:
@@ -141,7 +153,10 @@ class Q4Dispatch:
             raise ValueError("run_gemm_npu takes a (B, K) batch")
         B = X.shape[0]
         Y = torch.empty((B, N), dtype=torch.float32, device=self.device)
-        gemm_q(rw.tensor, X, Y, B=B, N=N, K=K)
+        if isinstance(W_combined, ResidentWeight):
+            rw.q4()(X.float(), Y, M=B)
+        else:
+            gemm_q(rw.tensor, X, Y, B=B, N=N, K=K)
         return Y.to(torch.bfloat16)
 
 

@@ -74,6 +74,7 @@ GEMV_SHAPES = [
     (8192, 3840, "syn"),      # fused QKV at the 12B-class shape
     (3840, 15360, "syn"),     # FFN down shape
     (100, 480, "syn"),        # K not a multiple of 128 (partial super-steps)
+    (64, 16896, "syn"),       # K past the one-shot plan (33 super-steps): executor fallback
 ]
 
 
@@ -417,8 +418,10 @@ def test_dispatch_entry_points(orc, dev):
     xp[:1152] = xs
     ref = orc.bf16_round(orc.gemv_q(W, xp, N, K))
     assert parity.max_rel(yg, ref) <= 2 ** -8
-    # resident weights and a batch
+    # resident weights (registered on first use) and a batch
     rw = ResidentWeight(to_dev(W.reshape(-1), dev), W.shape)
+    yr = d.run_gemv_npu(rw, torch.from_numpy(xs).to(torch.bfloat16)).float().cpu().numpy()
+    assert parity.max_rel(yr, ref) <= 2 ** -8
     Xb = orc.bf16_round(orc.synth_normal(5 * K, 57)).reshape(5, K)
     Yb = d.run_gemm_npu(rw, torch.from_numpy(Xb).to(torch.bfloat16)).float().cpu().numpy()
     assert parity.max_rel(Yb, orc.bf16_round(orc.gemm_q(W, Xb, 5, N, K))) <= 2 ** -8
