@@ -28,32 +28,53 @@ int hip_check(hipError_t e, const char* what) {
 }
 
 namespace {
+// Synchronisation words: one block per device holding kWsStreams sets, handed
+// out to streams on first use. The block is allocated (and zeroed) at the
+// first call on the device; a stream's later first use takes a set without
+// allocating, so it may happen during graph capture.
+constexpr int kWsStreams = 64;
 std::mutex g_ws_mu;
-std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+struct DeviceWs {
+    uint32_t* block = nullptr;
+    size_t words = 0;  // per set
+    std::map<hipStream_t, int> slot;
+};
+std::map<int, DeviceWs> g_ws;
 }  // namespace
 
 int get_workspace(hipStream_t s, size_t counters, Workspace* out) {
     int dev = 0;
     if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    Workspace& w = g_ws[{dev, s}];
-    if (w.counter_count < counters) {
+    DeviceWs& w = g_ws[dev];
+    if (!w.block) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         if (int rc = hip_check(hipStreamIsCapturing(s, &cs), "hipStreamIsCapturing")) return rc;
         if (cs != hipStreamCaptureStatusNone)
             return fail(ALV_ERR_ARG,
-                        "the synchronisation words of this stream are allocated on its first call, which "
-                        "cannot happen during graph capture: run one call on this stream before capturing");
-        // The old words may still be used by queued kernels.
-        if (int rc = hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize")) return rc;
-        if (w.counters) (void)hipFree(w.counters);
-        w = Workspace{};
-        if (hipMalloc(&w.counters, counters * sizeof(uint32_t)) != hipSuccess)
-            return fail(ALV_ERR_HIP, "hipMalloc of %zu counters failed", counters);
-        if (int rc = hip_check(hipMemset(w.counters, 0, counters * sizeof(uint32_t)), "hipMemset")) return rc;
-        w.counter_count = counters;
+                        "the synchronisation words of this device are allocated on its first call, which cannot "
+                        "happen during graph capture: run one call on this device before capturing");
+        const size_t words = counters > (size_t)kSyncWords ? counters : (size_t)kSyncWords;
+        if (hipMalloc(&w.block, words * kWsStreams * sizeof(uint32_t)) != hipSuccess) {
+            w.block = nullptr;
+            return fail(ALV_ERR_HIP, "hipMalloc of the synchronisation words failed");
+        }
+        if (int rc = hip_check(hipMemset(w.block, 0, words * kWsStreams * sizeof(uint32_t)), "hipMemset")) return rc;
+        w.words = words;
     }
-    *out = w;
+    if (counters > w.words) return fail(ALV_ERR_ARG, "%zu synchronisation words requested, %zu available", counters, w.words);
+    auto it = w.slot.find(s);
+    int idx;
+    if (it != w.slot.end()) {
+        idx = it->second;
+    } else {
+        if ((int)w.slot.size() >= kWsStreams)
+            return fail(ALV_ERR_ARG, "more than %d streams use chained ops on device %d", kWsStreams, dev);
+        idx = (int)w.slot.size();
+        w.slot[s] = idx;
+    }
+    out->counters = w.block + (size_t)idx * w.words;
+    out->counter_count = w.words;
     return ALV_OK;
 }
 

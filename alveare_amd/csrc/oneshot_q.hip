@@ -17,10 +17,11 @@
 // workgroup staged the activations in MFMA operand order.
 //
 // Work split: a workgroup holds RTW row tiles x KW waves per row tile; wave
-// (rtl, kw) takes SPW consecutive super-steps of row tile rtl, and the KW
-// waves of a row tile cover all of K. Every weight load of a wave is issued
-// when it starts, right after the activation loads, so staging waits only for
-// the activations while the weights stream in; nothing else waits on memory.
+// (rtl, kw) takes SPW consecutive super-steps of row tile rtl (2; 4 when K is
+// longer than 16 x 2 super-steps), and the KW waves of a row tile cover K.
+// Every weight load of a wave is issued when it starts, right after the
+// activation loads, so staging waits only for the activations while the
+// weights stream in; nothing else waits on memory.
 // The waves of a row tile add their D tiles through LDS in a fixed order, so
 // results do not depend on scheduling.
 #include <stdio.h>
@@ -299,6 +300,10 @@ bool plan_oneshot(const GemvLaunch& L, int cus, size_t lds_max, Plan* out) {
     Plan p{};
     p.SPW = tg.nss >= 2 ? 2 : 1;
     p.KW = (tg.nss + p.SPW - 1) / p.SPW;
+    if (p.KW > kMaxKW && !L.glu) {  // long K: four super-steps per wave
+        p.SPW = 4;
+        p.KW = (tg.nss + p.SPW - 1) / p.SPW;
+    }
     if (p.KW > kMaxKW) return false;
     const size_t x_bytes = (size_t)tg.nss * 1024 * R;
     auto lds_of = [&](int rtw) { return std::max(x_bytes, (size_t)p.KW * rtw * NT * 1024); };
@@ -333,6 +338,8 @@ hipError_t launch_one(const OneShotArgs& a, const Plan& p, int groups, hipStream
 template <bool GLU, bool XB, bool TILED>
 hipError_t launch_variant(const OneShotArgs& a, const Plan& p, int groups, hipStream_t s) {
     constexpr int R1 = XB ? 1 : 3;
+    if constexpr (!GLU)
+        if (p.SPW == 4) return launch_one<4, 0, GLU, XB, TILED>(a, p, groups, s);
     if (a.R == R1)
         return p.SPW == 2 ? launch_one<2, R1, GLU, XB, TILED>(a, p, groups, s)
                           : launch_one<1, R1, GLU, XB, TILED>(a, p, groups, s);
@@ -418,10 +425,13 @@ int launch_gemv(const GemvLaunch& L, hipStream_t s) {
     if (L.M < 1 || L.M > kGemvMaxM) return fail(ALV_ERR_ARG, "stream kernel takes 1 <= M <= %d (got %d)", kGemvMaxM, L.M);
     if (L.parts != 1 && L.parts != 3) return fail(ALV_ERR_ARG, "parts must be 1 or 3");
     if (L.Xb && (L.parts != 1 || L.glu)) return fail(ALV_ERR_ARG, "bf16 activations take one term and no GLU");
-    // Token groups of at most 16 A rows; a shape the one-shot plan does not
-    // cover (K above 16 super-steps per wave x 16 waves, or staging beyond the
-    // LDS) runs on the executor.
-    const int mc = std::max(1, 16 / L.parts);
+    // Token groups of at most 16 A rows whose activations (the whole K range
+    // of every token of the group) fit the LDS; a shape the one-shot plan does
+    // not cover (K above 16 waves x 4 super-steps, or one token's staging
+    // beyond the LDS) runs on the executor.
+    const size_t per_token = (size_t)tile_geom(L.K).nss * 1024 * L.parts;
+    const size_t lds_max = std::min<size_t>(device_lds(), 160 * 1024);
+    const int mc = std::max(1, std::min(16 / L.parts, (int)(lds_max / per_token)));
     for (int m0 = 0; m0 < L.M; m0 += mc) {
         GemvLaunch c = L;
         c.M = std::min(mc, L.M - m0);

@@ -16,8 +16,9 @@ void clear_error();
 int hip_check(hipError_t e, const char* what);
 
 // Per-(device, stream) synchronisation words of the op-chain executor. They
-// are zero when a launch starts and every launch leaves them zero. Allocated
-// on first use on a stream (which synchronises the device); steady-state calls
+// are zero when a launch starts and every launch leaves them zero. A device's
+// words (a set for each of up to 64 streams) are allocated at its first call,
+// which synchronises the device; later calls, a stream's first included,
 // allocate nothing.
 struct Workspace {
     uint32_t* counters = nullptr;
@@ -69,9 +70,11 @@ constexpr int kSyncError = kSyncExit2 + 1;
 constexpr int kSyncWords = kSyncError + 1;
 
 // Device-side descriptor of one op (kernel argument; every field is
-// wave-uniform). A row tile is 16 output rows; its work is U = nss * (glu ? 2 : 1)
-// units (one super-step of 512 k of one matrix), split over the `gw` waves of
-// one of the r wave groups of a workgroup.
+// wave-uniform). Work split: a workgroup of 16 waves holds rtw row-tile slots
+// of (1 << kw_shift) waves each; wave kw of a slot takes super-steps
+// [kw * spw, kw * spw + spw) of its row tile, for each of the op's one or two
+// matrices. Round r, slot s of workgroup b is row tile (r * rtw + s) * grid + b;
+// workgroup b runs nr_full + (b < nr_rem) rounds.
 struct OpDesc {
     const uint8_t* W0;
     const uint8_t* W1;
@@ -79,12 +82,9 @@ struct OpDesc {
     float* Y;
     uint16_t* Yb;
     uint32_t wbytes, xbytes, rstride;
-    int ldx, ldy, M, N, K, parts, R, nb, nss, ng_last, RT, U, r, act;
+    int ldx, ldy, M, N, K, parts, R, nb, nss, ng_last, RT, act;
     int glu, xb, dep, signal;
-    // Work split, precomputed: waves per group = 1 << gw_shift, steps per
-    // round numax, row-tile stride of a group wstride = grid * r; workgroup b
-    // runs nr_full + (b < nr_rem) rounds.
-    int gw_shift, numax, wstride, nr_full, nr_rem;
+    int spw, kw_shift, rtw, nr_full, nr_rem;
 };
 struct ExecArgs {
     OpDesc op[kMaxOps];
@@ -92,7 +92,6 @@ struct ExecArgs {
     uint32_t xs_bytes;  // LDS bytes of the staged activations (the reduction scratch follows)
     uint32_t spin_limit;
     int last_wait;  // the last op that waits for an earlier one (-1: none, no counters are used)
-    int flags;
     uint32_t* sync;
 };
 // Run ops[0..nops) on `s`: one launch per group of tokens that fits the LDS

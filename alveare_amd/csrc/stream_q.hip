@@ -1,58 +1,43 @@
-// Streaming Q4 executor for decode and small-M batches (gfx950): one launch
-// runs a chain of up to kMaxOps matrix-vector ops -- a projection, or a
+// Persistent op-chain executor for decode and small-M batches (gfx950): one
+// launch runs a chain of up to kMaxOps matrix-vector ops -- a projection, or a
 // gate/up pair with the GLU activation -- where an op may take its input from
-// an earlier op of the chain: the kernel behind alv_chain_run, and behind
-// single ops whose shape the one-shot kernel (oneshot_q.hip) does not cover.
+// an earlier op of the chain. It is the kernel behind alv_chain_run with
+// ALV_CHAIN_FUSED=1, and behind single ops whose shape the one-shot kernel
+// (oneshot_q.hip) does not cover.
 //
-// The kernel is HBM-bound by design: weights are read once with 16-byte
-// loads, dequantized in registers (q4_device.h::dequant8, ~2.4 VALU ops per
-// weight) and multiplied on the matrix cores. Doing the products on MFMA even
-// at M = 1 keeps the VALU budget for the exact bf16 dequantization.
+// Each op is computed the way the one-shot kernel computes it -- MFMA
+// v_mfma_f32_16x16x32_bf16 with B = 16 weight rows x 32 k and A = the
+// activation terms staged in LDS in operand order; a row tile's K range split
+// over the waves of one slot of a workgroup, whose D tiles are added through
+// LDS in a fixed order -- but the grid is resident for the whole chain (one
+// workgroup of 8 waves per CU; a wave holds up to 4 units -- 80 VGPRs -- of
+// loads in flight) and walks the ops in order:
 //
-// MFMA mapping (v_mfma_f32_16x16x32_bf16, D = A x B):
-//   B columns = 16 weight rows (one row tile), B k = 32 weights;
-//   A rows    = activation terms: token m contributes `parts` rows (its fp32
-//               value split exactly into 3 bf16 terms, or 1 term when the
-//               activation is bf16); rows >= parts*M are don't-care (their
-//               lanes read a valid row; the D rows they feed are unused).
-// Lane l = (j, g), j = l % 16, g = l / 16 owns weight row j and, within a
-// super-step of 16 blocks (512 k), blocks 4g..4g+3 of that row: an 80-byte
-// run held as five 16-byte pieces. The A operand for the same k comes from
-// LDS, where the workgroup staged the whole K range in MFMA operand order.
+//   for each op: wait for its input (if it reads an earlier op's output),
+//                stage the activations in LDS,
+//     for each round: compute the wave's units (their weights are already in
+//                flight), issue the weight loads of the NEXT round or op, add
+//                the slot's D tiles, write the outputs.
 //
-// Work split: one workgroup of 16 waves per CU (the grid is exactly the
-// resident capacity). A row tile's work is U units -- one super-step of one
-// matrix (gate and up are separate units of a gate/up op) -- split evenly over
-// a group of 16 / r waves; the r groups of a workgroup take different row
-// tiles. Each round every group finishes one row tile: the waves leave their
-// partial D tiles in LDS, and after a barrier the workgroup sums them per
-// output in a fixed order (waves, then terms) and writes the outputs. No
-// partial sum leaves the workgroup, so results do not depend on scheduling
-// and no global-memory handshake sits inside an op.
+// Issuing the next op's weights as soon as a wave's compute is done keeps HBM
+// busy across op boundaries: while the workgroup reduces, writes, signals and
+// waits for the next op's input, those loads are already in flight -- the
+// bubble a separate launch pays (drain, launch, ramp-up) is covered.
 //
-// Streaming: every wave walks one sequence of steps across all ops of the
-// chain and keeps the weight loads of the next P steps in flight while it
-// computes the current one -- also across op boundaries, so the next op's
-// weights stream in while the current op drains and while a workgroup waits
-// for its input. The ring is unrolled (each op's step count per wave is padded
-// to a multiple of P + 1), so every buffer index is static; all waves of a
-// workgroup run the same number of steps per round, so every barrier is the
-// same instruction for all of them.
+// Dependencies: a workgroup counts the row tiles it wrote into one of
+// kSyncSlots words per op once its stores have landed (same-address device
+// atomics serialise, so the counts are spread); a consumer's wave 0 polls the
+// words with one sc1 load per lane and a wave sum. Outputs are written with
+// agent-scope stores and a dependent op's activations read with sc1, so no
+// L2-wide writeback or invalidate is needed. Every workgroup of the grid is
+// resident (the grid is the occupancy), waits are bounded (a timeout sets a
+// flag the host reads through alv_check_async), and the last workgroup past
+// the chain's last wait resets the words for the next launch.
 //
-// Dependencies: an op whose input is an earlier op's output waits, per
-// workgroup, until every row tile of that op has been written. Outputs go
-// through the device-coherent level (agent-scope stores), activation staging
-// of a dependent op reads with sc1, so no L2-wide writeback or invalidate is
-// needed. Waits are bounded (a timeout sets a flag the host reads through
-// alv_check_async) and the last workgroup to leave resets the counters for the
-// next launch.
-//
-// Weights come either in the combined layout (RAW, one-op chains: a lane's
-// 80-byte run is contiguous, a wave's 16-byte loads touch 16 rows x 4 runs and
-// lean on the caches to merge) or in the tiled layout (TILED, q4_device.h:
-// every load instruction of a wave reads 1 KiB of contiguous memory, with the
-// nontemporal hint since weights are read once). Out-of-range loads (buffer
-// resource bounds) return zero, which is how tails and empty steps are handled.
+// Weights come either in the combined layout (RAW, one-op chains) or in the
+// tiled layout (TILED, q4_device.h: every 16-byte load instruction of a wave
+// reads 1 KiB of contiguous memory, nontemporal). Out-of-range loads (buffer
+// resource bounds) return zero, which is how tails and idle waves are handled.
 #include <stdio.h>
 #include <stdlib.h>
 
@@ -63,7 +48,7 @@
 
 namespace alv {
 
-constexpr int kExecThreads = 1024;           // 16 waves: one workgroup per CU
+constexpr int kExecThreads = 512;  // 8 waves: one workgroup per CU, 256 VGPRs per wave
 constexpr int kWPB = kExecThreads / 64;
 constexpr size_t kScratchBytes = kWPB * 2 * 1024;  // per wave: one 16x16 fp32 D tile per matrix
 
@@ -100,60 +85,33 @@ __device__ __forceinline__ void stage_octet(const u32x4 (&v)[2], __bf16* dst, in
     }
 }
 
-// Steps of one wave in one op (wave-uniform). Round i: the wave's group works
-// on row tile worker0 + i * wstride; step k of the round is unit u0 + k when
-// k < nu (steps nu..numax-1 are empty, so every wave of the workgroup runs
-// numax steps per round).
-struct WavePlan {
-    int worker0, wstride;
-    int u0, nu, numax;
-    int nrounds;           // rounds of this workgroup (those of its group 0)
-    int steps, steps_pad;  // nrounds * numax, padded to a multiple of the ring size
-};
 
-// No divisions: the scalar unit is shared by the CU's 16 waves, so per-op
-// set-up work is kept to shifts and the host precomputes the rest.
-template <int NB>
-__device__ __forceinline__ WavePlan wave_plan(const OpDesc& d, int b, int G, int wave) {
-    WavePlan p;
-    const int q = wave >> d.gw_shift, wi = wave & ((1 << d.gw_shift) - 1);
-    p.worker0 = q * G + b;
-    p.wstride = d.wstride;
-    p.u0 = (wi * d.U) >> d.gw_shift;
-    p.nu = (((wi + 1) * d.U) >> d.gw_shift) - p.u0;
-    p.numax = d.numax;
-    p.nrounds = d.nr_full + (b < d.nr_rem ? 1 : 0);
-    p.steps = p.nrounds * p.numax;
-    p.steps_pad = (p.steps + NB - 1) / NB * NB;
-    return p;
-}
-
-// Output (token m, row jj) of matrix n of group q, from the D tiles the
-// group's GW waves left in LDS: the sum over the waves (in order) of the sum
-// over the PARTS terms (in order) of D[m * PARTS + p][jj]. Straight-line code:
-// every load issues before the first add.
-template <int PARTS, int GW>
-__device__ __forceinline__ float group_sum(const float* scr, int q, int n, int NT, int m, int jj) {
+// Output (token m, row jj) of matrix n of the slot whose waves start at w0:
+// the sum over the slot's KW waves (in order) of the sum over the PARTS terms
+// (in order) of D[m * PARTS + p][jj]. Straight-line: the loads of a batch of
+// waves issue before their adds.
+template <int PARTS, int KW>
+__device__ __forceinline__ float slot_sum(const float* scr, int w0, int n, int NT, int m, int jj) {
     int off[PARTS];
 #pragma unroll
     for (int p = 0; p < PARTS; ++p) {
         const int i = m * PARTS + p;
         off[p] = (jj + 16 * (i >> 2)) * 4 + (i & 3);
     }
-    constexpr int C = GW < 4 ? GW : 4;  // waves per batch of loads (bounds the registers held)
+    constexpr int C = KW < 4 ? KW : 4;
     float s = 0.0f;
 #pragma unroll
-    for (int w0 = 0; w0 < GW; w0 += C) {
+    for (int k0 = 0; k0 < KW; k0 += C) {
         float v[C][PARTS];
 #pragma unroll
-        for (int w = 0; w < C; ++w)
+        for (int k = 0; k < C; ++k)
 #pragma unroll
-            for (int p = 0; p < PARTS; ++p) v[w][p] = scr[((q * GW + w0 + w) * NT + n) * 256 + off[p]];
+            for (int p = 0; p < PARTS; ++p) v[k][p] = scr[((w0 + k0 + k) * NT + n) * 256 + off[p]];
 #pragma unroll
-        for (int w = 0; w < C; ++w) {
-            float ws = v[w][0];
+        for (int k = 0; k < C; ++k) {
+            float ws = v[k][0];
 #pragma unroll
-            for (int p = 1; p < PARTS; ++p) ws += v[w][p];
+            for (int p = 1; p < PARTS; ++p) ws += v[k][p];
             s += ws;
         }
     }
@@ -161,20 +119,101 @@ __device__ __forceinline__ float group_sum(const float* scr, int q, int n, int N
 }
 
 template <int PARTS>
-__device__ __forceinline__ float group_sum_gw(int gw, const float* scr, int q, int n, int NT, int m, int jj) {
-    switch (gw) {
-        case 1: return group_sum<PARTS, 1>(scr, q, n, NT, m, jj);
-        case 2: return group_sum<PARTS, 2>(scr, q, n, NT, m, jj);
-        case 4: return group_sum<PARTS, 4>(scr, q, n, NT, m, jj);
-        case 8: return group_sum<PARTS, 8>(scr, q, n, NT, m, jj);
-        default: return group_sum<PARTS, 16>(scr, q, n, NT, m, jj);
+__device__ __forceinline__ float slot_sum_kw(int kw, const float* scr, int w0, int n, int NT, int m, int jj) {
+    switch (kw) {
+        case 1: return slot_sum<PARTS, 1>(scr, w0, n, NT, m, jj);
+        case 2: return slot_sum<PARTS, 2>(scr, w0, n, NT, m, jj);
+        case 4: return slot_sum<PARTS, 4>(scr, w0, n, NT, m, jj);
+        default: return slot_sum<PARTS, 8>(scr, w0, n, NT, m, jj);
     }
 }
 
-// P: steps of prefetch.
-template <int P, bool TILED>
+using UnitBuf = u32x4[4][5];  // [unit][16-byte piece]; unit k = matrix * spw + super-step of the wave
+
+// The weight loads of one round of op d for wave kw of a slot on row tile rt:
+// units k < NT * spw, unit k = super-step kw * spw + k % spw of matrix k / spw.
+// One code path for every split (unit indices are static, the unit count is a
+// uniform run-time bound), so one kernel runs every op of a chain. Tiled: lane
+// l at 16 l of each 256 * ng-byte plane of the (row tile, super-step) tile.
+// Combined: lane (j, g) reads the 80-byte run of row j at block 16 ss + 4 g.
+// Loads of a missing row tile, super-step or unit start past the buffer and
+// read zero.
+template <bool TILED>
+__device__ __forceinline__ void issue_round(UnitBuf& q, const OpDesc& d, int rt, int kw, int lane, bool valid) {
+    const int j = lane & 15, g = lane >> 4;
+    const int spw = d.spw, units = (d.glu ? 2 : 1) * spw;
+    const __amdgpu_buffer_rsrc_t r0 = make_rsrc(d.W0, d.wbytes);
+    const __amdgpu_buffer_rsrc_t r1 = make_rsrc(d.glu ? d.W1 : d.W0, d.wbytes);
+    // Every unit issues its five loads on every path (a unit past the op's
+    // count reads past the buffer, i.e. zero): the number of loads in flight
+    // is a compile-time constant, so the compiler's waits for each unit (and
+    // for activations loaded before it) count exactly, and compute starts on
+    // the first unit while the rest are still arriving.
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int n = k >= spw ? 1 : 0;
+        const int ss = kw * spw + (k - n * spw);
+        const bool ok = valid && k < units && ss < d.nss;
+        uint32_t off = d.wbytes, step = 16;
+        if constexpr (TILED) {
+            step = ss == d.nss - 1 ? 256u * (uint32_t)d.ng_last : 1024u;
+            if (ok) off = (uint32_t)rt * d.rstride + (uint32_t)ss * 5120u + 16u * (uint32_t)lane;
+        } else {
+            const int row = rt * 16 + j;
+            if (ok && row < d.N) off = (uint32_t)row * d.rstride + (uint32_t)(ss * 16 + g * 4) * kBlockBytes;
+        }
+        const __amdgpu_buffer_rsrc_t r = n ? r1 : r0;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) q[k][i] = buf_load16_so<TILED>(r, off, step * i);
+    }
+}
+
+// Dequantize + MFMA of one round's units into acc[matrix]. Blocks past the end
+// of a row (combined: the next row's bytes; tiled: lanes past the last
+// super-step's ng) get their scale cleared, so they dequantize to zero (their
+// activations are zero too).
+template <bool TILED>
+__device__ __forceinline__ void compute_round(const UnitBuf& q, const OpDesc& d, const __bf16* xs, int kw, int lane,
+                                              f32x4 (&acc)[2][2]) {
+    const int j = lane & 15, g = lane >> 4;
+    const int R = d.R;
+    const int spw = d.spw, units = (d.glu ? 2 : 1) * spw;
+    const __bf16* xa = xs + ((size_t)(kw * spw * 64 + g) * R + min(j, R - 1)) * 8;
+    const int tstride = 4 * R * 8;  // bf16 elements between consecutive operand slots of a lane
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if (k >= units) break;  // uniform
+        const int n = k >= spw ? 1 : 0;
+        const int s = k - n * spw;
+        const int ss = kw * spw + s;
+        if (ss >= d.nss) continue;  // uniform
+        const int nvalid = TILED ? (ss != d.nss - 1 || g < d.ng_last ? 4 : 0) : d.nb - (ss * 16 + g * 4);
+        const __bf16* xk = xa + s * 16 * tstride;
+#pragma unroll
+        for (int bl = 0; bl < 4; ++bl) {
+            uint32_t dw[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int w = 5 * bl + t;
+                dw[t] = q[k][w >> 2][w & 3];
+            }
+            const int w4 = 5 * bl + 4;
+            const Scale sc = make_scale(scale_of(bl < nvalid ? (uint32_t)q[k][w4 >> 2][w4 & 3] : 0u));
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const bf16x8 av = *reinterpret_cast<const bf16x8*>(xk + (bl * 4 + t) * tstride);
+                const bf16x8 b = dequant8(dw[t], sc);
+                if (n)
+                    acc[1][t & 1] = mfma16x16x32(av, b, acc[1][t & 1]);
+                else
+                    acc[0][t & 1] = mfma16x16x32(av, b, acc[0][t & 1]);
+            }
+        }
+    }
+}
+
+template <bool TILED>
 __global__ void __launch_bounds__(kExecThreads) q4_exec_kernel(ExecArgs a) {
-    constexpr int NB = P + 1;
     extern __shared__ __align__(16) unsigned char smem[];
     __bf16* xs = reinterpret_cast<__bf16*>(smem);
     float* scr = reinterpret_cast<float*>(smem + a.xs_bytes);
@@ -185,49 +224,15 @@ __global__ void __launch_bounds__(kExecThreads) q4_exec_kernel(ExecArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = gridDim.x;
     const int blk = blockIdx.x;
-    const int j = lane & 15;
-    const int g = lane >> 4;
 
-    // ---- weight loads of one step ----------------------------------------------
-    // Lane offset (fixed) + step offset (wave-uniform, in soffset). An empty
-    // step starts at wbytes: every piece is out of range and reads zero.
-    // Combined layout (one-op chains): lane (j, g) sits at row j, byte 80 g of
-    // the super-step; rows past N fall past wbytes. Tiled layout: lane l at
-    // 16 l of each plane.
-    const uint32_t voff = TILED ? 16u * (uint32_t)lane : (uint32_t)j * a.op[0].rstride + 80u * (uint32_t)g;
-    // The stream parameters of the op the prefetch cursor is in, copied once
-    // per op (kernel-argument loads are slow to come back and share a counter
-    // with LDS reads).
-    struct StreamOp {
-        const uint8_t* W0;
-        const uint8_t* W1;
-        uint32_t wbytes, rstride;
-        int nss, ng_last, RT;
-    };
-    auto stream_op = [&](int o) {
-        const OpDesc& d = a.op[o];
-        return StreamOp{d.W0, d.W1, d.wbytes, d.rstride, d.nss, d.ng_last, d.RT};
-    };
-    auto issue = [&](u32x4 (&q)[5], const StreamOp& d, int rt, int n, int ss, bool valid) {
-        uint32_t soff = d.wbytes, step = 16;
-        if constexpr (TILED) {
-            step = ss == d.nss - 1 ? 256u * (uint32_t)d.ng_last : 1024u;
-            if (valid) soff = (uint32_t)rt * d.rstride + (uint32_t)ss * 5120u;
-        } else {
-            if (valid) soff = (uint32_t)rt * 16u * d.rstride + (uint32_t)ss * 320u;
-        }
-        const __amdgpu_buffer_rsrc_t r = make_rsrc(n ? d.W1 : d.W0, d.wbytes);
-#pragma unroll
-        for (int i = 0; i < 5; ++i) q[i] = buf_load16_so<TILED>(r, voff, soff + step * i);
-    };
+    auto rounds_of = [&](const OpDesc& d) { return d.nr_full + (blk < d.nr_rem ? 1 : 0); };
 
-    // ---- activation staging ------------------------------------------------------
+    // ---- activations of op d into LDS, in MFMA operand order ---------------------
     // Octet o8 (8 consecutive k) of token m: k = 8 o8. It lives at operand slot
     // ((o8 / 64) * 16 + o8 % 16) * 4 + (o8 / 16) % 4, i.e. super-step o8 / 64,
     // block 4g + bl with g = (o8 / 16) % 4, bl = (o8 / 4) % 4, dword t = o8 % 4:
-    // slot = (ss * 16 + bl * 4 + t) * 4 + g. Staging unit u = m * octs + o8.
-    // A dependent op's input was just written through by other workgroups:
-    // those loads use sc1.
+    // slot = (ss * 16 + bl * 4 + t) * 4 + g. A dependent op's input was just
+    // written through by other workgroups: those loads use sc1.
     auto stage_load = [&](const OpDesc& d, int u, u32x4 (&v)[2]) {
         const int ES = d.xb ? 2 : 4;
         const int octs = d.nss * 64;
@@ -239,12 +244,15 @@ __global__ void __launch_bounds__(kExecThreads) q4_exec_kernel(ExecArgs a) {
         const int k = o8 * 8;
         const uint32_t off = k < d.K && m < d.M ? (uint32_t)((m * d.ldx + k) * ES) : d.xbytes;
         const __amdgpu_buffer_rsrc_t rx = make_rsrc(d.X, d.xbytes);
+        // Two loads on every path (the second is out of range for bf16 input)
+        // so that the count of loads in flight stays a compile-time constant.
+        const uint32_t off1 = d.xb ? d.xbytes : off + 16;
         if (d.dep >= 0) {
             v[0] = buf_load16_sc1(rx, off);
-            v[1] = d.xb ? u32x4{0u, 0u, 0u, 0u} : buf_load16_sc1(rx, off + 16);
+            v[1] = buf_load16_sc1(rx, off1);
         } else {
             v[0] = buf_load16(rx, off);
-            v[1] = d.xb ? u32x4{0u, 0u, 0u, 0u} : buf_load16(rx, off + 16);
+            v[1] = buf_load16(rx, off1);
         }
     };
     auto stage_store = [&](const OpDesc& d, int u, const u32x4 (&v)[2]) {
@@ -261,7 +269,7 @@ __global__ void __launch_bounds__(kExecThreads) q4_exec_kernel(ExecArgs a) {
         else
             stage_octet<false>(v, dst, d.parts);
     };
-    auto stage_all = [&](const OpDesc& d) {
+    auto stage = [&](const OpDesc& d) {
         const int units = d.nss * 64 * d.M;
         for (int u = tid; u < units; u += nthr) {
             u32x4 v[2];
@@ -269,72 +277,30 @@ __global__ void __launch_bounds__(kExecThreads) q4_exec_kernel(ExecArgs a) {
             stage_store(d, u, v);
         }
     };
-    // The first op's activations are staged before any weight load is issued:
-    // issued together, the small activation reads queue behind the weight
-    // stream (~3 us at full load) and every wave waits for them.
-    const OpDesc& d0 = a.op[0];
-    const int units0 = d0.nss * 64 * d0.M;
-    const bool reg_stage = (a.flags & 1) && units0 <= 2 * nthr;
-    u32x4 xv[2][2];
-    if (reg_stage) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) stage_load(d0, min(tid + i * nthr, units0), xv[i]);
-    } else {
-        stage_all(d0);
-    }
 
-    // Prefetch cursor: op po, step pstep of this wave in that op, round pround,
-    // step pk within the round.
-    u32x4 buf[NB][5];
-    int po = 0, pstep = 0, pround = 0, pk = 0;
-    WavePlan pp = wave_plan<NB>(a.op[0], blk, G, wave);
-    StreamOp ps = stream_op(0);
-    auto skip_empty_ops = [&]() {
-        while (po < a.nops && pstep >= pp.steps_pad) {
-            if (++po < a.nops) {
-                pp = wave_plan<NB>(a.op[po], blk, G, wave);
-                ps = stream_op(po);
-                pstep = pround = pk = 0;
-            }
-        }
+    // ---- the weights of round r of op o for this wave -----------------------------
+    UnitBuf q;
+    auto issue = [&](int o, int r) {
+        const OpDesc& d = a.op[o];
+        const int rtl = wave >> d.kw_shift, kw = wave & ((1 << d.kw_shift) - 1);
+        const int rt = (r * d.rtw + rtl) * G + blk;
+        issue_round<TILED>(q, d, rt, kw, lane, rtl < d.rtw && rt < d.RT);
     };
-    skip_empty_ops();
-    auto issue_next = [&](u32x4 (&q)[5]) {
-        int rt = 0, n = 0, ss = 0;
-        bool valid = false;
-        if (po < a.nops) {
-            rt = pp.worker0 + pround * pp.wstride;
-            const int u = pp.u0 + pk;
-            valid = pstep < pp.steps && pk < pp.nu && rt < ps.RT;
-            n = u >= ps.nss ? 1 : 0;
-            ss = u - n * ps.nss;
-        }
-        issue(q, ps, rt, n, ss, valid);
-        if (po < a.nops) {
-            ++pstep;
-            if (++pk == pp.numax) {
-                pk = 0;
-                ++pround;
-            }
-            skip_empty_ops();
-        }
+    f32x4 acc[2][2];
+    auto zero_acc = [&]() {
+#pragma unroll
+        for (int n = 0; n < 2; ++n) acc[n][0] = acc[n][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     };
-#pragma unroll
-    for (int b = 0; b < P; ++b) issue_next(buf[b]);
-    if (reg_stage) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-            if (tid + i * nthr < units0) stage_store(d0, tid + i * nthr, xv[i]);
-    }
+    auto compute = [&](const OpDesc& d, int kw) { compute_round<TILED>(q, d, xs, kw, lane, acc); };
 
     // ---- counters: the last workgroup past the chain's last wait resets them -------
     // Two-level count (same-address atomics serialise): workgroup blk into slot
     // blk % kSyncSlots; the workgroup that completes its slot counts the slot
     // into one word; the one that completes that word is the last. By then
     // every workgroup has passed every wait, and every count of a row tile done
-    // came before its workgroup's last wait (a producer precedes its
-    // consumer). Called by wave 0, which issued this workgroup's counts: they
-    // complete first, so the reset cannot be overtaken by one of them.
+    // came before its workgroup's last wait (a producer precedes its consumer).
+    // Called by wave 0, which issues this workgroup's counts: they complete
+    // first, so the reset cannot be overtaken by one of them.
     auto leave = [&]() {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         uint32_t last = 0;
@@ -355,109 +321,114 @@ __global__ void __launch_bounds__(kExecThreads) q4_exec_kernel(ExecArgs a) {
         }
     };
 
-    f32x4 acc[2][2];
-    auto zero_acc = [&]() {
-#pragma unroll
-        for (int n = 0; n < 2; ++n) acc[n][0] = acc[n][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // The round after (o, r) that this workgroup runs, or o = nops.
+    auto next_round = [&](int& o, int& r) {
+        if (++r < rounds_of(a.op[o])) return;
+        r = 0;
+        while (++o < a.nops && rounds_of(a.op[o]) == 0) {
+        }
     };
 
+    bool loaded = false;  // q holds the weights of the round about to run
     for (int o = 0; o < a.nops; ++o) {
         const OpDesc& d = a.op[o];
-        const WavePlan cp = wave_plan<NB>(d, blk, G, wave);
-        const int R = d.R;
-        const int NT = d.glu ? 2 : 1;
-
-        // ---- op boundary: wait for the input, stage the activations -----------
-        if (o > 0) {
-            __syncthreads();  // every wave is done with the previous op's operands
-            if (cp.nrounds > 0) {
-                if (d.dep >= 0) {
-                    // Wave 0 polls the producer's spread counters: one sc1 load
-                    // per lane, summed across the wave.
-                    if (wave == 0) {
-                        const uint32_t target = (uint32_t)a.op[d.dep].RT;
-                        uint32_t n = 0;
-                        while (true) {
-                            uint32_t v = __hip_atomic_load(&a.sync[d.dep * kSyncSlots + lane], __ATOMIC_RELAXED,
-                                                           __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-                            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-                            if (v >= target) break;
-                            __builtin_amdgcn_s_sleep(2);
-                            if (++n > a.spin_limit) {
-                                if (lane == 0)
-                                    __hip_atomic_store(&a.sync[kSyncError], 1u, __ATOMIC_RELAXED,
-                                                       __HIP_MEMORY_SCOPE_AGENT);
-                                break;
-                            }
-                        }
-                    }
-                    __syncthreads();
-                }
-                stage_all(d);
-            }
+        const int nr = rounds_of(d);
+        if (nr == 0) {
             if (o == a.last_wait && wave == 0) leave();
+            continue;
+        }
+        const int NT = d.glu ? 2 : 1;
+        const int KW = 1 << d.kw_shift;
+        const int rtl = wave >> d.kw_shift, kw = wave & (KW - 1);
+        const bool active = rtl < d.rtw;
+
+        // ---- op boundary: wait for the input, stage it --------------------------------
+        __syncthreads();  // the previous op is done with the LDS
+        if (d.dep >= 0) {
+            // Wave 0 polls the producer's spread counters: one sc1 load per
+            // lane, summed across the wave.
+            if (wave == 0) {
+                const uint32_t target = (uint32_t)a.op[d.dep].RT;
+                uint32_t n = 0;
+                while (true) {
+                    uint32_t v = __hip_atomic_load(&a.sync[d.dep * kSyncSlots + lane], __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+                    if (v >= target) break;
+                    __builtin_amdgcn_s_sleep(2);
+                    if (++n > a.spin_limit) {
+                        if (lane == 0)
+                            __hip_atomic_store(&a.sync[kSyncError], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        if (o == a.last_wait && wave == 0) leave();
+        const int xunits = d.nss * 64 * d.M;
+        if (!loaded && xunits <= 2 * nthr) {
+            // No weights in flight yet: the activation loads go out first, the
+            // weights right behind them, and the staging waits only for the
+            // activations (loads complete in order).
+            u32x4 xv[2][2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) stage_load(d, min(tid + i * nthr, xunits), xv[i]);
+            issue(o, 0);
+            loaded = true;
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                if (tid + i * nthr < xunits) stage_store(d, tid + i * nthr, xv[i]);
+        } else {
+            // Weights already in flight (issued during the previous op), or
+            // more activations than registers hold: stage, then load.
+            stage(d);
+            if (!loaded) {
+                issue(o, 0);
+                loaded = true;
+            }
         }
         __syncthreads();
 
-        // ---- stream this op's steps ------------------------------------------------
-        const __bf16* xa = xs + ((size_t)g * R + min(j, R - 1)) * 8;  // operand base: slot g, row j
-
-        // One unit: super-step ss of one matrix, into ac.
-        auto compute_into = [&](const u32x4 (&q)[5], int ss, f32x4 (&ac)[2]) {
-            const int sl_off = ss * 64 * R * 8;  // this super-step's operands (bf16 elements)
-            // Blocks of this lane that exist. Tiled: a lane past the last
-            // super-step's ng reads the next plane's bytes; combined: blocks
-            // past the row end read the next row's. Their scales are cleared
-            // (their activations are zero), so they dequantize to zero.
-            const int nvalid = TILED ? (ss != d.nss - 1 || g < d.ng_last ? 4 : 0) : d.nb - (ss * 16 + g * 4);
-#pragma unroll
-            for (int bl = 0; bl < 4; ++bl) {
-                // dwords 5*bl .. 5*bl+4 of the 80-byte run are this block.
-                uint32_t dw[4];
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const int w = 5 * bl + t;
-                    dw[t] = q[w >> 2][w & 3];
-                }
-                const int w4 = 5 * bl + 4;
-                const uint32_t sd = bl < nvalid ? (uint32_t)q[w4 >> 2][w4 & 3] : 0u;
-                const Scale sc = make_scale(scale_of(sd));
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const int so = sl_off + (bl * 4 + t) * 4 * R * 8;
-                    const bf16x8 b = dequant8(dw[t], sc);
-                    const bf16x8 av = *reinterpret_cast<const bf16x8*>(xa + so);
-                    ac[t & 1] = mfma16x16x32(av, b, ac[t & 1]);
-                }
+        for (int r = 0; r < nr; ++r) {
+            if (!loaded) issue(o, r);
+            zero_acc();
+            if (active) compute(d, kw);
+            loaded = false;
+            // The next round's (or op's) weights go out now, so they stream
+            // while this round is reduced and written and the next input is
+            // awaited. A wave that stores outputs a later op waits for issues
+            // them after its signal: its wait for the stores would also wait
+            // for them.
+            int no = o, nrr = r;
+            next_round(no, nrr);
+            const bool last = r == nr - 1;
+            const int outs = d.rtw * d.M * 16;
+            const bool storer = wave * 64 < outs;
+            const bool defer = storer && d.signal && last;
+            if (no < a.nops && !defer) {
+                issue(no, nrr);
+                loaded = true;
             }
-        };
-
-        // End of a round: the waves' D tiles go to LDS; output (group q, token
-        // m, row jj) = sum over the group's waves (in order) of the sum over
-        // terms p (in order) of D[m * parts + p][jj].
-        const int gw = 1 << d.gw_shift;
-        auto round_end = [&](int round) {
+            // ---- add the slot's D tiles, write the outputs ------------------------
 #pragma unroll
             for (int n = 0; n < 2; ++n)
-                if (n < NT)
-                    *reinterpret_cast<f32x4*>(scr + (wave * NT + n) * 256 + lane * 4) = acc[n][0] + acc[n][1];
-            zero_acc();
+                if (n < NT) *reinterpret_cast<f32x4*>(scr + (wave * NT + n) * 256 + lane * 4) = acc[n][0] + acc[n][1];
             __syncthreads();
-            const int per_group = d.M * 16;
-            const bool last = round == cp.nrounds - 1;
-            for (int idx = tid; idx < d.r * per_group; idx += nthr) {
-                const int q = idx / per_group, rem = idx - q * per_group;
+            for (int idx = tid; idx < outs; idx += nthr) {
+                const int per = d.M * 16;
+                const int sl = idx / per, rem = idx - sl * per;
                 const int m = rem >> 4, jj = rem & 15;
-                const int rt = q * G + blk + round * cp.wstride;
+                const int rt = (r * d.rtw + sl) * G + blk;
                 const int row = rt * 16 + jj;
                 if (rt >= d.RT || row >= d.N) continue;
                 float y[2] = {0.0f, 0.0f};
 #pragma unroll
                 for (int n = 0; n < 2; ++n)
                     if (n < NT)
-                        y[n] = d.parts == 3 ? group_sum_gw<3>(gw, scr, q, n, NT, m, jj)
-                                            : group_sum_gw<1>(gw, scr, q, n, NT, m, jj);
+                        y[n] = d.parts == 3 ? slot_sum_kw<3>(KW, scr, sl * KW, n, NT, m, jj)
+                                            : slot_sum_kw<1>(KW, scr, sl * KW, n, NT, m, jj);
                 // Final values, written through (a later op may read them).
                 float out = y[0];
                 if (d.glu) out = bf16_round(glu_act(bf16_round(y[0]), bf16_round(y[1]), d.act));
@@ -467,42 +438,23 @@ __global__ void __launch_bounds__(kExecThreads) q4_exec_kernel(ExecArgs a) {
                 else
                     __hip_atomic_store(&d.Y[(size_t)m * d.ldy + row], out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            // A later op reads this one: after the last round, the stores land
-            // before the workgroup counts its row tiles done. Only the waves
-            // that stored wait (the others keep their prefetch in flight).
-            if (d.signal && last && wave * 64 < d.r * per_group) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
-            if (d.signal && last && tid == 0) {
-                uint32_t done = 0;
-                for (int q = 0; q < d.r; ++q)
-                    for (int i = 0; i < cp.nrounds; ++i) done += q * G + blk + i * cp.wstride < d.RT ? 1u : 0u;
-                __hip_atomic_fetch_add(&a.sync[o * kSyncSlots + (blk & (kSyncSlots - 1))], done, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-            }
-        };
-
-        zero_acc();
-        int cround = 0, ck = 0;  // compute cursor
-        for (int s0 = 0; s0 < cp.steps_pad; s0 += NB) {
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                issue_next(buf[(b + P) % NB]);
-                if (s0 + b < cp.steps) {  // workgroup-uniform
-                    const int rt = cp.worker0 + cround * cp.wstride;
-                    if (ck < cp.nu && rt < d.RT) {  // wave-uniform
-                        const int u = cp.u0 + ck;
-                        if (u >= d.nss)
-                            compute_into(buf[b], u - d.nss, acc[1]);
-                        else
-                            compute_into(buf[b], u, acc[0]);
-                    }
-                    if (++ck == cp.numax) {
-                        round_end(cround);
-                        ck = 0;
-                        ++cround;
-                    }
+            if (d.signal && last) {
+                // The stores land before the workgroup counts its row tiles done.
+                if (storer) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+                if (tid == 0) {
+                    uint32_t done = 0;
+                    for (int rr = 0; rr < nr; ++rr)
+                        for (int sl = 0; sl < d.rtw; ++sl) done += (rr * d.rtw + sl) * G + blk < d.RT ? 1u : 0u;
+                    __hip_atomic_fetch_add(&a.sync[o * kSyncSlots + (blk & (kSyncSlots - 1))], done, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
+            if (no < a.nops && defer) {
+                issue(no, nrr);
+                loaded = true;
+            }
+            if (!last) __syncthreads();  // scratch reuse by the next round
         }
     }
 }
@@ -511,13 +463,13 @@ __global__ void __launch_bounds__(kExecThreads) q4_exec_kernel(ExecArgs a) {
 
 namespace {
 
-template <int P, bool TILED>
+template <bool TILED>
 hipError_t launch_one(const ExecArgs& a, int G, size_t lds, hipStream_t s) {
     static size_t allowed = 64 * 1024;
     if (lds > allowed) {
         // Dynamic LDS above 64 KiB (gfx950 has 160 KiB per CU) is opted into
         // per kernel.
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&q4_exec_kernel<P, TILED>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&q4_exec_kernel<TILED>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) {
             (void)hipGetLastError();
@@ -525,14 +477,14 @@ hipError_t launch_one(const ExecArgs& a, int G, size_t lds, hipStream_t s) {
         }
         allowed = lds;
     }
-    hipLaunchKernelGGL((q4_exec_kernel<P, TILED>), dim3(G), dim3(kExecThreads), lds, s, a);
+    hipLaunchKernelGGL((q4_exec_kernel<TILED>), dim3(G), dim3(kExecThreads), lds, s, a);
     return hipGetLastError();
 }
 
-template <int P, bool TILED>
+template <bool TILED>
 int occupancy(size_t lds) {
     int nb = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, q4_exec_kernel<P, TILED>, kExecThreads, lds) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, q4_exec_kernel<TILED>, kExecThreads, lds) != hipSuccess)
         return 0;
     return nb;
 }
@@ -557,35 +509,37 @@ DevInfo dev_info() {
     return d;
 }
 
-// Prefetch depth: P = 1 (one step in flight per wave while it computes
-// another: 16 waves x 5 KiB per CU cover the HBM latency-bandwidth product, and
-// the 128-VGPR budget of 16 waves per CU holds P = 1 without spills) unless
-// overridden (tuning: ALV_EXEC_P=1|2).
-int prefetch_depth() {
-    static int p = 0;
-    if (!p) {
-        p = 1;
-        if (const char* e = getenv("ALV_EXEC_P")) {
-            const int v = atoi(e);
-            if (v == 1 || v == 2) p = v;
+// Work split of one op over G workgroups of 16 waves: super-steps per wave
+// (spw), waves per row-tile slot (a power of two), slots per workgroup. The
+// fewest rounds win (each round's loads all go out at once); on a tie the
+// smaller spw (more waves, fewer registers held). False when K is too long.
+bool plan_op(OpDesc& d, int G) {
+    const int NT = d.glu ? 2 : 1;
+    int best_rounds = 0;
+    bool found = false;
+    for (int spw : {1, 2, 4}) {
+        if (spw * NT > 4) break;
+        const int kw = (d.nss + spw - 1) / spw;
+        if (kw > kWPB) continue;
+        int KW = 1;
+        while (KW < kw) KW *= 2;
+        const int rtw = kWPB / KW;
+        const long per_round = (long)G * rtw;
+        const int rounds = (int)((d.RT + per_round - 1) / per_round);
+        if (!found || rounds < best_rounds) {
+            found = true;
+            best_rounds = rounds;
+            d.spw = spw;
+            d.kw_shift = __builtin_ctz(KW);
+            d.rtw = rtw;
+            d.nr_full = (int)(d.RT / per_round);
+            d.nr_rem = (int)(d.RT % per_round);
         }
     }
-    return p;
-}
-
-// Wave groups per workgroup (a power of two dividing the 16 waves): enough
-// groups that one round covers every row tile (fewer rounds, fewer barriers;
-// each wave then streams several units of its row tile), and at least as many
-// as keep every wave busy with one unit.
-int groups_for(int U, int RT, int G) {
-    int r = 1;
-    while (r < kWPB && U * r * 2 <= kWPB) r *= 2;
-    while (r < kWPB && (long)G * r < RT) r *= 2;
-    return r;
+    return found;
 }
 
 int launch_chunk(const ExecOp* ops, int nops, bool tiled, int m0, int M, hipStream_t s) {
-    const int P = prefetch_depth();
     ExecArgs a{};
     a.nops = nops;
     size_t xs_bytes = 0;
@@ -620,7 +574,6 @@ int launch_chunk(const ExecOp* ops, int nops, bool tiled, int m0, int M, hipStre
         d.nss = tg.nss;
         d.ng_last = tg.ng_last;
         d.RT = RT;
-        d.U = tg.nss * (L.glu ? 2 : 1);
         d.act = L.act;
         d.glu = L.glu ? 1 : 0;
         d.xb = L.Xb != nullptr;
@@ -630,36 +583,26 @@ int launch_chunk(const ExecOp* ops, int nops, bool tiled, int m0, int M, hipStre
         xs_bytes = std::max(xs_bytes, (size_t)tg.nss * 1024 * d.R);
     }
     a.last_wait = -1;
-    a.flags = getenv("ALV_EXEC_FLAGS") ? atoi(getenv("ALV_EXEC_FLAGS")) : 0;
     for (int o = 0; o < nops; ++o)
         if (a.op[o].dep >= 0) {
             a.op[a.op[o].dep].signal = 1;
             a.last_wait = o;
         }
     const size_t lds = xs_bytes + kScratchBytes;
-    const int per_cu = tiled ? (P == 1 ? occupancy<1, true>(lds) : occupancy<2, true>(lds))
-                             : (P == 1 ? occupancy<1, false>(lds) : occupancy<2, false>(lds));
+    const int per_cu = tiled ? occupancy<true>(lds) : occupancy<false>(lds);
     if (per_cu < 1) return fail(ALV_ERR_HIP, "the executor kernel does not fit a CU with %zu bytes of LDS", lds);
     // Every workgroup of a chain must be resident at once (its waits rely on it).
     const int G = per_cu * dev_info().cus;
-    for (int o = 0; o < nops; ++o) {
-        OpDesc& d = a.op[o];
-        d.r = groups_for(d.U, d.RT, G);
-        const int gw = kWPB / d.r;
-        d.gw_shift = __builtin_ctz(gw);
-        d.numax = (d.U + gw - 1) / gw;
-        d.wstride = G * d.r;
-        d.nr_full = d.RT / d.wstride;
-        d.nr_rem = d.RT % d.wstride;
-    }
+    for (int o = 0; o < nops; ++o)
+        if (!plan_op(a.op[o], G))
+            return fail(ALV_ERR_RANGE, "op %d: K=%d is beyond what the executor splits over one workgroup", o, a.op[o].K);
     Workspace ws;
     if (int rc = get_workspace(s, kSyncWords, &ws)) return rc;
     a.sync = ws.counters;
     a.xs_bytes = (uint32_t)xs_bytes;
     // Waits poll with s_sleep; 2^24 polls is far beyond any chain's run time.
     a.spin_limit = any_dep ? (1u << 24) : 0u;
-    const hipError_t e = tiled ? (P == 1 ? launch_one<1, true>(a, G, lds, s) : launch_one<2, true>(a, G, lds, s))
-                               : (P == 1 ? launch_one<1, false>(a, G, lds, s) : launch_one<2, false>(a, G, lds, s));
+    const hipError_t e = tiled ? launch_one<true>(a, G, lds, s) : launch_one<false>(a, G, lds, s);
     return hip_check(e, "q4_exec_kernel launch");
 }
 

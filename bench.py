@@ -258,6 +258,25 @@ def main() -> int:
     gu_us = breakdown["ffn_gate_up"]["us"]
     gu_gbs = lb["ffn_gate_up"] / (gu_us * 1e-6) / 1e9
 
+    # Small-M decode against the 12B-class FFN (M tokens share one weight
+    # read) and prefill at M = 512 (MFMA tiled kernel, GeGLU fused): per call
+    # over distinct layers.
+    extra = {"small_m_ffn": {}, "prefill_ffn_m512": None}
+    for M in (2, 4, 8, 16):
+        xm = torch.randn(M * H, device=dev)
+        ym = torch.empty(M * H, device=dev)
+        us = graph_us(torch, lambda: [ffn(xm, ym, M=M) for _, _, ffn in layers], 2, nl)
+        byts = 3 * q4_bytes(I_FF, H) + M * (4 * H + 4 * H)
+        extra["small_m_ffn"][str(M)] = {"us": round(us, 3), "GBps": round(byts / us / 1e3, 1)}
+    Mp = 512
+    xp = torch.randn(Mp * H, device=dev)
+    yp = torch.empty(Mp * H, device=dev)
+    npf = min(nl, 8)
+    us = graph_us(torch, lambda: [ffn(xp, yp, M=Mp) for _, _, ffn in layers[:npf]], 2, npf)
+    flops = 2.0 * Mp * 3 * I_FF * H
+    extra["prefill_ffn_m512"] = {"us": round(us, 2), "TFLOPs": round(flops / us / 1e6, 1),
+                                 "mfma_frac_bf16_dense": round(flops / us / 1e6 / 2500.0, 4)}
+
     from alveare_amd import profiling
 
     out = {
@@ -296,6 +315,7 @@ def main() -> int:
             "avg_launch_us": gu_us,
         },
         "cpu_baseline": None,
+        "extra_configs": extra,
     }
     if not args.no_cpu_baseline:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)

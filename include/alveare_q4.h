@@ -25,11 +25,11 @@
  *    dense fp32, row-major, with the given leading dimensions (in elements).
  *  - Calls on different streams may run concurrently; calls that share an FFN
  *    handle must be serialised on one stream (the handle owns its scratch).
- *  - Shapes whose K is split across workgroups use a split-K workspace the
- *    library keeps per (device, stream). It grows on first need (that growth
- *    synchronises the device), so a stream that will be captured into a HIP
- *    graph must run the same calls once before capture; growth during capture
- *    fails with ALV_ERR_ARG.
+ *  - Chained ops synchronise through words the library keeps per (device,
+ *    stream). A device's words are allocated at the first call that needs
+ *    them (synchronising the device); if that first call happens during HIP
+ *    graph capture it fails with ALV_ERR_ARG, so run one call on the device
+ *    before capturing. Up to 64 streams per device use them.
  */
 #ifndef ALVEARE_Q4_H
 #define ALVEARE_Q4_H
