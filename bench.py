@@ -269,7 +269,9 @@ def main() -> int:
         byts = 3 * q4_bytes(I_FF, H) + M * (4 * H + 4 * H)
         extra["small_m_ffn"][str(M)] = {"us": round(us, 3), "GBps": round(byts / us / 1e3, 1)}
     Mp = 512
-    xp = torch.randn(Mp * H, device=dev)
+    # bf16-valued activations, as the reference's prefill passes them (x_bf16):
+    # one activation term per token tile.
+    xp = torch.randn(Mp * H, device=dev).bfloat16().float()
     yp = torch.empty(Mp * H, device=dev)
     npf = min(nl, 8)
     us = graph_us(torch, lambda: [ffn(xp, yp, M=Mp) for _, _, ffn in layers[:npf]], 2, npf)

@@ -314,14 +314,21 @@ def test_chain_long_and_repeated_ffn(orc, dev, chain_mode):
                                           (8, 3840, 15360, False), (16, 3840, 3840, False),
                                           (19, 1000, 1152, False), (32, 512, 1024, False),
                                           (64, 2048, 3840, True), (100, 777, 2048, False),
-                                          (512, 1024, 3840, True)])
+                                          (512, 1024, 3840, True), (300, 640, 1024, "mixed"),
+                                          (257, 384, 15360, False)])
 def test_gemm_parity(orc, dev, M, N, K, bf16x):
     import alveare_amd as aa
 
     _say(f"gemm M={M} N={N} K={K} bf16x={bf16x}")
     W = orc.synth_q4(N, K, 1000 + M)
     X = orc.synth_normal(M * K, 2000 + M).reshape(M, K)
-    if bf16x:
+    if bf16x == "mixed":
+        # First 256-token tile fp32-valued except its first row, the second
+        # bf16-valued: each tile takes its own number of activation terms.
+        X = X.copy()
+        X[256:] = orc.bf16_round(X[256:]).reshape(M - 256, K)
+        X[0] = orc.bf16_round(X[0])
+    elif bf16x:
         X = orc.bf16_round(X).reshape(M, K)
     Y = torch.empty((M, N), dtype=torch.float32, device=dev)
     aa.gemm_q(to_dev(W, dev), to_dev(X, dev), Y, B=M, N=N, K=K)
