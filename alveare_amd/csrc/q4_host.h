@@ -101,6 +101,12 @@ int exec_chain(const ExecOp* ops, int nops, bool tiled, hipStream_t s);
 // Report (and clear) a timed-out chain wait on stream `s` (synchronises it).
 int check_async(hipStream_t s);
 
+// ---- single-token streaming GEMV (gemv1_q.hip) -------------------------------------
+// L with M = 1 on registered weights whose activations and unit slots fit the
+// LDS (gemv1_ok) as one launch of the single-token kernel.
+bool gemv1_ok(const GemvLaunch& L);
+int launch_gemv1(const GemvLaunch& L, hipStream_t s);
+
 // Repack W (combined layout, N x K) into the tiled layout at `out`
 // (tile_bytes(N, K) bytes), on `s` (tile_q.hip).
 int launch_tile(const uint8_t* W, uint8_t* out, int N, int K, hipStream_t s);

@@ -13,7 +13,7 @@ weights and activations are resident in HBM before the timed region starts.
 Prints ONE JSON line. `value` is achieved HBM GB/s of algorithmic bytes
 (20 B per 32 weights plus activations in and out, once) over the whole step.
 `roofline` is the dominant kernel -- the FFN's gate/up launch (GLU epilogue),
-a third of the time of a layer -- timed with HIP events on its stream over a
+over 40 % of the time of a layer -- timed with HIP events on its stream over a
 graph of its 48 launches; `traffic` is its HBM bytes per launch from the
 committed FETCH_SIZE / WRITE_SIZE profile. `cpu_baseline` times the oracle's
 restatement of the reference CPU path (per call: dequantize to fp32, fp32
@@ -51,9 +51,9 @@ def layer_bytes() -> dict:
     return {k: w[k] + act[k] for k in w}
 
 
-ROOFLINE_KERNEL = "q4_oneshot_kernel<2, 3, true, false, true>"  # gate/up, one fp32 token, tiled weights
+ROOFLINE_KERNEL = "q4_gemv1_kernel<16, 1, 3, true>"  # gate/up + GLU, one fp32 token, registered weights
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                            "q4_oneshot_traffic_gemma12b_decode.txt")
+                            "q4_gemv1_traffic_gemma12b_decode.txt")
 CALIBRATION_BYTES = 256 << 20
 
 

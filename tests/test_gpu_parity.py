@@ -54,6 +54,36 @@ def test_dequant_exhaustive_scales(orc, dev):
     assert np.array_equal(got[dom], want[dom])
 
 
+def test_single_token_dequant_exact_scales(orc, dev):
+    """The single-token streaming kernel dequantizes with its own instruction
+    sequence (q4_device.h::dequant8_mix): a one-hot x selects a dequantized
+    column exactly, so every (code, scale) pair of its domain |s| < 2^112 --
+    all 16 codes in both nibble positions, every such bf16 scale, subnormal
+    ones included -- must match the oracle's dequant bit for bit."""
+    import alveare_amd as aa
+
+    _say("single-token dequant: one-hot GEMV over all bf16 scales with |s| < 2^112")
+    s = np.arange(65536, dtype=np.uint32)
+    exp_field = (s >> 7) & 0xFF
+    s = s[exp_field <= 127 + 111]
+    N, K = len(s), 32
+    W = np.zeros((N, 20), np.uint8)
+    lo = np.arange(16, dtype=np.uint8)
+    W[:, :16] = lo | ((15 - lo) << 4)
+    W[:, 16], W[:, 17] = s & 0xFF, s >> 8
+    want = parity.bf16_f32(orc.dequant_q4(W, N, K).reshape(N, K))
+    w = aa.Q4Weight(to_dev(W, dev), N, K)
+    for k in range(K):
+        x = np.zeros(K, np.float32)
+        x[k] = 1.0
+        y = w(to_dev(x, dev))
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        # -0.0 vs +0.0 of an exactly zero product is not distinguished.
+        assert np.array_equal(got, want[:, k]), f"column {k}"
+    w.close()
+
+
 def test_dequant_random_matches_oracle(orc, dev):
     import alveare_amd as aa
 
