@@ -101,9 +101,10 @@ int exec_chain(const ExecOp* ops, int nops, bool tiled, hipStream_t s);
 // Report (and clear) a timed-out chain wait on stream `s` (synchronises it).
 int check_async(hipStream_t s);
 
-// ---- single-token streaming GEMV (gemv1_q.hip) -------------------------------------
-// L with M = 1 on registered weights whose activations and unit slots fit the
-// LDS (gemv1_ok) as one launch of the single-token kernel.
+// ---- streaming GEMV for few tokens (gemv1_q.hip) -----------------------------------
+// L on registered weights as launches of the streaming kernel, up to four
+// tokens each; gemv1_ok: the shape's activations and unit slots fit the LDS
+// for one token at least.
 bool gemv1_ok(const GemvLaunch& L);
 int launch_gemv1(const GemvLaunch& L, hipStream_t s);
 
