@@ -28,15 +28,17 @@ int hip_check(hipError_t e, const char* what) {
 }
 
 namespace {
-// Synchronisation words: one block per device holding kWsStreams sets, handed
-// out to streams on first use. The block is allocated (and zeroed) at the
-// first call on the device; a stream's later first use takes a set without
-// allocating, so it may happen during graph capture.
+// Synchronisation words (and split-K scratch): one block per device holding
+// kWsStreams sets, handed out to streams on first use. The blocks are
+// allocated (the words zeroed) at the first call on the device; a stream's
+// later first use takes a set without allocating, so it may happen during
+// graph capture.
 constexpr int kWsStreams = 64;
 std::mutex g_ws_mu;
 struct DeviceWs {
     uint32_t* block = nullptr;
     size_t words = 0;  // per set
+    uint8_t* part = nullptr;  // kPartBytes per set
     std::map<hipStream_t, int> slot;
 };
 std::map<int, DeviceWs> g_ws;
@@ -54,10 +56,17 @@ int get_workspace(hipStream_t s, size_t counters, Workspace* out) {
             return fail(ALV_ERR_ARG,
                         "the synchronisation words of this device are allocated on its first call, which cannot "
                         "happen during graph capture: run one call on this device before capturing");
-        const size_t words = counters > (size_t)kSyncWords ? counters : (size_t)kSyncWords;
+        const size_t all = (size_t)kSyncWords + kSplitCounters;
+        const size_t words = counters > all ? counters : all;
         if (hipMalloc(&w.block, words * kWsStreams * sizeof(uint32_t)) != hipSuccess) {
             w.block = nullptr;
             return fail(ALV_ERR_HIP, "hipMalloc of the synchronisation words failed");
+        }
+        if (hipMalloc(&w.part, kPartBytes * kWsStreams) != hipSuccess) {
+            (void)hipFree(w.block);
+            w.block = nullptr;
+            w.part = nullptr;
+            return fail(ALV_ERR_HIP, "hipMalloc of the split-K scratch failed");
         }
         if (int rc = hip_check(hipMemset(w.block, 0, words * kWsStreams * sizeof(uint32_t)), "hipMemset")) return rc;
         w.words = words;
@@ -75,6 +84,7 @@ int get_workspace(hipStream_t s, size_t counters, Workspace* out) {
     }
     out->counters = w.block + (size_t)idx * w.words;
     out->counter_count = w.words;
+    out->part = reinterpret_cast<float*>(w.part + (size_t)idx * kPartBytes);
     return ALV_OK;
 }
 

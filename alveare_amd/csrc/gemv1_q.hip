@@ -41,28 +41,25 @@ namespace {
 struct Gemv1Args {
     const uint8_t* W0;
     const uint8_t* W1;  // up matrix of a GLU pair
-    const void* X;      // fp32 (R = 3) or bf16 (R = 1) activations, token m at m * ldx
+    const void* X;      // fp32 or bf16 activations, token m at m * ldx
     float* Y;           // fp32 output, or
     uint16_t* Yb;       // bf16 output (bit patterns); token m at m * ldy
+    float* part;        // split-K partial sums, [row][ks][token][matrix] (ks > 1)
+    uint32_t* cnt;      // split-K arrivals per tile group (zero between launches)
     uint32_t wbytes;    // bytes of one matrix (row tiles x rtb)
     uint32_t rtb;       // bytes per row tile
-    uint32_t xbytes;    // activation buffer range
+    uint32_t xbytes;    // activation buffer range (M tokens)
     int N, K, nss, ng_last;
-    int ldx, ldy;
-    int rt_q, rt_r;  // workgroup b owns rt_q + (b < rt_r) row tiles
+    int ldx, ldy, M;
+    int rt_q, rt_r;  // tile group t owns rt_q + (t < rt_r) row tiles
+    int ks;          // K splits: workgroup b is tile group b / ks, super-step range b % ks
     int act;
 };
 
 constexpr int kXO = 4;  // activation octets per thread and staging round
 
-// Row tiles [rt0, rt0 + nt) of workgroup b.
-__device__ __forceinline__ void wg_tiles(const Gemv1Args& a, int b, int& rt0, int& nt) {
-    rt0 = b * a.rt_q + min(b, a.rt_r);
-    nt = a.rt_q + (b < a.rt_r ? 1 : 0);
-}
-
-// Eight activations of one token as R bf16 terms at dst, dst + 8, dst + 16
-// (R = 3: the exact split of fp32 values; R = 1: bf16 values as they are).
+// Eight activations of one token as R bf16 terms at dst, dst + 8, ...: R = 3
+// is the exact split of fp32 values, R = 1 bf16 values as they are.
 template <int R>
 __device__ __forceinline__ void stage_octet(const u32x4 (&v)[2], __bf16* dst) {
     if constexpr (R == 1) {
@@ -87,22 +84,38 @@ __device__ __forceinline__ void stage_octet(const u32x4 (&v)[2], __bf16* dst) {
     }
 }
 
+// The work of workgroup b: row tiles [rt0, rt0 + nt) x super-steps [s0, s0 + nsw).
+struct WgWork {
+    int tg, kq, rt0, nt, s0, nsw;
+};
+
+__device__ __forceinline__ WgWork wg_work(const Gemv1Args& a, int b) {
+    WgWork w;
+    w.tg = b / a.ks;
+    w.kq = b - w.tg * a.ks;
+    w.rt0 = w.tg * a.rt_q + min(w.tg, a.rt_r);
+    w.nt = a.rt_q + (w.tg < a.rt_r ? 1 : 0);
+    w.s0 = w.kq * a.nss / a.ks;
+    w.nsw = (w.kq + 1) * a.nss / a.ks - w.s0;
+    return w;
+}
+
 // Byte offset of unit u's tile in its matrix, the plane step of its pieces,
-// its super-step and matrix index. Units of a workgroup: ((tl * nss) + ss) * NT + n.
-template <int NT>
+// its super-step (absolute) and matrix index. Units of a workgroup:
+// ((tl * nsw) + ss - s0) * NT + n.
 struct UnitPos {
     uint32_t off, step;
     int ss, n;
 };
 
 template <int NT>
-__device__ __forceinline__ UnitPos<NT> unit_pos(const Gemv1Args& a, int rt0, int u) {
-    UnitPos<NT> p;
+__device__ __forceinline__ UnitPos unit_pos(const Gemv1Args& a, const WgWork& wk, int u) {
+    UnitPos p;
     const int t = NT == 2 ? u >> 1 : u;
     p.n = NT == 2 ? u & 1 : 0;
-    const int tl = t / a.nss;
-    p.ss = t - tl * a.nss;
-    p.off = (uint32_t)(rt0 + tl) * a.rtb + (uint32_t)p.ss * 5120u;
+    const int tl = t / wk.nsw;
+    p.ss = wk.s0 + t - tl * wk.nsw;
+    p.off = (uint32_t)(wk.rt0 + tl) * a.rtb + (uint32_t)p.ss * 5120u;
     p.step = p.ss == a.nss - 1 ? 256u * (uint32_t)a.ng_last : 1024u;
     return p;
 }
@@ -115,24 +128,24 @@ struct ARows {
     static constexpr int DL = 16 * ((RM + 3) / 4);
 };
 
-template <int NW, int P, int R, bool GLU, int MT>
+template <int NW, int P, int R, bool XB, bool GLU, int MT>
 __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     constexpr int NT = GLU ? 2 : 1;
-    constexpr int ES = R == 3 ? 4 : 2;  // activation element size
+    constexpr int ES = XB ? 2 : 4;  // activation element size
     constexpr int RM = ARows<R, MT>::RM, DL = ARows<R, MT>::DL;
     static_assert(RM <= 16, "one MFMA row block");
+    static_assert(!XB || R == 1, "bf16 activations take one term");
     extern __shared__ __align__(16) unsigned char smem[];
-    __bf16* xs = reinterpret_cast<__bf16*>(smem);
-    f32x4* part = reinterpret_cast<f32x4*>(smem + (size_t)a.nss * 1024 * RM);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 15;
     const int g = lane >> 4;
-    int rt0, nt;
-    wg_tiles(a, blockIdx.x, rt0, nt);
-    const int U = nt * a.nss * NT;
+    const WgWork wk = wg_work(a, blockIdx.x);
+    const int U = wk.nt * wk.nsw * NT;
+    __bf16* xs = reinterpret_cast<__bf16*>(smem);
+    f32x4* part = reinterpret_cast<f32x4*>(smem + (size_t)wk.nsw * 1024 * RM);
     // Unit counter of the workgroup, after the unit slots: the first P * NW
     // units go to the waves statically, the rest to whichever wave frees a ring
     // slot first, so a wave whose loads come back late does fewer units.
@@ -141,10 +154,11 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
 
     // ---- 1. stage the activation terms before any weight load --------------------
     // Octet o (8 consecutive k) of token m sits at operand slot
-    // ((o / 64) * 16 + o % 16) * 4 + (o / 16) % 4 -- super-step o / 64, block
-    // 4 g + bl with g = (o / 16) % 4, bl = (o / 4) % 4, dword t = o % 4 of the
-    // block -- rows m * R .. m * R + R - 1 of the slot's RM rows.
-    const int octs = a.nss * 64;
+    // ((o / 64 - s0) * 16 + o % 16) * 4 + (o / 16) % 4 -- super-step o / 64,
+    // block 4 g + bl with g = (o / 16) % 4, bl = (o / 4) % 4, dword t = o % 4
+    // of the block -- rows m * R .. m * R + R - 1 of the slot's RM rows.
+    // Tokens past M (a launch's last group) read zeros.
+    const int octs = wk.nsw * 64;
     const int E = MT * octs;
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.X, a.xbytes);
     for (int e0 = 0; e0 < E; e0 += kXO * 64 * NW) {
@@ -153,16 +167,17 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
         for (int i = 0; i < kXO; ++i) {
             const int e = e0 + tid + i * 64 * NW;
             const int m = MT == 1 ? 0 : e / octs;
-            const int o = e - m * octs;
-            const uint32_t off = e < E && o * 8 < a.K ? (uint32_t)((m * a.ldx + o * 8) * ES) : a.xbytes;  // past: zeros
+            const int k = (wk.s0 * 64 + e - m * octs) * 8;
+            const uint32_t off =
+                e < E && m < a.M && k < a.K ? (uint32_t)((m * a.ldx + k) * ES) : a.xbytes;  // past: zeros
             xr[i][0] = buf_load16(rx, off);
-            xr[i][1] = R == 3 ? buf_load16(rx, off + 16) : u32x4{0u, 0u, 0u, 0u};
+            xr[i][1] = XB ? u32x4{0u, 0u, 0u, 0u} : buf_load16(rx, off + 16);
         }
 #pragma unroll
         for (int i = 0; i < kXO; ++i) {
             const int e = e0 + tid + i * 64 * NW;
             const int m = MT == 1 ? 0 : e / octs;
-            const int o = e - m * octs;
+            const int o = e - m * octs;  // relative to super-step s0
             if (e < E) {
                 const int slot = ((o >> 6) * 16 + (o & 15)) * 4 + ((o >> 4) & 3);
                 stage_octet<R>(xr[i], xs + ((size_t)slot * RM + m * R) * 8);
@@ -180,7 +195,7 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
         uint32_t off = a.wbytes, step = 1024u;  // past the range: zeros, no memory traffic
         int n = 0;
         if (u < U) {
-            const UnitPos<NT> p = unit_pos<NT>(a, rt0, u);
+            const UnitPos p = unit_pos<NT>(a, wk, u);
             off = p.off;
             step = p.step;
             n = p.n;
@@ -216,11 +231,11 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
             un = __builtin_amdgcn_readfirstlane(un);
             const int u = uk[k];
             if (u < U) {
-                const UnitPos<NT> p = unit_pos<NT>(a, rt0, u);
+                const UnitPos p = unit_pos<NT>(a, wk, u);
                 // The last super-step holds ng_last lanes of g per row; the
                 // other lanes read the next plane's bytes: zero their scales.
                 const bool valid = p.ss != a.nss - 1 || g < a.ng_last;
-                const __bf16* xu = xa + (size_t)p.ss * 16 * 4 * RM * 8;
+                const __bf16* xu = xa + (size_t)(p.ss - wk.s0) * 16 * 4 * RM * 8;
                 f32x4 t0 = {0.f, 0.f, 0.f, 0.f}, t1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int bl = 0; bl < 4; ++bl) {
@@ -247,16 +262,17 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     }
     lds_barrier();
 
-    // ---- 4. per row: sum the unit slots in a fixed order, epilogue, store ----------
+    // ---- 4. per row: sum the unit slots in a fixed order ---------------------------
     // D row m * R + p (token m, term p) of column jj sits in slot lane
     // 16 * (row / 4) + jj, element row % 4. Wave w takes rows 16 w .. 16 w + 15
     // of the workgroup (then 16 NW further on); four lanes share a row: lane c
-    // sums super-steps c, c + 4, ... in ascending order, the four partial sums
-    // combine in a fixed butterfly, so the result does not depend on timing,
-    // and lane 0 of the four finishes the row -- the epilogue is spread over
-    // nt waves.
+    // sums super-steps c, c + 4, ... in ascending order and the four partial
+    // sums combine in a fixed butterfly, so the result does not depend on
+    // timing; lane 0 of the four finishes the row -- the epilogue is spread
+    // over nt waves.
     const int c = lane & 3;
-    for (int r0 = w * 16; r0 < nt * 16; r0 += NW * 16) {
+    const bool split = a.ks > 1;
+    for (int r0 = w * 16; r0 < wk.nt * 16; r0 += NW * 16) {
         const int rid = r0 + (lane >> 2);
         const int tl = rid >> 4, jj = rid & 15;
         float y[MT][NT];
@@ -264,10 +280,10 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
         for (int m = 0; m < MT; ++m)
 #pragma unroll
             for (int n = 0; n < NT; ++n) y[m][n] = 0.0f;
-        for (int ss = c; ss < a.nss; ss += 4) {
+        for (int ss = c; ss < wk.nsw; ss += 4) {
 #pragma unroll
             for (int n = 0; n < NT; ++n) {
-                const f32x4* sl = part + ((size_t)(tl * a.nss + ss) * NT + n) * DL + jj;
+                const f32x4* sl = part + ((size_t)(tl * wk.nsw + ss) * NT + n) * DL + jj;
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
                     float v = 0.0f;
@@ -287,10 +303,21 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
                 y[m][n] += __shfl_xor(y[m][n], 1);
                 y[m][n] += __shfl_xor(y[m][n], 2);
             }
-        const int row = (rt0 + tl) * 16 + jj;
-        if (c != 0 || row >= a.N) continue;
+        const int row = (wk.rt0 + tl) * 16 + jj;
+        if (row >= a.N) continue;
+        // Lane c of the four finishes tokens c, c + 4, ... (each holds every sum).
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
+            if ((m & 3) != c || m >= a.M) continue;
+            if (split) {
+                // This workgroup's share of K, written through for the last of
+                // the ks workgroups of the tile group to add up.
+                float* dst = a.part + (((size_t)row * a.ks + wk.kq) * MT + m) * NT;
+#pragma unroll
+                for (int n = 0; n < NT; ++n)
+                    __hip_atomic_store(dst + n, y[m][n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                continue;
+            }
             float out = y[m][0];
             if constexpr (GLU) out = bf16_round(glu_act(bf16_round(y[m][0]), bf16_round(y[m][NT - 1]), a.act));
             if (a.Yb)
@@ -299,6 +326,43 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
                 a.Y[(size_t)m * a.ldy + row] = out;
         }
     }
+    if (!split) return;
+
+    // ---- 5. split K: the last workgroup of the tile group adds the shares ---------
+    // The shares land before the workgroup counts itself in; the workgroup
+    // that brings the count to ks reads all of them (sc1, past this XCD's L2)
+    // and sums them in split order, so the result does not depend on which
+    // workgroup came last; it then clears the count for the next launch.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(&a.cnt[wk.tg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *next = old == (uint32_t)(a.ks - 1) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!*next) return;
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.part, kPartBytes);
+    for (int i = tid; i < wk.nt * 16 * MT; i += 64 * NW) {  // one (row, token) per thread
+        const int r = i / MT, m = i - r * MT;
+        const int row = wk.rt0 * 16 + r;
+        if (row >= a.N || m >= a.M) continue;
+        const uint32_t base = (uint32_t)((((size_t)row * a.ks) * MT + m) * NT * sizeof(float));
+        float y[NT];
+#pragma unroll
+        for (int n = 0; n < NT; ++n) y[n] = 0.0f;
+#pragma unroll 4
+        for (int kq = 0; kq < a.ks; ++kq)
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+                y[n] += __builtin_bit_cast(float, buf_load4_sc1(rp, base + (uint32_t)(((size_t)kq * MT * NT + n) * 4)));
+        float out = y[0];
+        if constexpr (GLU) out = bf16_round(glu_act(bf16_round(y[0]), bf16_round(y[NT - 1]), a.act));
+        if (a.Yb)
+            a.Yb[(size_t)m * a.ldy + row] = __builtin_bit_cast(uint16_t, (__bf16)out);
+        else
+            a.Y[(size_t)m * a.ldy + row] = out;
+    }
+    if (tid == 0) __hip_atomic_store(&a.cnt[wk.tg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 struct DevInfo {
@@ -323,9 +387,9 @@ const DevInfo& dev_info() {
 
 constexpr int kNW = 16;
 
-template <int P, int R, bool GLU, int MT>
+template <int P, int R, bool XB, bool GLU, int MT>
 hipError_t launch_k(const Gemv1Args& a, int groups, size_t lds, hipStream_t s) {
-    auto k = q4_gemv1_kernel<kNW, P, R, GLU, MT>;
+    auto k = q4_gemv1_kernel<kNW, P, R, XB, GLU, MT>;
     if (lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -338,75 +402,127 @@ hipError_t launch_k(const Gemv1Args& a, int groups, size_t lds, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int P, int R, bool GLU>
-hipError_t launch_mt(const Gemv1Args& a, int mt, int groups, size_t lds, hipStream_t s) {
-    switch (mt) {
-        case 1: return launch_k<P, R, GLU, 1>(a, groups, lds, s);
-        case 2: return launch_k<P, R, GLU, 2>(a, groups, lds, s);
-        case 3: return launch_k<P, R, GLU, 3>(a, groups, lds, s);
-        default: return launch_k<P, R, GLU, 4>(a, groups, lds, s);
+// Ring depth: one unit in flight per wave (16 per CU) measures faster than two
+// on every decode shape -- a deeper ring only lengthens the memory queues.
+constexpr int kP = 1;
+
+// Token capacity of a launch and activation terms per token: fp32
+// activations take the exact three-term split, up to 5 tokens (15 A rows);
+// bf16 activations one term, up to 16 tokens.
+struct Shape {
+    int mt, r;
+};
+
+Shape shape_for(const GemvLaunch& L, int m) {
+    if (L.Xb) {
+        int mt = 1;
+        while (mt < m && mt < 16) mt *= 2;
+        return {mt, 1};
+    }
+    if (m <= 2) return {m, 3};
+    if (m <= 4) return {4, 3};
+    return {5, 3};
+}
+
+hipError_t launch_shape(const Gemv1Args& a, const GemvLaunch& L, Shape sh, int groups, size_t lds, hipStream_t s) {
+    if (L.Xb) {
+        switch (sh.mt) {
+            case 1: return launch_k<kP, 1, true, false, 1>(a, groups, lds, s);
+            case 2: return launch_k<kP, 1, true, false, 2>(a, groups, lds, s);
+            case 4: return launch_k<kP, 1, true, false, 4>(a, groups, lds, s);
+            case 8: return launch_k<kP, 1, true, false, 8>(a, groups, lds, s);
+            default: return launch_k<kP, 1, true, false, 16>(a, groups, lds, s);
+        }
+    }
+    if (L.glu) {
+        switch (sh.mt) {
+            case 1: return launch_k<kP, 3, false, true, 1>(a, groups, lds, s);
+            case 2: return launch_k<kP, 3, false, true, 2>(a, groups, lds, s);
+            case 4: return launch_k<kP, 3, false, true, 4>(a, groups, lds, s);
+            default: return launch_k<kP, 3, false, true, 5>(a, groups, lds, s);
+        }
+    }
+    switch (sh.mt) {
+        case 1: return launch_k<kP, 3, false, false, 1>(a, groups, lds, s);
+        case 2: return launch_k<kP, 3, false, false, 2>(a, groups, lds, s);
+        case 4: return launch_k<kP, 3, false, false, 4>(a, groups, lds, s);
+        default: return launch_k<kP, 3, false, false, 5>(a, groups, lds, s);
     }
 }
 
 struct Gemv1Plan {
-    int groups, rt_q, rt_r;
+    Shape sh;
+    int tg, rt_q, rt_r, ks;
     size_t lds;
 };
 
-// Ring depth: one unit in flight per wave (16 per CU) measures faster than two
-// on every decode shape -- a deeper ring only lengthens the memory queues.
-constexpr int kP = 1;
-// Tokens per launch: the activations of all of them sit in LDS with the unit
-// slots, which bounds the count (4 at the 12B-class shapes).
-constexpr int kMaxMT = 4;
-
-bool plan_gemv1(const GemvLaunch& L, int mt, Gemv1Plan* out) {
-    if (!L.tiled || L.parts != (L.Xb ? 1 : 3) || mt < 1 || mt > kMaxMT) return false;
+// K splits (1, 2, 4, ... up to 16 and the super-step count) until the
+// workgroup's activations and unit slots fit the LDS and the split's partial
+// sums fit their scratch. One split when it fits: no partial sums at all.
+bool plan_gemv1(const GemvLaunch& L, int m, Gemv1Plan* out) {
+    if (!L.tiled || L.parts != (L.Xb ? 1 : 3) || m < 1) return false;
     const DevInfo& d = dev_info();
     const TileGeom tg = tile_geom(L.K);
     const int RT = (L.N + 15) / 16;
     const int NT = L.glu ? 2 : 1;
-    const int RM = L.parts * mt;
     Gemv1Plan p;
-    p.groups = std::min(RT, d.cus);
-    p.rt_q = RT / p.groups;
-    p.rt_r = RT % p.groups;
-    const int tiles = p.rt_q + (p.rt_r ? 1 : 0);
-    const int units = tiles * tg.nss * NT;
-    p.lds = (size_t)tg.nss * 1024 * RM + (size_t)units * 256 * ((RM + 3) / 4) + 16;
-    if (p.lds > d.lds) return false;
-    *out = p;
-    return true;
+    p.sh = shape_for(L, m);
+    const int RM = p.sh.mt * p.sh.r;
+    for (p.ks = 1; p.ks <= 16 && p.ks <= tg.nss; p.ks *= 2) {
+        p.tg = std::min(RT, std::max(1, d.cus / p.ks));
+        p.rt_q = RT / p.tg;
+        p.rt_r = RT % p.tg;
+        const int tiles = p.rt_q + (p.rt_r ? 1 : 0);
+        const int nsw = (tg.nss + p.ks - 1) / p.ks;
+        const int units = tiles * nsw * NT;
+        p.lds = (size_t)nsw * 1024 * RM + (size_t)units * 256 * ((RM + 3) / 4) + 16;
+        const size_t part = p.ks > 1 ? (size_t)RT * 16 * p.ks * p.sh.mt * NT * sizeof(float) : 0;
+        if (p.lds <= d.lds && part <= kPartBytes && (p.ks == 1 || p.tg <= kSplitCounters)) {
+            *out = p;
+            return true;
+        }
+    }
+    return false;
 }
 
-// Most tokens one launch takes for this shape (0: none).
-int max_mt(const GemvLaunch& L) {
+// Most tokens one launch takes (0: the shape has no plan).
+int max_tokens(const GemvLaunch& L) {
     Gemv1Plan p;
-    for (int mt = kMaxMT; mt >= 1; --mt)
-        if (plan_gemv1(L, mt, &p)) return mt;
+    for (int m : {16, 8, 5, 4, 2, 1})
+        if (m <= (L.Xb ? 16 : 5) && plan_gemv1(L, m, &p)) return m;
     return 0;
 }
 
 }  // namespace
 
-bool gemv1_ok(const GemvLaunch& L) { return L.M >= 1 && max_mt(L) > 0; }
+bool gemv1_ok(const GemvLaunch& L) { return L.M >= 1 && max_tokens(L) > 0; }
 
 int launch_gemv1(const GemvLaunch& L, hipStream_t s) {
-    const int mtmax = L.M >= 1 ? max_mt(L) : 0;
-    if (!mtmax) return fail(ALV_ERR_ARG, "streaming GEMV: shape M=%d N=%d K=%d outside its plan", L.M, L.N, L.K);
+    const int mmax = L.M >= 1 ? max_tokens(L) : 0;
+    if (!mmax) return fail(ALV_ERR_ARG, "streaming GEMV: shape M=%d N=%d K=%d outside its plan", L.M, L.N, L.K);
     const TileGeom tg = tile_geom(L.K);
     const int RT = (L.N + 15) / 16;
     const uint64_t wbytes = (uint64_t)RT * tg.rtb;
     if (wbytes >= 0xFFFFE000ull)
         return fail(ALV_ERR_RANGE, "weight matrix of %llu bytes exceeds the 4 GiB buffer range", (unsigned long long)wbytes);
     const int ES = L.Xb ? 2 : 4;
-    for (int m0 = 0; m0 < L.M; m0 += mtmax) {
-        const int mt = std::min(mtmax, L.M - m0);
+    // Groups of as equal a size as the capacity allows (16 tokens at a
+    // capacity of 5: four groups of 4, not 5 + 5 + 5 + 1).
+    const int ngroups = (L.M + mmax - 1) / mmax;
+    const int gsize = (L.M + ngroups - 1) / ngroups;
+    for (int m0 = 0; m0 < L.M; m0 += gsize) {
+        const int m = std::min(gsize, L.M - m0);
         Gemv1Plan p;
-        if (!plan_gemv1(L, mt, &p)) return fail(ALV_ERR_ARG, "streaming GEMV: no plan for %d tokens", mt);
-        const uint64_t xbytes = ((uint64_t)(mt - 1) * L.ldx + L.K) * ES;
+        if (!plan_gemv1(L, m, &p)) return fail(ALV_ERR_ARG, "streaming GEMV: no plan for %d tokens", m);
+        const uint64_t xbytes = ((uint64_t)(m - 1) * L.ldx + L.K) * ES;
         if (xbytes >= 0x7FFFFF00ull) return fail(ALV_ERR_RANGE, "activation buffer exceeds the 2 GiB range");
         Gemv1Args a{};
+        if (p.ks > 1) {
+            Workspace ws;
+            if (int rc = get_workspace(s, kSyncWords + kSplitCounters, &ws)) return rc;
+            a.cnt = ws.counters + kSyncWords;
+            a.part = ws.part;
+        }
         a.W0 = L.W0;
         a.W1 = L.W1;
         a.X = L.Xb ? (const void*)(L.Xb + (size_t)m0 * L.ldx) : (const void*)(L.X + (size_t)m0 * L.ldx);
@@ -421,12 +537,12 @@ int launch_gemv1(const GemvLaunch& L, hipStream_t s) {
         a.ng_last = tg.ng_last;
         a.ldx = L.ldx;
         a.ldy = L.ldy;
+        a.M = m;
         a.rt_q = p.rt_q;
         a.rt_r = p.rt_r;
+        a.ks = p.ks;
         a.act = L.act;
-        const hipError_t e = L.glu ? launch_mt<kP, 3, true>(a, mt, p.groups, p.lds, s)
-                             : L.Xb ? launch_mt<kP, 1, false>(a, mt, p.groups, p.lds, s)
-                                    : launch_mt<kP, 3, false>(a, mt, p.groups, p.lds, s);
+        const hipError_t e = launch_shape(a, L, p.sh, p.tg * p.ks, p.lds, s);
         if (int rc = hip_check(e, "q4_gemv1_kernel launch")) return rc;
     }
     return ALV_OK;

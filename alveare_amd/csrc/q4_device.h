@@ -93,6 +93,10 @@ __device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
 
+__device__ __forceinline__ uint32_t buf_load4_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 16);
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h16) {
     return __builtin_bit_cast(float, h16 << 16);
 }

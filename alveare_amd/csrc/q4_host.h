@@ -20,9 +20,14 @@ int hip_check(hipError_t e, const char* what);
 // words (a set for each of up to 64 streams) are allocated at its first call,
 // which synchronises the device; later calls, a stream's first included,
 // allocate nothing.
+//
+// Each set also holds kPartBytes of partial-sum scratch for the streaming
+// GEMV's split-K launches (rewritten by every such launch before it is read).
+constexpr size_t kPartBytes = 2u << 20;
 struct Workspace {
     uint32_t* counters = nullptr;
     size_t counter_count = 0;
+    float* part = nullptr;
 };
 int get_workspace(hipStream_t s, size_t counters, Workspace* out);
 
@@ -68,6 +73,9 @@ constexpr int kSyncExit1 = kMaxOps * kSyncSlots;
 constexpr int kSyncExit2 = kSyncExit1 + kSyncSlots;
 constexpr int kSyncError = kSyncExit2 + 1;
 constexpr int kSyncWords = kSyncError + 1;
+// Split-K arrival counters of the streaming GEMV, after the executor's words
+// (one per tile group of a launch).
+constexpr int kSplitCounters = 1024;
 
 // Device-side descriptor of one op (kernel argument; every field is
 // wave-uniform). Work split: a workgroup of 16 waves holds rtw row-tile slots

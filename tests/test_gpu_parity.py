@@ -202,7 +202,8 @@ def test_registered_gemv_parity(orc, dev, N, K):
     w.close()
 
 
-@pytest.mark.parametrize("M,N,K", [(3, 3840, 3840), (16, 1000, 1152), (40, 700, 3840)])
+@pytest.mark.parametrize("M,N,K", [(3, 3840, 3840), (5, 2000, 2048), (16, 1000, 1152), (8, 3840, 15360),
+                                   (40, 700, 3840)])
 def test_registered_gemm_parity(orc, dev, M, N, K):
     import alveare_amd as aa
 
@@ -216,6 +217,26 @@ def test_registered_gemm_parity(orc, dev, M, N, K):
     assert err <= parity.TOL
     for m in sorted({0, M - 1}):
         parity.gemv_check(orc, W, X[m], Y[m], N, K)
+    w.close()
+
+
+def test_registered_split_k_deterministic(orc, dev):
+    """Eight tokens against a long K: the launch splits K over workgroups and
+    the last of each tile group adds the shares in split order, so repeated
+    launches agree bit for bit (and the arrival counters reset themselves)."""
+    import alveare_amd as aa
+
+    M, N, K = 8, 3840, 15360
+    _say(f"split-K determinism M={M} N={N} K={K}")
+    W = orc.synth_q4(N, K, 8100)
+    X = orc.synth_normal(M * K, 8101).reshape(M, K)
+    w = aa.Q4Weight(to_dev(W, dev), N, K)
+    Xd = to_dev(X, dev)
+    ys = [w(Xd, M=M).cpu().numpy() for _ in range(3)]
+    for y in ys[1:]:
+        assert np.array_equal(y, ys[0])
+    for m in (0, M - 1):
+        parity.gemv_check(orc, W, X[m], ys[0][m], N, K)
     w.close()
 
 
@@ -390,6 +411,7 @@ def _ffn_inputs(orc, H, I, kind, seed):
 @pytest.mark.parametrize("H,I,M,act,kind", [(256, 512, 1, "gelu", "ref"), (1024, 2048, 1, "gelu", "syn"),
                                             (1152, 6912, 1, "gelu", "syn"), (1152, 6912, 1, "silu", "syn"),
                                             (3840, 15360, 1, "gelu", "syn"), (3840, 15360, 4, "gelu", "syn"),
+                                            (3840, 15360, 8, "gelu", "syn"),
                                             (1152, 6912, 16, "gelu", "syn"), (1152, 6912, 64, "gelu", "syn")])
 def test_ffn_parity(orc, dev, H, I, M, act, kind):
     import alveare_amd as aa
