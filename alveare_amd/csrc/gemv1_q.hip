@@ -58,9 +58,9 @@ struct Gemv1Args {
 
 constexpr int kXO = 4;  // activation octets per thread and staging round
 
-// Eight activations of one token as R bf16 terms at dst, dst + 8, ...: R = 3
-// is the exact split of fp32 values, R = 1 bf16 values as they are.
-template <int R>
+// Eight activations of one token as R bf16 terms at dst, dst + TS, dst + 2 TS:
+// R = 3 is the exact split of fp32 values, R = 1 bf16 values as they are.
+template <int R, int TS>
 __device__ __forceinline__ void stage_octet(const u32x4 (&v)[2], __bf16* dst) {
     if constexpr (R == 1) {
         *reinterpret_cast<u32x4*>(dst) = v[0];
@@ -79,8 +79,8 @@ __device__ __forceinline__ void stage_octet(const u32x4 (&v)[2], __bf16* dst) {
             p2[e] = s.p2;
         }
         *reinterpret_cast<bf16x8*>(dst) = p0;
-        *reinterpret_cast<bf16x8*>(dst + 8) = p1;
-        *reinterpret_cast<bf16x8*>(dst + 16) = p2;
+        *reinterpret_cast<bf16x8*>(dst + TS) = p1;
+        *reinterpret_cast<bf16x8*>(dst + 2 * TS) = p2;
     }
 }
 
@@ -120,20 +120,25 @@ __device__ __forceinline__ UnitPos unit_pos(const Gemv1Args& a, const WgWork& wk
     return p;
 }
 
-// Rows of A in use (MT tokens x R terms, row m * R + p) and the lanes whose D
-// output holds them (lane l holds D rows 4 (l / 16) .. + 3 of column l % 16).
-template <int R, int MT>
+// Activation rows of an operand slot (MT tokens x R terms) and how they meet
+// the MFMA. Token-major (TB = false): one A block, row m * R + p, the terms
+// added up per row at the end. Term-major (TB = true): R blocks of MT rows,
+// block p = term p of every token, one MFMA per block into the same
+// accumulator, so D row m is already token m's sum. Lane l holds D rows
+// 4 (l / 16) .. + 3 of column l % 16; DL lanes hold the rows in use.
+template <int R, int MT, bool TB>
 struct ARows {
-    static constexpr int RM = R * MT;
-    static constexpr int DL = 16 * ((RM + 3) / 4);
+    static constexpr int RM = R * MT;        // rows per slot in LDS
+    static constexpr int AR = TB ? MT : RM;  // rows per A block
+    static constexpr int DL = 16 * ((AR + 3) / 4);
 };
 
-template <int NW, int P, int R, bool XB, bool GLU, int MT>
+template <int NW, int P, int R, bool XB, bool GLU, int MT, bool TB>
 __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     constexpr int NT = GLU ? 2 : 1;
     constexpr int ES = XB ? 2 : 4;  // activation element size
-    constexpr int RM = ARows<R, MT>::RM, DL = ARows<R, MT>::DL;
-    static_assert(RM <= 16, "one MFMA row block");
+    constexpr int RM = ARows<R, MT, TB>::RM, AR = ARows<R, MT, TB>::AR, DL = ARows<R, MT, TB>::DL;
+    static_assert(AR <= 16, "MFMA row block");
     static_assert(!XB || R == 1, "bf16 activations take one term");
     extern __shared__ __align__(16) unsigned char smem[];
 
@@ -156,7 +161,8 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     // Octet o (8 consecutive k) of token m sits at operand slot
     // ((o / 64 - s0) * 16 + o % 16) * 4 + (o / 16) % 4 -- super-step o / 64,
     // block 4 g + bl with g = (o / 16) % 4, bl = (o / 4) % 4, dword t = o % 4
-    // of the block -- rows m * R .. m * R + R - 1 of the slot's RM rows.
+    // of the block -- rows m * R + p (token-major) or p * MT + m (term-major)
+    // of the slot's RM rows.
     // Tokens past M (a launch's last group) read zeros.
     const int octs = wk.nsw * 64;
     const int E = MT * octs;
@@ -180,7 +186,7 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
             const int o = e - m * octs;  // relative to super-step s0
             if (e < E) {
                 const int slot = ((o >> 6) * 16 + (o & 15)) * 4 + ((o >> 4) & 3);
-                stage_octet<R>(xr[i], xs + ((size_t)slot * RM + m * R) * 8);
+                stage_octet<R, TB ? MT * 8 : 8>(xr[i], xs + ((size_t)slot * RM + (TB ? m : m * R)) * 8);
             }
         }
     }
@@ -216,9 +222,9 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     }
 
     // ---- 3. stream: dequantize + MFMA one unit, refill its ring slot ---------------
-    // Lane base of the A operand: slot g, row j (rows >= RM read row RM - 1;
-    // their D rows are never used).
-    const __bf16* xa = xs + ((size_t)g * RM + min(j, RM - 1)) * 8;
+    // Lane base of the A operand: slot g, row j of the (first) block (rows >= AR
+    // read row AR - 1; their D rows are never used).
+    const __bf16* xa = xs + ((size_t)g * RM + min(j, AR - 1)) * 8;
     // Every pass refills every slot (past the last unit the loads read past the
     // buffer and return zeros), so the loads in flight per slot are the same on
     // every path and the compiler's wait counts keep P - 1 units in flight.
@@ -245,12 +251,16 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
                         const int wi = 5 * bl + t;
-                        const bf16x8 av = *reinterpret_cast<const bf16x8*>(xu + (bl * 4 + t) * 4 * RM * 8);
                         const bf16x8 bv = dequant8_mix((uint32_t)q[k][wi >> 2][wi & 3], sc);
-                        if (t & 1)
-                            t1 = mfma16x16x32(av, bv, t1);
-                        else
-                            t0 = mfma16x16x32(av, bv, t0);
+#pragma unroll
+                        for (int pb = 0; pb < (TB ? R : 1); ++pb) {
+                            const bf16x8 av =
+                                *reinterpret_cast<const bf16x8*>(xu + ((bl * 4 + t) * 4 * RM + pb * MT) * 8);
+                            if (t & 1)
+                                t1 = mfma16x16x32(av, bv, t1);
+                            else
+                                t0 = mfma16x16x32(av, bv, t0);
+                        }
                     }
                 }
                 if (lane < DL) part[(size_t)u * DL + lane] = t0 + t1;
@@ -263,8 +273,8 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     lds_barrier();
 
     // ---- 4. per row: sum the unit slots in a fixed order ---------------------------
-    // D row m * R + p (token m, term p) of column jj sits in slot lane
-    // 16 * (row / 4) + jj, element row % 4. Wave w takes rows 16 w .. 16 w + 15
+    // D row m * R + p (token m, term p; term-major: row m, terms summed) of
+    // column jj sits in slot lane 16 * (row / 4) + jj, element row % 4. Wave w takes rows 16 w .. 16 w + 15
     // of the workgroup (then 16 NW further on); four lanes share a row: lane c
     // sums super-steps c, c + 4, ... in ascending order and the four partial
     // sums combine in a fixed butterfly, so the result does not depend on
@@ -288,8 +298,8 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
                 for (int m = 0; m < MT; ++m) {
                     float v = 0.0f;
 #pragma unroll
-                    for (int p = 0; p < R; ++p) {
-                        const int row = m * R + p;
+                    for (int p = 0; p < (TB ? 1 : R); ++p) {
+                        const int row = TB ? m : m * R + p;
                         v += sl[(row >> 2) * 16][row & 3];
                     }
                     y[m][n] += v;
@@ -387,9 +397,9 @@ const DevInfo& dev_info() {
 
 constexpr int kNW = 16;
 
-template <int P, int R, bool XB, bool GLU, int MT>
+template <int P, int R, bool XB, bool GLU, int MT, bool TB = false>
 hipError_t launch_k(const Gemv1Args& a, int groups, size_t lds, hipStream_t s) {
-    auto k = q4_gemv1_kernel<kNW, P, R, XB, GLU, MT>;
+    auto k = q4_gemv1_kernel<kNW, P, R, XB, GLU, MT, TB>;
     if (lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -406,22 +416,25 @@ hipError_t launch_k(const Gemv1Args& a, int groups, size_t lds, hipStream_t s) {
 // on every decode shape -- a deeper ring only lengthens the memory queues.
 constexpr int kP = 1;
 
-// Token capacity of a launch and activation terms per token: fp32
-// activations take the exact three-term split, up to 5 tokens (15 A rows);
-// bf16 activations one term, up to 16 tokens.
+// Token capacity of a launch, activation terms per token and row layout:
+// fp32 activations take the exact three-term split, token-major up to 5
+// tokens (15 A rows, one MFMA per weight octet), term-major for 8 (three
+// MFMAs); bf16 activations one term, up to 16 tokens.
 struct Shape {
     int mt, r;
+    bool tb;
 };
 
 Shape shape_for(const GemvLaunch& L, int m) {
     if (L.Xb) {
         int mt = 1;
         while (mt < m && mt < 16) mt *= 2;
-        return {mt, 1};
+        return {mt, 1, false};
     }
-    if (m <= 2) return {m, 3};
-    if (m <= 4) return {4, 3};
-    return {5, 3};
+    if (m <= 2) return {m, 3, false};
+    if (m <= 4) return {4, 3, false};
+    if (m <= 5) return {5, 3, false};
+    return {8, 3, true};
 }
 
 hipError_t launch_shape(const Gemv1Args& a, const GemvLaunch& L, Shape sh, int groups, size_t lds, hipStream_t s) {
@@ -439,14 +452,16 @@ hipError_t launch_shape(const Gemv1Args& a, const GemvLaunch& L, Shape sh, int g
             case 1: return launch_k<kP, 3, false, true, 1>(a, groups, lds, s);
             case 2: return launch_k<kP, 3, false, true, 2>(a, groups, lds, s);
             case 4: return launch_k<kP, 3, false, true, 4>(a, groups, lds, s);
-            default: return launch_k<kP, 3, false, true, 5>(a, groups, lds, s);
+            case 5: return launch_k<kP, 3, false, true, 5>(a, groups, lds, s);
+            default: return launch_k<kP, 3, false, true, 8, true>(a, groups, lds, s);
         }
     }
     switch (sh.mt) {
         case 1: return launch_k<kP, 3, false, false, 1>(a, groups, lds, s);
         case 2: return launch_k<kP, 3, false, false, 2>(a, groups, lds, s);
         case 4: return launch_k<kP, 3, false, false, 4>(a, groups, lds, s);
-        default: return launch_k<kP, 3, false, false, 5>(a, groups, lds, s);
+        case 5: return launch_k<kP, 3, false, false, 5>(a, groups, lds, s);
+        default: return launch_k<kP, 3, false, false, 8, true>(a, groups, lds, s);
     }
 }
 
@@ -468,6 +483,7 @@ bool plan_gemv1(const GemvLaunch& L, int m, Gemv1Plan* out) {
     Gemv1Plan p;
     p.sh = shape_for(L, m);
     const int RM = p.sh.mt * p.sh.r;
+    const int AR = p.sh.tb ? p.sh.mt : RM;
     for (p.ks = 1; p.ks <= 16 && p.ks <= tg.nss; p.ks *= 2) {
         p.tg = std::min(RT, std::max(1, d.cus / p.ks));
         p.rt_q = RT / p.tg;
@@ -475,7 +491,7 @@ bool plan_gemv1(const GemvLaunch& L, int m, Gemv1Plan* out) {
         const int tiles = p.rt_q + (p.rt_r ? 1 : 0);
         const int nsw = (tg.nss + p.ks - 1) / p.ks;
         const int units = tiles * nsw * NT;
-        p.lds = (size_t)nsw * 1024 * RM + (size_t)units * 256 * ((RM + 3) / 4) + 16;
+        p.lds = (size_t)nsw * 1024 * RM + (size_t)units * 256 * ((AR + 3) / 4) + 16;
         const size_t part = p.ks > 1 ? (size_t)RT * 16 * p.ks * p.sh.mt * NT * sizeof(float) : 0;
         if (p.lds <= d.lds && part <= kPartBytes && (p.ks == 1 || p.tg <= kSplitCounters)) {
             *out = p;
@@ -489,7 +505,7 @@ bool plan_gemv1(const GemvLaunch& L, int m, Gemv1Plan* out) {
 int max_tokens(const GemvLaunch& L) {
     Gemv1Plan p;
     for (int m : {16, 8, 5, 4, 2, 1})
-        if (m <= (L.Xb ? 16 : 5) && plan_gemv1(L, m, &p)) return m;
+        if (m <= (L.Xb ? 16 : 8) && plan_gemv1(L, m, &p)) return m;
     return 0;
 }
 
