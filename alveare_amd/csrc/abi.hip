@@ -88,6 +88,38 @@ int get_workspace(hipStream_t s, size_t counters, Workspace* out) {
     return ALV_OK;
 }
 
+namespace {
+struct Scratch {
+    void* p = nullptr;
+    size_t cap = 0;
+};
+std::map<std::pair<int, hipStream_t>, Scratch> g_scratch;
+}  // namespace
+
+int get_scratch(hipStream_t s, size_t bytes, void** out) {
+    int dev = 0;
+    if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    Scratch& sc = g_scratch[{dev, s}];
+    if (bytes > sc.cap) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (int rc = hip_check(hipStreamIsCapturing(s, &cs), "hipStreamIsCapturing")) return rc;
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(ALV_ERR_ARG, "prefill scratch of %zu bytes must grow, which cannot happen during graph capture: "
+                        "run one call of this size on this stream before capturing", bytes);
+        if (int rc = hip_check(hipStreamSynchronize(s), "hipStreamSynchronize")) return rc;
+        if (sc.p) (void)hipFree(sc.p);
+        sc.p = nullptr;
+        sc.cap = 0;
+        const size_t cap = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+        if (int rc = hip_check(hipMalloc(&sc.p, cap), "hipMalloc(prefill scratch)")) return rc;
+        if (int rc = hip_check(hipMemsetAsync(sc.p, 0, cap, s), "hipMemsetAsync(prefill scratch)")) return rc;
+        sc.cap = cap;
+    }
+    *out = sc.p;
+    return ALV_OK;
+}
+
 }  // namespace alv
 
 extern "C" const char* alv_last_error(void) { return alv::g_err; }

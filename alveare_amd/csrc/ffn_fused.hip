@@ -1,9 +1,9 @@
 // Fused FFN (gate/up projection, GLU activation, down projection) on gfx950:
 // alv_ffn_register / alv_ffn_fused / alv_ffn_shape / alv_ffn_release.
 //
-// Decode (M <= 16): two launches of the one-shot kernel (oneshot_q.hip).
-//   1. gate and up rows of one 16-row I-tile are streamed together by the same
-//      waves against the same activation operands; the epilogue rounds both to
+// Decode (M <= 16): two launches of the streaming kernel (gemv1_q.hip).
+//   1. gate and up tiles of the same rows are streamed by the same workgroup
+//      against the same activation operands; the epilogue rounds both to
 //      bf16, applies the GLU and rounds the activation to bf16 -- the
 //      reference CPU path's three rounding points (runtime/py/model.py:798-803).
 //      The activation (M x I bf16) stays in the handle's scratch, which is

@@ -6,7 +6,7 @@
 // 256-token x 128-weight-row tile and walks K 64 at a time (two Q4 blocks per
 // row):
 //   * the 128 x 64 weight tile is dequantized once into LDS as bf16
-//     (q4_device.h::dequant8, exact), shared by 256 tokens;
+//     (q4_device.h::dequant8_mix, exact), shared by 256 tokens;
 //   * the 256 x 64 activation tile goes into LDS as bf16. fp32 activations
 //     are split exactly into up to three bf16 terms (x = t0 + t1 + t2,
 //     q4_device.h::split3), one pass over K per term: the first pass stages
@@ -16,9 +16,17 @@
 //     (runtime/py/model.py:399-485) -- cost one pass;
 //   * each wave computes a 64 x 64 sub-tile with v_mfma_f32_16x16x32_bf16
 //     (fp32 accumulation);
-//   * the global loads of step k + 1 are issued before the MFMAs of step k and
-//     land in the other half of a double-buffered LDS, so one barrier per step
-//     separates them.
+//   * the global loads of step k + 2 are issued before the MFMAs of step k
+//     (two register stages for bf16 activations, one for fp32) and land in
+//     the other half of a double-buffered LDS, so one barrier per step
+//     separates them; the dequantization of step k + 1 sits between the two
+//     k-halves of step k's MFMAs;
+//   * fp32 activations are first split into three bf16 term arrays by
+//     split_x_kernel (half the bytes per re-read, the token tile fits the
+//     L2), with a per-token flag for the second and third terms;
+//   * a grid that leaves half the CUs idle (the FFN's down projection: 30
+//     weight tiles x 2 token tiles) splits K; the last workgroup of each tile
+//     adds the partial tiles in split order (deterministic).
 // Workgroups are numbered token-tile fastest: with the round-robin placement
 // of workgroups on the 8 XCDs, the workgroups of one XCD share token tiles, so
 // their activation reads hit that XCD's L2.
@@ -46,9 +54,18 @@ struct GemmArgs {
     float* Y;                // fp32 output, or
     uint16_t* Yb;            // bf16 output (bit patterns)
     uint32_t wbytes;
-    uint32_t xbytes;         // bytes of X (buffer range)
+    uint32_t xbytes;         // bytes of X (buffer range, all terms)
     int ldx, ldy, M, N, K, parts, act;
     TileGeom tg;
+    // bf16 activations given as three term arrays tstride elements apart
+    // (split_x_kernel): tflags[m] != 0 when token m has a nonzero second or
+    // third term. Null: one term.
+    const uint32_t* tflags;
+    uint32_t tstride;
+    // Split K (grid.z = ks): partial tiles and per-tile arrival counters.
+    int ks;
+    float* part;
+    uint32_t* cnt;
 };
 
 template <int NT, bool TILED, bool XF32>
@@ -60,23 +77,42 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 waves of 64 x 64
     const int m0 = blockIdx.x * TM;
     const int n0 = blockIdx.y * TN;
-    const int nsteps = (a.K + TK - 1) / TK;
+    const int nsteps_all = (a.K + TK - 1) / TK;
+    // Split K: this workgroup's steps [st0, st0 + nsteps).
+    const int kq = blockIdx.z;
+    const int st0 = kq * nsteps_all / a.ks;
+    const int nsteps = (kq + 1) * nsteps_all / a.ks - st0;
     const int j = lane & 15, g = lane >> 4;
     const uint32_t rs = (uint32_t)(a.K >> 5) * kBlockBytes;
 
-    // Staging roles. Weights: thread -> (matrix, row, block) of the
-    // NT x 128 x 2 blocks of a step (threads past them stay idle).
-    // Activations: thread -> 8 consecutive k of one token, 4 such pieces.
-    const int wmat = tid >> 8;
-    const int wr = (tid >> 1) & (TN - 1), wb = tid & 1;
-    const bool wstage = wmat < NT;
+    // Staging roles. Weights: wave -> (block wb of the step's two, matrix
+    // wmat, half of the 128 rows), lane -> row, so a thread's row is fixed and
+    // the part of each load address that moves with the step is wave-uniform
+    // (an SGPR soffset; no per-step address arithmetic per lane). Waves past
+    // the NT x 2 x 2 roles stay idle. Activations: thread -> 8 consecutive k
+    // of one token, 4 tokens 64 apart.
+    const int wb = wave & 1;
+    const int wmat = NT == 2 ? (wave >> 1) & 1 : 0;
+    const int rh = NT == 2 ? wave >> 2 : wave >> 1;
+    const bool wstage = rh < 2;
+    const int wr = rh * 64 + lane;
     const int wrow = n0 + wr;
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(wmat ? a.W1 : a.W0, a.wbytes);
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.X, a.xbytes);
+    // Lane parts of the addresses (past the range: the loads return zeros).
+    const uint32_t wv = wstage && wrow < a.N ? (TILED ? (uint32_t)(wrow >> 4) * a.tg.rtb + (uint32_t)(wrow & 15) * 16u
+                                                      : (uint32_t)wrow * rs)
+                                             : a.wbytes;
+    uint32_t xv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + (tid >> 3) + 64 * i;
+        xv[i] = m < a.M ? (uint32_t)(((size_t)m * a.ldx + (tid & 7) * 8) * (XF32 ? 4 : 2)) : a.xbytes;
+    }
 
     f32x4 acc[NT][4][4];
 #pragma unroll
@@ -87,43 +123,56 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
             for (int jj = 0; jj < 4; ++jj) acc[n][i][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     constexpr int XV = XF32 ? 2 : 1;  // 16-byte loads per 8 activations
-    uint32_t wreg[5];
-    u32x4 xreg[4][XV];
+    // Two register stages (bf16 activations): the loads of step s + 2 are
+    // issued while step s is computed from LDS and step s + 1 waits in the
+    // other stage.
+    uint32_t wreg0[5], wreg1[5];
+    u32x4 xreg0[4][XV], xreg1[4][XV];
     uint32_t lowbits = 0;  // OR of all fp32 activation bits seen by the first pass
 
-    // Global loads of step s into registers.
-    auto load = [&](int s) {
+    // Global loads of step s (absolute) of activation term p into registers.
+    // Activations past K (a last step half past it) read the next token's
+    // values or zeros: finite, and their weights are zero.
+    auto load = [&](int s, int p, uint32_t (&wreg)[5], u32x4 (&xreg)[4][XV]) __attribute__((always_inline)) {
         const int kb = s * 2 + wb;
-        const bool ok = wstage && wrow < a.N && kb < (a.K >> 5);
+        const bool ok = kb < (a.K >> 5);
 #pragma unroll
         for (int x = 0; x < 5; ++x) {
-            uint32_t off = a.wbytes;
-            if (ok) off = TILED ? tiled_offset(a.tg, wrow, kb, 4 * x) : (uint32_t)wrow * rs + (uint32_t)kb * kBlockBytes + 4 * x;
-            wreg[x] = buf_load4(rw, off);
+            uint32_t so = a.wbytes;
+            if (ok) {
+                if constexpr (TILED) {
+                    // Byte 4x of block kb within the row's run: super-step kb / 16,
+                    // plane (20 bl + 4x) / 16, lane group g (q4_device.h tiled layout).
+                    const int ss = kb >> 4, gq = (kb >> 2) & 3, rb = 20 * (kb & 3) + 4 * x;
+                    const uint32_t ng = ss == a.tg.nss - 1 ? (uint32_t)a.tg.ng_last : 4u;
+                    so = (uint32_t)ss * 5120u + (uint32_t)(rb >> 4) * 256u * ng + (uint32_t)gq * 256u + (uint32_t)(rb & 15);
+                } else {
+                    so = (uint32_t)kb * kBlockBytes + 4u * x;
+                }
+            }
+            wreg[x] = __builtin_amdgcn_raw_buffer_load_b32(rw, wv, __builtin_amdgcn_readfirstlane(so), 0);
         }
+        const uint32_t xo = __builtin_amdgcn_readfirstlane(
+            (uint32_t)(((size_t)s * TK + (XF32 ? 0 : (size_t)p * a.tstride)) * (XF32 ? 4 : 2)));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int piece = tid + i * kGemmThreads;  // 256 tokens x 8 pieces
-            const int r = piece >> 3, c = (piece & 7) * 8;
-            const int m = m0 + r, k = s * TK + c;
-            const bool in = m < a.M && k < a.K;
-            const uint32_t off = in ? (uint32_t)(((size_t)m * a.ldx + k) * (XF32 ? 4 : 2)) : a.xbytes;
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int v = 0; v < XV; ++v) xreg[i][v] = buf_load16(rx, off + 16 * v);
-        }
+            for (int v = 0; v < XV; ++v)
+                xreg[i][v] = __builtin_amdgcn_raw_buffer_load_b128(rx, xv[i] + 16 * v, xo, 0);
     };
-    // Registers of the last load into LDS buffer b, activations as term p.
-    auto store = [&](int b, int p) {
+    // Registers of a load into LDS buffer b, activations as term p.
+    auto store_w = [&](int b, const uint32_t (&wreg)[5]) __attribute__((always_inline)) {
         if (wstage) {
-            const Scale sc = make_scale(bf16_bits_to_f32(wreg[4] & 0xFFFFu));
+            const Scale2 sc = make_scale2(bf16_bits_to_f32(wreg[4] & 0xFFFFu));
             __bf16* dst = wsm + ((size_t)(b * NT + wmat) * TN + wr) * LDR + 32 * wb;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) *reinterpret_cast<bf16x8*>(dst + 8 * t) = dequant8(wreg[t], sc);
+            for (int t = 0; t < 4; ++t) *reinterpret_cast<bf16x8*>(dst + 8 * t) = dequant8_mix(wreg[t], sc);
         }
+    };
+    auto store_x = [&](int b, int p, const u32x4 (&xreg)[4][XV]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int piece = tid + i * kGemmThreads;
-            const int r = piece >> 3, c = (piece & 7) * 8;
+            const int r = (tid >> 3) + 64 * i, c = (tid & 7) * 8;
             u32x4* dst = reinterpret_cast<u32x4*>(xsm + ((size_t)b * TM + r) * LDR + c);
             if constexpr (XF32) {
                 bf16x8 t;
@@ -145,40 +194,135 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
             }
         }
     };
+    auto store = [&](int b, int p, const uint32_t (&wreg)[5], const u32x4 (&xreg)[4][XV]) __attribute__((always_inline)) {
+        store_w(b, wreg);
+        store_x(b, p, xreg);
+    };
 
     int nterms = 1;
-    for (int p = 0; p < nterms; ++p) {
-        load(0);
-        store(0, p);
-        __syncthreads();
-        for (int s = 0; s < nsteps; ++s) {
-            const int b = s & 1;
-            if (s + 1 < nsteps) load(s + 1);
+    if (!XF32 && a.tflags) {
+        // Terms 1 and 2 only for a token tile with a token that has them.
+        const int m = m0 + (tid & (TM - 1));
+        nterms = __syncthreads_or(tid < TM && m < a.M && a.tflags[m] != 0) ? 3 : 1;
+    }
+    auto compute_kk = [&](int b, int kk) __attribute__((always_inline)) {
+        {
+            bf16x8 bv[NT][4];
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                bf16x8 bv[NT][4];
+            for (int n = 0; n < NT; ++n)
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj)
+                    bv[n][jj] = *reinterpret_cast<const bf16x8*>(
+                        wsm + ((size_t)(b * NT + n) * TN + wn * 64 + jj * 16 + j) * LDR + kk * 32 + 8 * g);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bf16x8 av = *reinterpret_cast<const bf16x8*>(
+                    xsm + ((size_t)b * TM + wm * 64 + i * 16 + j) * LDR + kk * 32 + 8 * g);
 #pragma unroll
                 for (int n = 0; n < NT; ++n)
 #pragma unroll
-                    for (int jj = 0; jj < 4; ++jj)
-                        bv[n][jj] = *reinterpret_cast<const bf16x8*>(
-                            wsm + ((size_t)(b * NT + n) * TN + wn * 64 + jj * 16 + j) * LDR + kk * 32 + 8 * g);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const bf16x8 av = *reinterpret_cast<const bf16x8*>(
-                        xsm + ((size_t)b * TM + wm * 64 + i * 16 + j) * LDR + kk * 32 + 8 * g);
-#pragma unroll
-                    for (int n = 0; n < NT; ++n)
-#pragma unroll
-                        for (int jj = 0; jj < 4; ++jj) acc[n][i][jj] = mfma16x16x32(av, bv[n][jj], acc[n][i][jj]);
-                }
+                    for (int jj = 0; jj < 4; ++jj) acc[n][i][jj] = mfma16x16x32(av, bv[n][jj], acc[n][i][jj]);
             }
-            if (s + 1 < nsteps) store(b ^ 1, p);
+        }
+    };
+    auto compute = [&](int b) __attribute__((always_inline)) {
+        compute_kk(b, 0);
+        compute_kk(b, 1);
+    };
+    for (int p = 0; p < nterms; ++p) {
+        if constexpr (XF32) {
+            // fp32 activations take twice the registers per stage: one stage,
+            // loads one step ahead.
+            load(st0, p, wreg0, xreg0);
+            store(0, p, wreg0, xreg0);
             __syncthreads();
+            for (int s = 0; s < nsteps; ++s) {
+                const int b = s & 1;
+                if (s + 1 < nsteps) load(st0 + s + 1, p, wreg0, xreg0);
+                compute(b);
+                if (s + 1 < nsteps) store(b ^ 1, p, wreg0, xreg0);
+                __syncthreads();
+            }
+        } else {
+            load(st0, p, wreg0, xreg0);
+            if (nsteps > 1) load(st0 + 1, p, wreg1, xreg1);
+            store(0, p, wreg0, xreg0);
+            __syncthreads();
+            // Steps in pairs: even steps compute LDS buffer 0 (stage 1 holds
+            // the next step), odd steps buffer 1 (stage 0 holds the next).
+            // The dequantization and activation stores of the next step sit
+            // between the two k halves of this step's MFMAs, so VALU and matrix
+            // work of one wave overlap.
+            for (int s = 0; s < nsteps; s += 2) {
+                if (s + 2 < nsteps) load(st0 + s + 2, p, wreg0, xreg0);
+                compute_kk(0, 0);
+                if (s + 1 < nsteps) store_w(1, wreg1);
+                compute_kk(0, 1);
+                if (s + 1 < nsteps) store_x(1, p, xreg1);
+                __syncthreads();
+                if (s + 1 >= nsteps) break;
+                if (s + 3 < nsteps) load(st0 + s + 3, p, wreg1, xreg1);
+                compute_kk(1, 0);
+                if (s + 2 < nsteps) store_w(0, wreg0);
+                compute_kk(1, 1);
+                if (s + 2 < nsteps) store_x(0, p, xreg0);
+                __syncthreads();
+            }
         }
         // After the first pass: residual terms only for a token tile with
         // activations that are not bf16-valued.
         if (XF32 && p == 0 && a.parts == 3) nterms = __syncthreads_or((lowbits & 0xFFFFu) != 0) ? 3 : 1;
+    }
+
+    // ---- split K: the last workgroup of the tile adds the partial tiles -------------
+    // Each workgroup writes its partial tile through (agent-scope stores) and
+    // counts itself in once they have landed; the one that completes the count
+    // reads all of them (sc1) and sums them in split order, so the result does
+    // not depend on which came last, then resets the count.
+    if (a.ks > 1) {
+        const size_t tile = (size_t)blockIdx.y * gridDim.x + blockIdx.x;
+        const size_t tsz = (size_t)NT * TM * TN;
+        auto at = [&](int n, int i, int jj, int r) -> size_t {
+            return ((size_t)n * TM + wm * 64 + i * 16 + 4 * g + r) * TN + wn * 64 + jj * 16 + j;
+        };
+        float* mine = a.part + (tile * a.ks + kq) * tsz;
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        __hip_atomic_store(mine + at(n, i, jj, r), acc[n][i][jj][r], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __shared__ int last;
+        __syncthreads();
+        if (tid == 0)
+            last = __hip_atomic_fetch_add(&a.cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   (uint32_t)(a.ks - 1);
+        __syncthreads();
+        if (!last) return;
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.part + tile * a.ks * tsz, (uint32_t)(a.ks * tsz * sizeof(float)));
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) acc[n][i][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < a.ks; ++q)
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            acc[n][i][jj][r] += __builtin_bit_cast(
+                                float, buf_load4_sc1(rp, (uint32_t)((q * tsz + at(n, i, jj, r)) * sizeof(float))));
+        if (tid == 0) __hip_atomic_store(&a.cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     // ---- epilogue: D[4g + r][j] of each 16 x 16 sub-tile ----------------------------
@@ -199,6 +343,28 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
                 else
                     a.Y[(size_t)m * a.ldy + n] = out;
             }
+}
+
+// fp32 activations -> three bf16 term arrays (exact split, q4_device.h::split3)
+// once per call, so the GEMM reads half the bytes per activation and its
+// token tiles hold them in L2; flags[m] != 0 when token m has a nonzero second
+// or third term. One workgroup per token.
+__global__ void __launch_bounds__(256) split_x_kernel(const float* X, int ldx, int K, uint16_t* T, uint32_t tstride,
+                                                      uint32_t* flags) {
+    const int m = blockIdx.x;
+    const float* x = X + (size_t)m * ldx;
+    uint16_t* t = T + (size_t)m * K;
+    bool more = false;
+    for (int k = threadIdx.x; k < K; k += 256) {
+        const Split3 sp = split3(x[k]);
+        const uint16_t b1 = __builtin_bit_cast(uint16_t, sp.p1), b2 = __builtin_bit_cast(uint16_t, sp.p2);
+        t[k] = __builtin_bit_cast(uint16_t, sp.p0);
+        t[k + tstride] = b1;
+        t[(size_t)k + 2 * (size_t)tstride] = b2;
+        more |= ((b1 | b2) & 0x7FFFu) != 0;
+    }
+    more = __syncthreads_or(more);
+    if (threadIdx.x == 0) flags[m] = more ? 1u : 0u;
 }
 
 template <int NT, bool TILED, bool XF32>
@@ -227,18 +393,60 @@ hipError_t launch_gemm_x(const GemmArgs& a, bool xf32, dim3 grid, hipStream_t s)
 
 }  // namespace
 
+namespace {
+
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    }
+    return cus[dev];
+}
+
+}  // namespace
+
 int launch_gemm_tiled(const GemvLaunch& L, hipStream_t s) {
     const uint64_t wbytes = L.tiled ? tile_bytes(L.N, L.K) : (uint64_t)L.N * (uint64_t)(L.K / 32) * kBlockBytes;
-    if (wbytes >= 0xFFFFFF00ull) return fail(ALV_ERR_RANGE, "weight matrix of %llu bytes exceeds the 4 GiB buffer range", (unsigned long long)wbytes);
+    // Lane offset + step offset of a load must not wrap 32 bits: weights below
+    // 3.75 GiB, activations below 2 GiB.
+    if (wbytes >= 0xF0000000ull) return fail(ALV_ERR_RANGE, "weight matrix of %llu bytes exceeds the 3.75 GiB prefill range", (unsigned long long)wbytes);
     if (L.parts != 1 && L.parts != 3) return fail(ALV_ERR_ARG, "parts must be 1 or 3");
-    const bool xf32 = L.Xb == nullptr;
+    bool xf32 = L.Xb == nullptr;
     const void* x = xf32 ? static_cast<const void*>(L.X) : static_cast<const void*>(L.Xb);
     // 16-byte activation loads: 4-byte aligned rows for fp32; for bf16 (the FFN's
     // own activation buffer) 16-byte aligned rows.
     if (xf32 ? reinterpret_cast<uintptr_t>(x) % 4 != 0 : reinterpret_cast<uintptr_t>(x) % 16 != 0 || L.ldx % 8 != 0)
         return fail(ALV_ERR_ALIGN, "prefill activations are not aligned for 16-byte loads");
-    const uint64_t xbytes = ((uint64_t)(L.M - 1) * L.ldx + L.K) * (xf32 ? 4 : 2);
-    if (xbytes >= 0xFFFFFF00ull) return fail(ALV_ERR_RANGE, "activations of %llu bytes exceed the 4 GiB buffer range", (unsigned long long)xbytes);
+    uint64_t xbytes = ((uint64_t)(L.M - 1) * L.ldx + L.K) * (xf32 ? 4 : 2);
+    if (xbytes >= 0x7FFFFF00ull) return fail(ALV_ERR_RANGE, "activations of %llu bytes exceed the 2 GiB buffer range", (unsigned long long)xbytes);
+    const int NT = L.glu ? 2 : 1;
+    const dim3 tiles((L.M + TM - 1) / TM, (L.N + TN - 1) / TN);
+    const int ntiles = (int)(tiles.x * tiles.y);
+    // Split K while the grid leaves half the CUs idle and each split keeps at
+    // least 16 steps.
+    const int nsteps = (L.K + TK - 1) / TK;
+    int ks = 1;
+    while (ntiles * ks * 2 <= device_cus() && nsteps / (ks * 2) >= 16) ks *= 2;
+    // Scratch: split-K counters and partial tiles, then the activation terms.
+    const size_t cnt_bytes = ((size_t)ntiles * 4 + 255) & ~(size_t)255;
+    const size_t flag_bytes = ((size_t)L.M * 4 + 255) & ~(size_t)255;
+    const size_t part_bytes = ks > 1 ? (size_t)ntiles * ks * NT * TM * TN * sizeof(float) : 0;
+    const size_t tstride = (size_t)L.M * L.K;
+    const size_t term_bytes = xf32 ? 3 * tstride * sizeof(uint16_t) : 0;
+    void* scratch = nullptr;
+    if (ks > 1 || xf32) {
+        if (6 * tstride >= 0x7FFFFF00ull || get_scratch(s, cnt_bytes + flag_bytes + part_bytes + term_bytes, &scratch)) {
+            // No scratch (a graph capture that would have to grow it): one
+            // launch over all of K, activations split inside the kernel.
+            clear_error();
+            scratch = nullptr;
+            ks = 1;
+        }
+    }
+    uint8_t* sb = static_cast<uint8_t*>(scratch);
     GemmArgs a{};
     a.W0 = L.W0;
     a.W1 = L.W1;
@@ -255,7 +463,24 @@ int launch_gemm_tiled(const GemvLaunch& L, hipStream_t s) {
     a.parts = L.parts;
     a.act = L.act;
     a.tg = tile_geom(L.K);
-    const dim3 grid((L.M + TM - 1) / TM, (L.N + TN - 1) / TN);
+    a.ks = ks;
+    if (sb) {
+        a.cnt = reinterpret_cast<uint32_t*>(sb);
+        a.part = reinterpret_cast<float*>(sb + cnt_bytes + flag_bytes);
+        if (xf32) {
+            uint32_t* flags = reinterpret_cast<uint32_t*>(sb + cnt_bytes);
+            uint16_t* terms = reinterpret_cast<uint16_t*>(sb + cnt_bytes + flag_bytes + part_bytes);
+            hipLaunchKernelGGL(split_x_kernel, dim3(L.M), dim3(256), 0, s, L.X, L.ldx, L.K, terms, (uint32_t)tstride, flags);
+            if (int rc = hip_check(hipGetLastError(), "split_x_kernel launch")) return rc;
+            a.X = terms;
+            a.ldx = L.K;
+            a.tflags = L.parts == 3 ? flags : nullptr;
+            a.tstride = (uint32_t)tstride;
+            a.xbytes = (uint32_t)(3 * tstride * sizeof(uint16_t));
+            xf32 = false;
+        }
+    }
+    const dim3 grid(tiles.x, tiles.y, ks);
     hipError_t e;
     if (L.glu)
         e = L.tiled ? launch_gemm_x<2, true>(a, xf32, grid, s) : launch_gemm_x<2, false>(a, xf32, grid, s);

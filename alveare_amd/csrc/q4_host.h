@@ -31,6 +31,12 @@ struct Workspace {
 };
 int get_workspace(hipStream_t s, size_t counters, Workspace* out);
 
+// Per-(device, stream) scratch of at least `bytes`, zeroed when allocated, for
+// launches whose temporaries grow with M (prefill). Growing synchronises the
+// stream and reallocates, so it cannot happen during graph capture (an error
+// then); a call that fits what the stream already holds allocates nothing.
+int get_scratch(hipStream_t s, size_t bytes, void** out);
+
 // One launch of the streaming kernel (stream_q.hip):
 //   out[m, n] = sum_k X[m, k] * dequant(W0)[n, k]            (glu == false)
 //   out[m, n] = act(bf16(X W0^T), bf16(X W1^T)) rounded to bf16 (glu == true)

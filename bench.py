@@ -161,14 +161,25 @@ def profile_pass(torch, aa, dev) -> int:
     return 0
 
 
+_CAPTURE_STREAM = None
+
+
 def graph_us(torch, fn, reps: int, per: int) -> float:
     """Mean time of one of the `per` launches `fn` enqueues: a HIP graph of
     fn replayed `reps` times between HIP events on the replay stream."""
     s = torch.cuda.current_stream()
-    fn()
+    # Warm up on the capture stream itself: per-stream scratch (prefill) is
+    # sized by an ordinary call, never during capture.
+    global _CAPTURE_STREAM
+    if _CAPTURE_STREAM is None:
+        _CAPTURE_STREAM = torch.cuda.Stream()
+    cs = _CAPTURE_STREAM
+    cs.wait_stream(s)
+    with torch.cuda.stream(cs):
+        fn()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=cs):
         fn()
     g.replay()
     torch.cuda.synchronize()
