@@ -132,10 +132,13 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
 
     // Global loads of step s (absolute) of activation term p into registers.
     // Activations past K (a last step half past it) read the next token's
-    // values or zeros: finite, and their weights are zero.
-    auto load = [&](int s, int p, uint32_t (&wreg)[5], u32x4 (&xreg)[4][XV]) __attribute__((always_inline)) {
+    // values or zeros: finite, and their weights are zero. Issued on every
+    // path -- past the last step (in = false) the loads read past the buffers
+    // and return zeros -- so the compiler's wait counts stay exact and a wait
+    // for one register stage never drains the other.
+    auto load = [&](int s, bool in, int p, uint32_t (&wreg)[5], u32x4 (&xreg)[4][XV]) __attribute__((always_inline)) {
         const int kb = s * 2 + wb;
-        const bool ok = kb < (a.K >> 5);
+        const bool ok = in && kb < (a.K >> 5);
 #pragma unroll
         for (int x = 0; x < 5; ++x) {
             uint32_t so = a.wbytes;
@@ -153,7 +156,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
             wreg[x] = __builtin_amdgcn_raw_buffer_load_b32(rw, wv, __builtin_amdgcn_readfirstlane(so), 0);
         }
         const uint32_t xo = __builtin_amdgcn_readfirstlane(
-            (uint32_t)(((size_t)s * TK + (XF32 ? 0 : (size_t)p * a.tstride)) * (XF32 ? 4 : 2)));
+            in ? (uint32_t)(((size_t)s * TK + (XF32 ? 0 : (size_t)p * a.tstride)) * (XF32 ? 4 : 2)) : a.xbytes);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -233,19 +236,19 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
         if constexpr (XF32) {
             // fp32 activations take twice the registers per stage: one stage,
             // loads one step ahead.
-            load(st0, p, wreg0, xreg0);
+            load(st0, true, p, wreg0, xreg0);
             store(0, p, wreg0, xreg0);
             __syncthreads();
             for (int s = 0; s < nsteps; ++s) {
                 const int b = s & 1;
-                if (s + 1 < nsteps) load(st0 + s + 1, p, wreg0, xreg0);
+                load(st0 + s + 1, s + 1 < nsteps, p, wreg0, xreg0);
                 compute(b);
                 if (s + 1 < nsteps) store(b ^ 1, p, wreg0, xreg0);
                 __syncthreads();
             }
         } else {
-            load(st0, p, wreg0, xreg0);
-            if (nsteps > 1) load(st0 + 1, p, wreg1, xreg1);
+            load(st0, true, p, wreg0, xreg0);
+            load(st0 + 1, nsteps > 1, p, wreg1, xreg1);
             store(0, p, wreg0, xreg0);
             __syncthreads();
             // Steps in pairs: even steps compute LDS buffer 0 (stage 1 holds
@@ -254,14 +257,14 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
             // between the two k halves of this step's MFMAs, so VALU and matrix
             // work of one wave overlap.
             for (int s = 0; s < nsteps; s += 2) {
-                if (s + 2 < nsteps) load(st0 + s + 2, p, wreg0, xreg0);
+                load(st0 + s + 2, s + 2 < nsteps, p, wreg0, xreg0);
                 compute_kk(0, 0);
                 if (s + 1 < nsteps) store_w(1, wreg1);
                 compute_kk(0, 1);
                 if (s + 1 < nsteps) store_x(1, p, xreg1);
                 __syncthreads();
                 if (s + 1 >= nsteps) break;
-                if (s + 3 < nsteps) load(st0 + s + 3, p, wreg1, xreg1);
+                load(st0 + s + 3, s + 3 < nsteps, p, wreg1, xreg1);
                 compute_kk(1, 0);
                 if (s + 2 < nsteps) store_w(0, wreg0);
                 compute_kk(1, 1);
