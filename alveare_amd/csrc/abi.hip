@@ -56,7 +56,7 @@ int get_workspace(hipStream_t s, size_t counters, Workspace* out) {
             return fail(ALV_ERR_ARG,
                         "the synchronisation words of this device are allocated on its first call, which cannot "
                         "happen during graph capture: run one call on this device before capturing");
-        const size_t all = (size_t)kSyncWords + kSplitCounters;
+        const size_t all = (size_t)kWsWords;
         const size_t words = counters > all ? counters : all;
         if (hipMalloc(&w.block, words * kWsStreams * sizeof(uint32_t)) != hipSuccess) {
             w.block = nullptr;

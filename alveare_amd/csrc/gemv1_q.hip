@@ -133,37 +133,28 @@ struct ARows {
     static constexpr int DL = 16 * ((AR + 3) / 4);
 };
 
-template <int NW, int P, int R, bool XB, bool GLU, int MT, bool TB>
-__global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
-    constexpr int NT = GLU ? 2 : 1;
-    constexpr int ES = XB ? 2 : 4;  // activation element size
-    constexpr int RM = ARows<R, MT, TB>::RM, AR = ARows<R, MT, TB>::AR, DL = ARows<R, MT, TB>::DL;
+// Operand geometry of one phase: MT tokens x R activation terms, one or two
+// weight matrices (GLU: gate and up of the same rows).
+template <int R, bool XB, bool GLU, int MT, bool TB>
+struct PhaseT {
+    static constexpr int NT = GLU ? 2 : 1;
+    static constexpr int ES = XB ? 2 : 4;  // activation element size
+    static constexpr int RM = ARows<R, MT, TB>::RM, AR = ARows<R, MT, TB>::AR, DL = ARows<R, MT, TB>::DL;
     static_assert(AR <= 16, "MFMA row block");
     static_assert(!XB || R == 1, "bf16 activations take one term");
-    extern __shared__ __align__(16) unsigned char smem[];
+};
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int j = lane & 15;
-    const int g = lane >> 4;
-    const WgWork wk = wg_work(a, blockIdx.x);
-    const int U = wk.nt * wk.nsw * NT;
-    __bf16* xs = reinterpret_cast<__bf16*>(smem);
-    f32x4* part = reinterpret_cast<f32x4*>(smem + (size_t)wk.nsw * 1024 * RM);
-    // Unit counter of the workgroup, after the unit slots: the first P * NW
-    // units go to the waves statically, the rest to whichever wave frees a ring
-    // slot first, so a wave whose loads come back late does fewer units.
-    int* next = reinterpret_cast<int*>(part + (size_t)U * DL);
-    if (tid == 0) *next = P * NW;
-
-    // ---- 1. stage the activation terms before any weight load --------------------
-    // Octet o (8 consecutive k) of token m sits at operand slot
-    // ((o / 64 - s0) * 16 + o % 16) * 4 + (o / 16) % 4 -- super-step o / 64,
-    // block 4 g + bl with g = (o / 16) % 4, bl = (o / 4) % 4, dword t = o % 4
-    // of the block -- rows m * R + p (token-major) or p * MT + m (term-major)
-    // of the slot's RM rows.
-    // Tokens past M (a launch's last group) read zeros.
+// ---- 1. stage the activation terms of workgroup work wk into xs -------------------
+// Octet o (8 consecutive k) of token m sits at operand slot
+// ((o / 64 - s0) * 16 + o % 16) * 4 + (o / 16) % 4 -- super-step o / 64,
+// block 4 g + bl with g = (o / 16) % 4, bl = (o / 4) % 4, dword t = o % 4
+// of the block -- rows m * R + p (token-major) or p * MT + m (term-major)
+// of the slot's RM rows. Tokens past M (a launch's last group) read zeros.
+// SC1: the activations were written earlier in the same launch by other
+// workgroups (agent-scope stores): read them past this XCD's L2.
+template <int NW, int R, bool XB, int MT, bool TB, bool SC1>
+__device__ __forceinline__ void stage_acts(const Gemv1Args& a, const WgWork& wk, __bf16* xs, int tid) {
+    using Ph = PhaseT<R, XB, false, MT, TB>;
     const int octs = wk.nsw * 64;
     const int E = MT * octs;
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.X, a.xbytes);
@@ -175,9 +166,9 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
             const int m = MT == 1 ? 0 : e / octs;
             const int k = (wk.s0 * 64 + e - m * octs) * 8;
             const uint32_t off =
-                e < E && m < a.M && k < a.K ? (uint32_t)((m * a.ldx + k) * ES) : a.xbytes;  // past: zeros
-            xr[i][0] = buf_load16(rx, off);
-            xr[i][1] = XB ? u32x4{0u, 0u, 0u, 0u} : buf_load16(rx, off + 16);
+                e < E && m < a.M && k < a.K ? (uint32_t)((m * a.ldx + k) * Ph::ES) : a.xbytes;  // past: zeros
+            xr[i][0] = SC1 ? buf_load16_sc1(rx, off) : buf_load16(rx, off);
+            xr[i][1] = XB ? u32x4{0u, 0u, 0u, 0u} : (SC1 ? buf_load16_sc1(rx, off + 16) : buf_load16(rx, off + 16));
         }
 #pragma unroll
         for (int i = 0; i < kXO; ++i) {
@@ -186,100 +177,105 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
             const int o = e - m * octs;  // relative to super-step s0
             if (e < E) {
                 const int slot = ((o >> 6) * 16 + (o & 15)) * 4 + ((o >> 4) & 3);
-                stage_octet<R, TB ? MT * 8 : 8>(xr[i], xs + ((size_t)slot * RM + (TB ? m : m * R)) * 8);
+                stage_octet<R, TB ? MT * 8 : 8>(xr[i], xs + ((size_t)slot * Ph::RM + (TB ? m : m * R)) * 8);
             }
         }
     }
-    lds_barrier();
+}
 
-    // ---- 2. the first P units of this wave -----------------------------------------
-    const __amdgpu_buffer_rsrc_t r0 = make_rsrc(a.W0, a.wbytes);
-    const __amdgpu_buffer_rsrc_t r1 = make_rsrc(GLU ? a.W1 : a.W0, a.wbytes);
-    const uint32_t voff = 16u * (uint32_t)lane;
-    u32x4 q[P][5];
-    auto issue = [&](u32x4 (&d)[5], int u) __attribute__((always_inline)) {
-        uint32_t off = a.wbytes, step = 1024u;  // past the range: zeros, no memory traffic
-        int n = 0;
-        if (u < U) {
-            const UnitPos p = unit_pos<NT>(a, wk, u);
-            off = p.off;
-            step = p.step;
-            n = p.n;
-        }
-        // Wave-uniform by construction; saying so keeps the loads out of
-        // per-lane (waterfall) loops.
-        off = __builtin_amdgcn_readfirstlane(off);
-        step = __builtin_amdgcn_readfirstlane(step);
-        const __amdgpu_buffer_rsrc_t r = (GLU && __builtin_amdgcn_readfirstlane(n)) ? r1 : r0;
-#pragma unroll
-        for (int i = 0; i < 5; ++i) d[i] = buf_load16_so<true>(r, voff, off + step * i);
-    };
-    int uk[P];  // the unit in each ring slot (>= U: none)
-#pragma unroll
-    for (int k = 0; k < P; ++k) {
-        uk[k] = w + k * NW;
-        issue(q[k], uk[k]);
+// The five 16-byte pieces of unit u (u >= U: past the range, zeros and no
+// memory traffic). Offsets are wave-uniform by construction; saying so keeps
+// the loads out of per-lane (waterfall) loops.
+template <bool GLU>
+__device__ __forceinline__ void issue_unit(const Gemv1Args& a, const WgWork& wk, int U, __amdgpu_buffer_rsrc_t r0,
+                                           __amdgpu_buffer_rsrc_t r1, uint32_t voff, u32x4 (&d)[5], int u) {
+    constexpr int NT = GLU ? 2 : 1;
+    uint32_t off = a.wbytes, step = 1024u;
+    int n = 0;
+    if (u < U) {
+        const UnitPos p = unit_pos<NT>(a, wk, u);
+        off = p.off;
+        step = p.step;
+        n = p.n;
     }
+    off = __builtin_amdgcn_readfirstlane(off);
+    step = __builtin_amdgcn_readfirstlane(step);
+    const __amdgpu_buffer_rsrc_t r = (GLU && __builtin_amdgcn_readfirstlane(n)) ? r1 : r0;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) d[i] = buf_load16_so<true>(r, voff, off + step * i);
+}
 
-    // ---- 3. stream: dequantize + MFMA one unit, refill its ring slot ---------------
-    // Lane base of the A operand: slot g, row j of the (first) block (rows >= AR
-    // read row AR - 1; their D rows are never used).
-    const __bf16* xa = xs + ((size_t)g * RM + min(j, AR - 1)) * 8;
-    // Every pass refills every slot (past the last unit the loads read past the
-    // buffer and return zeros), so the loads in flight per slot are the same on
-    // every path and the compiler's wait counts keep P - 1 units in flight.
-    for (bool live = true; live;) {
-        live = false;
+// ---- 3. dequantize + MFMA unit u (held in q) into its LDS slot ----------------------
+// Lane base of the A operand: slot g, row j of the (first) block (rows >= AR
+// read row AR - 1; their D rows are never used). The last super-step holds
+// ng_last lanes of g per row; the other lanes read the next plane's bytes:
+// their scales are zeroed.
+template <int R, bool GLU, int MT, bool TB>
+__device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& wk, const u32x4 (&q)[5], int u,
+                                             const __bf16* xs, f32x4* part, int lane) {
+    using Ph = PhaseT<R, false, GLU, MT, TB>;
+    constexpr int RM = Ph::RM, AR = Ph::AR, DL = Ph::DL;
+    const int j = lane & 15;
+    const int g = lane >> 4;
+    const UnitPos p = unit_pos<Ph::NT>(a, wk, u);
+    const bool valid = p.ss != a.nss - 1 || g < a.ng_last;
+    const __bf16* xu = xs + ((size_t)g * RM + min(j, AR - 1)) * 8 + (size_t)(p.ss - wk.s0) * 16 * 4 * RM * 8;
+    f32x4 t0 = {0.f, 0.f, 0.f, 0.f}, t1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int k = 0; k < P; ++k) {
-            int un = 0;
-            if (lane == 0) un = __hip_atomic_fetch_add(next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            un = __builtin_amdgcn_readfirstlane(un);
-            const int u = uk[k];
-            if (u < U) {
-                const UnitPos p = unit_pos<NT>(a, wk, u);
-                // The last super-step holds ng_last lanes of g per row; the
-                // other lanes read the next plane's bytes: zero their scales.
-                const bool valid = p.ss != a.nss - 1 || g < a.ng_last;
-                const __bf16* xu = xa + (size_t)(p.ss - wk.s0) * 16 * 4 * RM * 8;
-                f32x4 t0 = {0.f, 0.f, 0.f, 0.f}, t1 = {0.f, 0.f, 0.f, 0.f};
+    for (int bl = 0; bl < 4; ++bl) {
+        const int w4 = 5 * bl + 4;
+        const uint32_t sd = valid ? (uint32_t)q[w4 >> 2][w4 & 3] : 0u;
+        const Scale2 sc = make_scale2(scale_of(sd));
 #pragma unroll
-                for (int bl = 0; bl < 4; ++bl) {
-                    const int w4 = 5 * bl + 4;
-                    const uint32_t sd = valid ? (uint32_t)q[k][w4 >> 2][w4 & 3] : 0u;
-                    const Scale2 sc = make_scale2(scale_of(sd));
+        for (int t = 0; t < 4; ++t) {
+            const int wi = 5 * bl + t;
+            const bf16x8 bv = dequant8_mix((uint32_t)q[wi >> 2][wi & 3], sc);
 #pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        const int wi = 5 * bl + t;
-                        const bf16x8 bv = dequant8_mix((uint32_t)q[k][wi >> 2][wi & 3], sc);
-#pragma unroll
-                        for (int pb = 0; pb < (TB ? R : 1); ++pb) {
-                            const bf16x8 av =
-                                *reinterpret_cast<const bf16x8*>(xu + ((bl * 4 + t) * 4 * RM + pb * MT) * 8);
-                            if (t & 1)
-                                t1 = mfma16x16x32(av, bv, t1);
-                            else
-                                t0 = mfma16x16x32(av, bv, t0);
-                        }
-                    }
-                }
-                if (lane < DL) part[(size_t)u * DL + lane] = t0 + t1;
+            for (int pb = 0; pb < (TB ? R : 1); ++pb) {
+                const bf16x8 av = *reinterpret_cast<const bf16x8*>(xu + ((bl * 4 + t) * 4 * RM + pb * MT) * 8);
+                if (t & 1)
+                    t1 = mfma16x16x32(av, bv, t1);
+                else
+                    t0 = mfma16x16x32(av, bv, t0);
             }
-            issue(q[k], un);
-            uk[k] = un;
-            live |= un < U;
         }
     }
-    lds_barrier();
+    if (lane < DL) part[(size_t)u * DL + lane] = t0 + t1;
+}
 
-    // ---- 4. per row: sum the unit slots in a fixed order ---------------------------
-    // D row m * R + p (token m, term p; term-major: row m, terms summed) of
-    // column jj sits in slot lane 16 * (row / 4) + jj, element row % 4. Wave w takes rows 16 w .. 16 w + 15
-    // of the workgroup (then 16 NW further on); four lanes share a row: lane c
-    // sums super-steps c, c + 4, ... in ascending order and the four partial
-    // sums combine in a fixed butterfly, so the result does not depend on
-    // timing; lane 0 of the four finishes the row -- the epilogue is spread
-    // over nt waves.
+template <bool THROUGH>
+__device__ __forceinline__ void ystore(const Gemv1Args& a, int m, int row, float out) {
+    if (a.Yb) {
+        const uint16_t b = __builtin_bit_cast(uint16_t, (__bf16)out);
+        if constexpr (THROUGH)
+            __hip_atomic_store(&a.Yb[(size_t)m * a.ldy + row], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            a.Yb[(size_t)m * a.ldy + row] = b;
+    } else {
+        if constexpr (THROUGH)
+            __hip_atomic_store(&a.Y[(size_t)m * a.ldy + row], out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            a.Y[(size_t)m * a.ldy + row] = out;
+    }
+}
+
+// ---- 4. per row: sum the unit slots in a fixed order --------------------------------
+// D row m * R + p (token m, term p; term-major: row m, terms summed) of
+// column jj sits in slot lane 16 * (row / 4) + jj, element row % 4. Wave w
+// takes rows 16 w .. 16 w + 15 of the workgroup (then 16 NW further on); four
+// lanes share a row: lane c sums super-steps c, c + 4, ... in ascending order
+// and the four partial sums combine in a fixed butterfly, so the result does
+// not depend on timing; lane c of the four finishes tokens c, c + 4, ...
+// Split K: this workgroup's shares go out instead, and the last workgroup of
+// the tile group adds them (section 5). THROUGH: the outputs are read later in
+// the same launch by other workgroups (agent-scope stores).
+template <int NW, int R, bool GLU, int MT, bool TB, bool THROUGH>
+__device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk, const f32x4* part, int* flag,
+                                            int tid) {
+    using Ph = PhaseT<R, false, GLU, MT, TB>;
+    constexpr int NT = Ph::NT, DL = Ph::DL;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 3;
     const bool split = a.ks > 1;
     for (int r0 = w * 16; r0 < wk.nt * 16; r0 += NW * 16) {
@@ -315,7 +311,6 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
             }
         const int row = (wk.rt0 + tl) * 16 + jj;
         if (row >= a.N) continue;
-        // Lane c of the four finishes tokens c, c + 4, ... (each holds every sum).
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             if ((m & 3) != c || m >= a.M) continue;
@@ -330,10 +325,7 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
             }
             float out = y[m][0];
             if constexpr (GLU) out = bf16_round(glu_act(bf16_round(y[m][0]), bf16_round(y[m][NT - 1]), a.act));
-            if (a.Yb)
-                a.Yb[(size_t)m * a.ldy + row] = __builtin_bit_cast(uint16_t, (__bf16)out);
-            else
-                a.Y[(size_t)m * a.ldy + row] = out;
+            ystore<THROUGH>(a, m, row, out);
         }
     }
     if (!split) return;
@@ -347,10 +339,10 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     __syncthreads();
     if (tid == 0) {
         const uint32_t old = __hip_atomic_fetch_add(&a.cnt[wk.tg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *next = old == (uint32_t)(a.ks - 1) ? 1 : 0;
+        *flag = old == (uint32_t)(a.ks - 1) ? 1 : 0;
     }
     __syncthreads();
-    if (!*next) return;
+    if (!*flag) return;
     const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.part, kPartBytes);
     for (int i = tid; i < wk.nt * 16 * MT; i += 64 * NW) {  // one (row, token) per thread
         const int r = i / MT, m = i - r * MT;
@@ -367,12 +359,66 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
                 y[n] += __builtin_bit_cast(float, buf_load4_sc1(rp, base + (uint32_t)(((size_t)kq * MT * NT + n) * 4)));
         float out = y[0];
         if constexpr (GLU) out = bf16_round(glu_act(bf16_round(y[0]), bf16_round(y[NT - 1]), a.act));
-        if (a.Yb)
-            a.Yb[(size_t)m * a.ldy + row] = __builtin_bit_cast(uint16_t, (__bf16)out);
-        else
-            a.Y[(size_t)m * a.ldy + row] = out;
+        ystore<THROUGH>(a, m, row, out);
     }
     if (tid == 0) __hip_atomic_store(&a.cnt[wk.tg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int NW, int P, int R, bool XB, bool GLU, int MT, bool TB>
+__global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
+    using Ph = PhaseT<R, XB, GLU, MT, TB>;
+    constexpr int NT = Ph::NT, RM = Ph::RM, DL = Ph::DL;
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const WgWork wk = wg_work(a, blockIdx.x);
+    const int U = wk.nt * wk.nsw * NT;
+    __bf16* xs = reinterpret_cast<__bf16*>(smem);
+    f32x4* part = reinterpret_cast<f32x4*>(smem + (size_t)wk.nsw * 1024 * RM);
+    // Unit counter of the workgroup, after the unit slots: the first P * NW
+    // units go to the waves statically, the rest to whichever wave frees a ring
+    // slot first, so a wave whose loads come back late does fewer units.
+    int* next = reinterpret_cast<int*>(part + (size_t)U * DL);
+    if (tid == 0) *next = P * NW;
+
+    // The activation is staged before any weight load: queued behind the
+    // weight loads of every CU it would wait for (bytes in flight) / bandwidth.
+    stage_acts<NW, R, XB, MT, TB, false>(a, wk, xs, tid);
+    lds_barrier();
+
+    // ---- 2. the first P units of this wave -----------------------------------------
+    const __amdgpu_buffer_rsrc_t r0 = make_rsrc(a.W0, a.wbytes);
+    const __amdgpu_buffer_rsrc_t r1 = make_rsrc(GLU ? a.W1 : a.W0, a.wbytes);
+    const uint32_t voff = 16u * (uint32_t)lane;
+    u32x4 q[P][5];
+    int uk[P];  // the unit in each ring slot (>= U: none)
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        uk[k] = w + k * NW;
+        issue_unit<GLU>(a, wk, U, r0, r1, voff, q[k], uk[k]);
+    }
+
+    // ---- 3. stream: dequantize + MFMA one unit, refill its ring slot ---------------
+    // Every pass refills every slot (past the last unit the loads read past the
+    // buffer and return zeros), so the loads in flight per slot are the same on
+    // every path and the compiler's wait counts keep P - 1 units in flight.
+    for (bool live = true; live;) {
+        live = false;
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            int un = 0;
+            if (lane == 0) un = __hip_atomic_fetch_add(next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            un = __builtin_amdgcn_readfirstlane(un);
+            if (uk[k] < U) compute_unit<R, GLU, MT, TB>(a, wk, q[k], uk[k], xs, part, lane);
+            issue_unit<GLU>(a, wk, U, r0, r1, voff, q[k], un);
+            uk[k] = un;
+            live |= un < U;
+        }
+    }
+    lds_barrier();
+    finish_rows<NW, R, GLU, MT, TB, false>(a, wk, part, next, tid);
 }
 
 struct DevInfo {
@@ -513,15 +559,53 @@ int max_tokens(const GemvLaunch& L) {
 
 bool gemv1_ok(const GemvLaunch& L) { return L.M >= 1 && max_tokens(L) > 0; }
 
-int launch_gemv1(const GemvLaunch& L, hipStream_t s) {
-    const int mmax = L.M >= 1 ? max_tokens(L) : 0;
-    if (!mmax) return fail(ALV_ERR_ARG, "streaming GEMV: shape M=%d N=%d K=%d outside its plan", L.M, L.N, L.K);
+namespace {
+
+// Kernel arguments of tokens [m0, m0 + m) of L under plan p.
+int fill_args(const GemvLaunch& L, const Gemv1Plan& p, int m0, int m, hipStream_t s, Gemv1Args* out) {
     const TileGeom tg = tile_geom(L.K);
     const int RT = (L.N + 15) / 16;
     const uint64_t wbytes = (uint64_t)RT * tg.rtb;
     if (wbytes >= 0xFFFFE000ull)
         return fail(ALV_ERR_RANGE, "weight matrix of %llu bytes exceeds the 4 GiB buffer range", (unsigned long long)wbytes);
     const int ES = L.Xb ? 2 : 4;
+    const uint64_t xbytes = ((uint64_t)(m - 1) * L.ldx + L.K) * ES;
+    if (xbytes >= 0x7FFFFF00ull) return fail(ALV_ERR_RANGE, "activation buffer exceeds the 2 GiB range");
+    Gemv1Args a{};
+    if (p.ks > 1) {
+        Workspace ws;
+        if (int rc = get_workspace(s, kWsWords, &ws)) return rc;
+        a.cnt = ws.counters + kSyncWords;
+        a.part = ws.part;
+    }
+    a.W0 = L.W0;
+    a.W1 = L.W1;
+    a.X = L.Xb ? (const void*)(L.Xb + (size_t)m0 * L.ldx) : (const void*)(L.X + (size_t)m0 * L.ldx);
+    a.Y = L.Y ? L.Y + (size_t)m0 * L.ldy : nullptr;
+    a.Yb = L.Yb ? L.Yb + (size_t)m0 * L.ldy : nullptr;
+    a.wbytes = (uint32_t)wbytes;
+    a.rtb = tg.rtb;
+    a.xbytes = (uint32_t)xbytes;
+    a.N = L.N;
+    a.K = L.K;
+    a.nss = tg.nss;
+    a.ng_last = tg.ng_last;
+    a.ldx = L.ldx;
+    a.ldy = L.ldy;
+    a.M = m;
+    a.rt_q = p.rt_q;
+    a.rt_r = p.rt_r;
+    a.ks = p.ks;
+    a.act = L.act;
+    *out = a;
+    return ALV_OK;
+}
+
+}  // namespace
+
+int launch_gemv1(const GemvLaunch& L, hipStream_t s) {
+    const int mmax = L.M >= 1 ? max_tokens(L) : 0;
+    if (!mmax) return fail(ALV_ERR_ARG, "streaming GEMV: shape M=%d N=%d K=%d outside its plan", L.M, L.N, L.K);
     // Groups of as equal a size as the capacity allows (16 tokens at a
     // capacity of 5: four groups of 4, not 5 + 5 + 5 + 1).
     const int ngroups = (L.M + mmax - 1) / mmax;
@@ -530,34 +614,8 @@ int launch_gemv1(const GemvLaunch& L, hipStream_t s) {
         const int m = std::min(gsize, L.M - m0);
         Gemv1Plan p;
         if (!plan_gemv1(L, m, &p)) return fail(ALV_ERR_ARG, "streaming GEMV: no plan for %d tokens", m);
-        const uint64_t xbytes = ((uint64_t)(m - 1) * L.ldx + L.K) * ES;
-        if (xbytes >= 0x7FFFFF00ull) return fail(ALV_ERR_RANGE, "activation buffer exceeds the 2 GiB range");
-        Gemv1Args a{};
-        if (p.ks > 1) {
-            Workspace ws;
-            if (int rc = get_workspace(s, kSyncWords + kSplitCounters, &ws)) return rc;
-            a.cnt = ws.counters + kSyncWords;
-            a.part = ws.part;
-        }
-        a.W0 = L.W0;
-        a.W1 = L.W1;
-        a.X = L.Xb ? (const void*)(L.Xb + (size_t)m0 * L.ldx) : (const void*)(L.X + (size_t)m0 * L.ldx);
-        a.Y = L.Y ? L.Y + (size_t)m0 * L.ldy : nullptr;
-        a.Yb = L.Yb ? L.Yb + (size_t)m0 * L.ldy : nullptr;
-        a.wbytes = (uint32_t)wbytes;
-        a.rtb = tg.rtb;
-        a.xbytes = (uint32_t)xbytes;
-        a.N = L.N;
-        a.K = L.K;
-        a.nss = tg.nss;
-        a.ng_last = tg.ng_last;
-        a.ldx = L.ldx;
-        a.ldy = L.ldy;
-        a.M = m;
-        a.rt_q = p.rt_q;
-        a.rt_r = p.rt_r;
-        a.ks = p.ks;
-        a.act = L.act;
+        Gemv1Args a;
+        if (int rc = fill_args(L, p, m0, m, s, &a)) return rc;
         const hipError_t e = launch_shape(a, L, p.sh, p.tg * p.ks, p.lds, s);
         if (int rc = hip_check(e, "q4_gemv1_kernel launch")) return rc;
     }

@@ -82,6 +82,8 @@ constexpr int kSyncWords = kSyncError + 1;
 // Split-K arrival counters of the streaming GEMV, after the executor's words
 // (one per tile group of a launch).
 constexpr int kSplitCounters = 1024;
+// Words of a stream's set: the executor's, then the split-K counters.
+constexpr int kWsWords = kSyncWords + kSplitCounters;
 
 // Device-side descriptor of one op (kernel argument; every field is
 // wave-uniform). Work split: a workgroup of 16 waves holds rtw row-tile slots

@@ -458,6 +458,32 @@ def test_ffn_parity(orc, dev, H, I, M, act, kind):
     ffn.close()
 
 
+def test_ffn_one_token_sequence(orc, dev):
+    """One-token calls back to back: each token's output follows its own
+    activation, never the one a previous call left in the handle's scratch, and
+    a repeated token repeats bit for bit."""
+    import alveare_amd as aa
+
+    H, I = 3840, 15360
+    seed = orc.seed_for(2, 0) + 11
+    Wg, Wu, Wd = orc.synth_q4(I, H, seed), orc.synth_q4(I, H, seed + 1), orc.synth_q4(H, I, seed + 2)
+    ffn = aa.pack_ffn_fused_weights(to_dev(Wg, dev), to_dev(Wu, dev), to_dev(Wd, dev), H, I)
+    xs = [orc.synth_normal(H, seed + 10 + t) for t in range(3)]
+    outs = []
+    for t, x in enumerate(xs):
+        y = torch.empty((1, H), dtype=torch.float32, device=dev)
+        ffn(to_dev(x[None, :], dev), y, 1)
+        A = ffn.last_activation(1).cpu().numpy()
+        st = parity.ffn_check(orc, Wg, Wu, Wd, x, H, I, 0, y.cpu().numpy()[0], A[0])
+        _say(f"  token {t}: {st}")
+        outs.append(y.clone())
+    y = torch.empty((1, H), dtype=torch.float32, device=dev)
+    ffn(to_dev(xs[0][None, :], dev), y, 1)
+    assert torch.equal(y, outs[0])
+    aa.check_async()
+    ffn.close()
+
+
 def test_ffn_deterministic(orc, dev):
     import alveare_amd as aa
 
