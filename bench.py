@@ -164,6 +164,36 @@ def profile_pass(torch, aa, dev) -> int:
 _CAPTURE_STREAM = None
 
 
+def read_floor(torch, aa, dev) -> dict:
+    """The practical ceiling per launch: a plain streaming read
+    (alv_stream_read) of each op's weight bytes, from distinct regions of a
+    2 GiB buffer (far beyond the Infinity Cache), timed like the ops."""
+    L = aa.lib()
+    big = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(2048, dtype=torch.int32, device=dev)
+    sizes = {"qkv": q4_bytes(N_QKV, H), "o": q4_bytes(H, K_O), "ffn_gate_up": 2 * q4_bytes(I_FF, H),
+             "ffn_down": q4_bytes(H, I_FF)}
+    out = {}
+    for k, nbytes in sizes.items():
+        nb = nbytes // 256 * 256
+        n = min(48, big.numel() // nb)
+
+        def fn(nb=nb, n=n):
+            st = torch.cuda.current_stream().cuda_stream
+            for i in range(n):
+                rc = L.alv_stream_read(big.data_ptr() + i * nb, nb, sink.data_ptr(), st)
+                if rc:
+                    raise RuntimeError(f"alv_stream_read failed ({rc})")
+
+        us = graph_us(torch, fn, 3, n)
+        out[k] = {"us": round(us, 3), "GBps": round(nb / us / 1e3, 1)}
+    layer = out["qkv"]["us"] + out["o"]["us"] + out["ffn_gate_up"]["us"] + out["ffn_down"]["us"]
+    out["layer_us"] = round(layer, 3)
+    del big
+    torch.cuda.empty_cache()
+    return out
+
+
 def graph_us(torch, fn, reps: int, per: int) -> float:
     """Mean time of one of the `per` launches `fn` enqueues: a HIP graph of
     fn replayed `reps` times between HIP events on the replay stream."""
@@ -245,6 +275,8 @@ def main() -> int:
         us = graph_us(torch, fn, 3, nl * per)
         breakdown[k] = {"us": round(us, 3), "GBps": round(lb[k] / us / 1e3, 1)}
 
+    floor = read_floor(torch, aa, dev)
+
     # Whole step from a HIP graph (the launch-bound loop of 3 x 48 ops).
     for _ in range(max(1, args.warmup)):
         step()
@@ -316,6 +348,7 @@ def main() -> int:
         "us_per_layer": round(ms * 1e3 / nl, 3),
         "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
         "breakdown": breakdown,
+        "read_floor": floor,
         "roofline": {
             "bound": "hbm",
             "kernel": ROOFLINE_KERNEL + " (ffn gate/up + GeGLU, 15360x3840 x2)",

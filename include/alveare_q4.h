@@ -206,6 +206,16 @@ int alv_check_async(void* stream);
  */
 int alv_dequant_q4(const uint8_t* W, uint16_t* out, int N, int K, void* stream);
 
+/*
+ * Read `bytes` at `buf` once with a plain streaming kernel and XOR-fold them
+ * into sink[0], sink[32], ..., sink[32 * 63] (sink: 2048 words of device
+ * memory; the XOR of those 64 words changes by the XOR of every word read).
+ * Measurement aid with no counterpart in the reference: the practical HBM
+ * read ceiling for a launch of that size, which the benchmark reports beside
+ * the Q4 kernels. buf and bytes need 16-byte alignment.
+ */
+int alv_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

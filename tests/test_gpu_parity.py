@@ -531,3 +531,16 @@ def test_dispatch_entry_points(orc, dev):
     Yb = d.run_gemm_npu(rw, torch.from_numpy(Xb).to(torch.bfloat16)).float().cpu().numpy()
     assert parity.max_rel(Yb, orc.bf16_round(orc.gemm_q(W, Xb, 5, N, K))) <= 2 ** -8
     del st
+
+
+def test_stream_read_probe(dev):
+    """alv_stream_read reads every byte: its XOR fold equals the host's."""
+    import alveare_amd as aa
+
+    for n in (4, 1 << 20, (1 << 20) + 12):  # words: one chunk, 4 MiB, a ragged tail
+        buf = torch.randint(-2**31, 2**31 - 1, (n,), dtype=torch.int32, device=dev)
+        sink = torch.zeros(2048, dtype=torch.int32, device=dev)
+        rc = aa.lib().alv_stream_read(buf.data_ptr(), n * 4, sink.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        want = np.bitwise_xor.reduce(buf.cpu().numpy().view(np.uint32))
+        assert np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32)[::32]) == want
