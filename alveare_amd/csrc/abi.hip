@@ -4,6 +4,7 @@
 
 #include <map>
 #include <mutex>
+#include <tuple>
 #include <utility>
 
 #include "q4_host.h"
@@ -28,7 +29,7 @@ int hip_check(hipError_t e, const char* what) {
 }
 
 namespace {
-// Synchronisation words (and split-K scratch): one block per device holding
+// Synchronisation words: one block per device holding
 // kWsStreams sets, handed out to streams on first use. The blocks are
 // allocated (the words zeroed) at the first call on the device; a stream's
 // later first use takes a set without allocating, so it may happen during
@@ -38,7 +39,6 @@ std::mutex g_ws_mu;
 struct DeviceWs {
     uint32_t* block = nullptr;
     size_t words = 0;  // per set
-    uint8_t* part = nullptr;  // kPartBytes per set
     std::map<hipStream_t, int> slot;
 };
 std::map<int, DeviceWs> g_ws;
@@ -62,12 +62,6 @@ int get_workspace(hipStream_t s, size_t counters, Workspace* out) {
             w.block = nullptr;
             return fail(ALV_ERR_HIP, "hipMalloc of the synchronisation words failed");
         }
-        if (hipMalloc(&w.part, kPartBytes * kWsStreams) != hipSuccess) {
-            (void)hipFree(w.block);
-            w.block = nullptr;
-            w.part = nullptr;
-            return fail(ALV_ERR_HIP, "hipMalloc of the split-K scratch failed");
-        }
         if (int rc = hip_check(hipMemset(w.block, 0, words * kWsStreams * sizeof(uint32_t)), "hipMemset")) return rc;
         w.words = words;
     }
@@ -84,7 +78,6 @@ int get_workspace(hipStream_t s, size_t counters, Workspace* out) {
     }
     out->counters = w.block + (size_t)idx * w.words;
     out->counter_count = w.words;
-    out->part = reinterpret_cast<float*>(w.part + (size_t)idx * kPartBytes);
     return ALV_OK;
 }
 
@@ -93,27 +86,27 @@ struct Scratch {
     void* p = nullptr;
     size_t cap = 0;
 };
-std::map<std::pair<int, hipStream_t>, Scratch> g_scratch;
+std::map<std::tuple<int, hipStream_t, int>, Scratch> g_scratch;
 }  // namespace
 
-int get_scratch(hipStream_t s, size_t bytes, void** out) {
+int get_scratch(hipStream_t s, int slot, size_t bytes, void** out) {
     int dev = 0;
     if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    Scratch& sc = g_scratch[{dev, s}];
+    Scratch& sc = g_scratch[{dev, s, slot}];
     if (bytes > sc.cap) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         if (int rc = hip_check(hipStreamIsCapturing(s, &cs), "hipStreamIsCapturing")) return rc;
         if (cs != hipStreamCaptureStatusNone)
-            return fail(ALV_ERR_ARG, "prefill scratch of %zu bytes must grow, which cannot happen during graph capture: "
-                        "run one call of this size on this stream before capturing", bytes);
+            return fail(ALV_ERR_ARG, "scratch of %zu bytes must grow, which cannot happen during graph capture: "
+                        "run one call of this shape on this stream before capturing", bytes);
         if (int rc = hip_check(hipStreamSynchronize(s), "hipStreamSynchronize")) return rc;
         if (sc.p) (void)hipFree(sc.p);
         sc.p = nullptr;
         sc.cap = 0;
         const size_t cap = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
-        if (int rc = hip_check(hipMalloc(&sc.p, cap), "hipMalloc(prefill scratch)")) return rc;
-        if (int rc = hip_check(hipMemsetAsync(sc.p, 0, cap, s), "hipMemsetAsync(prefill scratch)")) return rc;
+        if (int rc = hip_check(hipMalloc(&sc.p, cap), "hipMalloc(scratch)")) return rc;
+        if (int rc = hip_check(hipMemsetAsync(sc.p, 0, cap, s), "hipMemsetAsync(scratch)")) return rc;
         sc.cap = cap;
     }
     *out = sc.p;

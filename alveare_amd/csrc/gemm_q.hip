@@ -441,7 +441,7 @@ int launch_gemm_tiled(const GemvLaunch& L, hipStream_t s) {
     const size_t term_bytes = xf32 ? 3 * tstride * sizeof(uint16_t) : 0;
     void* scratch = nullptr;
     if (ks > 1 || xf32) {
-        if (6 * tstride >= 0x7FFFFF00ull || get_scratch(s, cnt_bytes + flag_bytes + part_bytes + term_bytes, &scratch)) {
+        if (6 * tstride >= 0x7FFFFF00ull || get_scratch(s, kScratchGemm, cnt_bytes + flag_bytes + part_bytes + term_bytes, &scratch)) {
             // No scratch (a graph capture that would have to grow it): one
             // launch over all of K, activations split inside the kernel.
             clear_error();

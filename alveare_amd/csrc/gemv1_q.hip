@@ -2,7 +2,7 @@
 // gfx950: the kernel behind alv_gemv_q / alv_gemv / alv_ffn_fused /
 // alv_chain_run for M <= 16 (the decode step of runtime/py/model.py:632-818,
 // where every projection and FFN half is a matrix-vector product, and the
-// small-M batches of speculative verification), up to four tokens per launch.
+// small-M batches of speculative verification), up to 16 tokens per launch.
 //
 // HBM-bound: every weight byte is read once per launch, with 16-byte
 // nontemporal buffer loads, and dequantized in registers
@@ -45,6 +45,7 @@ struct Gemv1Args {
     float* Y;           // fp32 output, or
     uint16_t* Yb;       // bf16 output (bit patterns); token m at m * ldy
     float* part;        // split-K partial sums, [row][ks][token][matrix] (ks > 1)
+    uint32_t pbytes;    // bytes of part
     uint32_t* cnt;      // split-K arrivals per tile group (zero between launches)
     uint32_t wbytes;    // bytes of one matrix (row tiles x rtb)
     uint32_t rtb;       // bytes per row tile
@@ -343,7 +344,7 @@ __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk
     }
     __syncthreads();
     if (!*flag) return;
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.part, kPartBytes);
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.part, a.pbytes);
     for (int i = tid; i < wk.nt * 16 * MT; i += 64 * NW) {  // one (row, token) per thread
         const int r = i / MT, m = i - r * MT;
         const int row = wk.rt0 * 16 + r;
@@ -464,8 +465,9 @@ constexpr int kP = 1;
 
 // Token capacity of a launch, activation terms per token and row layout:
 // fp32 activations take the exact three-term split, token-major up to 5
-// tokens (15 A rows, one MFMA per weight octet), term-major for 8 (three
-// MFMAs); bf16 activations one term, up to 16 tokens.
+// tokens (15 A rows, one MFMA per weight octet), term-major for 8 and 16
+// (three MFMAs; 16 tokens fill every A row, and K splits until the 48 staged
+// rows fit the LDS); bf16 activations one term, up to 16 tokens.
 struct Shape {
     int mt, r;
     bool tb;
@@ -480,7 +482,8 @@ Shape shape_for(const GemvLaunch& L, int m) {
     if (m <= 2) return {m, 3, false};
     if (m <= 4) return {4, 3, false};
     if (m <= 5) return {5, 3, false};
-    return {8, 3, true};
+    if (m <= 8) return {8, 3, true};
+    return {16, 3, true};
 }
 
 hipError_t launch_shape(const Gemv1Args& a, const GemvLaunch& L, Shape sh, int groups, size_t lds, hipStream_t s) {
@@ -499,7 +502,8 @@ hipError_t launch_shape(const Gemv1Args& a, const GemvLaunch& L, Shape sh, int g
             case 2: return launch_k<kP, 3, false, true, 2>(a, groups, lds, s);
             case 4: return launch_k<kP, 3, false, true, 4>(a, groups, lds, s);
             case 5: return launch_k<kP, 3, false, true, 5>(a, groups, lds, s);
-            default: return launch_k<kP, 3, false, true, 8, true>(a, groups, lds, s);
+            case 8: return launch_k<kP, 3, false, true, 8, true>(a, groups, lds, s);
+            default: return launch_k<kP, 3, false, true, 16, true>(a, groups, lds, s);
         }
     }
     switch (sh.mt) {
@@ -507,7 +511,8 @@ hipError_t launch_shape(const Gemv1Args& a, const GemvLaunch& L, Shape sh, int g
         case 2: return launch_k<kP, 3, false, false, 2>(a, groups, lds, s);
         case 4: return launch_k<kP, 3, false, false, 4>(a, groups, lds, s);
         case 5: return launch_k<kP, 3, false, false, 5>(a, groups, lds, s);
-        default: return launch_k<kP, 3, false, false, 8, true>(a, groups, lds, s);
+        case 8: return launch_k<kP, 3, false, false, 8, true>(a, groups, lds, s);
+        default: return launch_k<kP, 3, false, false, 16, true>(a, groups, lds, s);
     }
 }
 
@@ -539,7 +544,7 @@ bool plan_gemv1(const GemvLaunch& L, int m, Gemv1Plan* out) {
         const int units = tiles * nsw * NT;
         p.lds = (size_t)nsw * 1024 * RM + (size_t)units * 256 * ((AR + 3) / 4) + 16;
         const size_t part = p.ks > 1 ? (size_t)RT * 16 * p.ks * p.sh.mt * NT * sizeof(float) : 0;
-        if (p.lds <= d.lds && part <= kPartBytes && (p.ks == 1 || p.tg <= kSplitCounters)) {
+        if (p.lds <= d.lds && part <= kPartMax && (p.ks == 1 || p.tg <= kSplitCounters)) {
             *out = p;
             return true;
         }
@@ -551,7 +556,7 @@ bool plan_gemv1(const GemvLaunch& L, int m, Gemv1Plan* out) {
 int max_tokens(const GemvLaunch& L) {
     Gemv1Plan p;
     for (int m : {16, 8, 5, 4, 2, 1})
-        if (m <= (L.Xb ? 16 : 8) && plan_gemv1(L, m, &p)) return m;
+        if (plan_gemv1(L, m, &p)) return m;
     return 0;
 }
 
@@ -576,7 +581,11 @@ int fill_args(const GemvLaunch& L, const Gemv1Plan& p, int m0, int m, hipStream_
         Workspace ws;
         if (int rc = get_workspace(s, kWsWords, &ws)) return rc;
         a.cnt = ws.counters + kSyncWords;
-        a.part = ws.part;
+        const size_t pb = (size_t)RT * 16 * p.ks * p.sh.mt * (L.glu ? 2 : 1) * sizeof(float);
+        void* part = nullptr;
+        if (int rc = get_scratch(s, kScratchSplit, pb, &part)) return rc;
+        a.part = static_cast<float*>(part);
+        a.pbytes = (uint32_t)pb;
     }
     a.W0 = L.W0;
     a.W1 = L.W1;

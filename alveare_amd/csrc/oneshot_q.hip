@@ -425,7 +425,7 @@ int launch_gemv(const GemvLaunch& L, hipStream_t s) {
     if (L.M < 1 || L.M > kGemvMaxM) return fail(ALV_ERR_ARG, "stream kernel takes 1 <= M <= %d (got %d)", kGemvMaxM, L.M);
     if (L.parts != 1 && L.parts != 3) return fail(ALV_ERR_ARG, "parts must be 1 or 3");
     if (L.Xb && (L.parts != 1 || L.glu)) return fail(ALV_ERR_ARG, "bf16 activations take one term and no GLU");
-    // Registered weights: the streaming kernel, up to four tokens per launch.
+    // Registered weights: the streaming kernel, up to 16 tokens per launch.
     if (gemv1_ok(L)) return launch_gemv1(L, s);
     // Token groups of at most 16 A rows whose activations (the whole K range
     // of every token of the group) fit the LDS; a shape the one-shot plan does

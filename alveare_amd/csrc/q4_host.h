@@ -20,22 +20,24 @@ int hip_check(hipError_t e, const char* what);
 // words (a set for each of up to 64 streams) are allocated at its first call,
 // which synchronises the device; later calls, a stream's first included,
 // allocate nothing.
-//
-// Each set also holds kPartBytes of partial-sum scratch for the streaming
-// GEMV's split-K launches (rewritten by every such launch before it is read).
-constexpr size_t kPartBytes = 2u << 20;
 struct Workspace {
     uint32_t* counters = nullptr;
     size_t counter_count = 0;
-    float* part = nullptr;
 };
 int get_workspace(hipStream_t s, size_t counters, Workspace* out);
 
-// Per-(device, stream) scratch of at least `bytes`, zeroed when allocated, for
-// launches whose temporaries grow with M (prefill). Growing synchronises the
-// stream and reallocates, so it cannot happen during graph capture (an error
-// then); a call that fits what the stream already holds allocates nothing.
-int get_scratch(hipStream_t s, size_t bytes, void** out);
+// Per-(device, stream, slot) scratch of at least `bytes`, zeroed when
+// allocated, for launches whose temporaries grow with their shape: slot 0 the
+// prefill GEMM's (counters, partial tiles, activation terms), slot 1 the
+// streaming GEMV's split-K partial sums (rewritten by every such launch before
+// it is read). Growing synchronises the stream and reallocates, so it cannot
+// happen during graph capture (an error then); a call that fits what the slot
+// already holds allocates nothing.
+constexpr int kScratchGemm = 0;
+constexpr int kScratchSplit = 1;
+int get_scratch(hipStream_t s, int slot, size_t bytes, void** out);
+// Largest split-K partial-sum block of one streaming GEMV launch.
+constexpr size_t kPartMax = 256u << 20;
 
 // One launch of the streaming kernel (stream_q.hip):
 //   out[m, n] = sum_k X[m, k] * dequant(W0)[n, k]            (glu == false)
