@@ -141,6 +141,10 @@ struct PhaseT {
     static constexpr int NT = GLU ? 2 : 1;
     static constexpr int ES = XB ? 2 : 4;  // activation element size
     static constexpr int RM = ARows<R, MT, TB>::RM, AR = ARows<R, MT, TB>::AR, DL = ARows<R, MT, TB>::DL;
+    // Rows per operand slot in LDS: term-major slots (24 or 48 rows, a
+    // multiple of 256 bytes apart) take one row of padding so the four lane
+    // groups of an operand read fall on different banks.
+    static constexpr int SR = RM + (TB ? 1 : 0);
     static_assert(AR <= 16, "MFMA row block");
     static_assert(!XB || R == 1, "bf16 activations take one term");
 };
@@ -178,7 +182,7 @@ __device__ __forceinline__ void stage_acts(const Gemv1Args& a, const WgWork& wk,
             const int o = e - m * octs;  // relative to super-step s0
             if (e < E) {
                 const int slot = ((o >> 6) * 16 + (o & 15)) * 4 + ((o >> 4) & 3);
-                stage_octet<R, TB ? MT * 8 : 8>(xr[i], xs + ((size_t)slot * Ph::RM + (TB ? m : m * R)) * 8);
+                stage_octet<R, TB ? MT * 8 : 8>(xr[i], xs + ((size_t)slot * Ph::SR + (TB ? m : m * R)) * 8);
             }
         }
     }
@@ -215,12 +219,12 @@ template <int R, bool GLU, int MT, bool TB>
 __device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& wk, const u32x4 (&q)[5], int u,
                                              const __bf16* xs, f32x4* part, int lane) {
     using Ph = PhaseT<R, false, GLU, MT, TB>;
-    constexpr int RM = Ph::RM, AR = Ph::AR, DL = Ph::DL;
+    constexpr int SR = Ph::SR, AR = Ph::AR, DL = Ph::DL;
     const int j = lane & 15;
     const int g = lane >> 4;
     const UnitPos p = unit_pos<Ph::NT>(a, wk, u);
     const bool valid = p.ss != a.nss - 1 || g < a.ng_last;
-    const __bf16* xu = xs + ((size_t)g * RM + min(j, AR - 1)) * 8 + (size_t)(p.ss - wk.s0) * 16 * 4 * RM * 8;
+    const __bf16* xu = xs + ((size_t)g * SR + min(j, AR - 1)) * 8 + (size_t)(p.ss - wk.s0) * 16 * 4 * SR * 8;
     f32x4 t0 = {0.f, 0.f, 0.f, 0.f}, t1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int bl = 0; bl < 4; ++bl) {
@@ -233,7 +237,7 @@ __device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& w
             const bf16x8 bv = dequant8_mix((uint32_t)q[wi >> 2][wi & 3], sc);
 #pragma unroll
             for (int pb = 0; pb < (TB ? R : 1); ++pb) {
-                const bf16x8 av = *reinterpret_cast<const bf16x8*>(xu + ((bl * 4 + t) * 4 * RM + pb * MT) * 8);
+                const bf16x8 av = *reinterpret_cast<const bf16x8*>(xu + ((bl * 4 + t) * 4 * SR + pb * MT) * 8);
                 if (t & 1)
                     t1 = mfma16x16x32(av, bv, t1);
                 else
@@ -368,7 +372,7 @@ __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk
 template <int NW, int P, int R, bool XB, bool GLU, int MT, bool TB>
 __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     using Ph = PhaseT<R, XB, GLU, MT, TB>;
-    constexpr int NT = Ph::NT, RM = Ph::RM, DL = Ph::DL;
+    constexpr int NT = Ph::NT, SR = Ph::SR, DL = Ph::DL;
     extern __shared__ __align__(16) unsigned char smem[];
 
     const int tid = threadIdx.x;
@@ -377,7 +381,7 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     const WgWork wk = wg_work(a, blockIdx.x);
     const int U = wk.nt * wk.nsw * NT;
     __bf16* xs = reinterpret_cast<__bf16*>(smem);
-    f32x4* part = reinterpret_cast<f32x4*>(smem + (size_t)wk.nsw * 1024 * RM);
+    f32x4* part = reinterpret_cast<f32x4*>(smem + (size_t)wk.nsw * 1024 * SR);
     // Unit counter of the workgroup, after the unit slots: the first P * NW
     // units go to the waves statically, the rest to whichever wave frees a ring
     // slot first, so a wave whose loads come back late does fewer units.
@@ -535,6 +539,7 @@ bool plan_gemv1(const GemvLaunch& L, int m, Gemv1Plan* out) {
     p.sh = shape_for(L, m);
     const int RM = p.sh.mt * p.sh.r;
     const int AR = p.sh.tb ? p.sh.mt : RM;
+    const int SR = RM + (p.sh.tb ? 1 : 0);  // rows per LDS operand slot (PhaseT::SR)
     for (p.ks = 1; p.ks <= 16 && p.ks <= tg.nss; p.ks *= 2) {
         p.tg = std::min(RT, std::max(1, d.cus / p.ks));
         p.rt_q = RT / p.tg;
@@ -542,7 +547,7 @@ bool plan_gemv1(const GemvLaunch& L, int m, Gemv1Plan* out) {
         const int tiles = p.rt_q + (p.rt_r ? 1 : 0);
         const int nsw = (tg.nss + p.ks - 1) / p.ks;
         const int units = tiles * nsw * NT;
-        p.lds = (size_t)nsw * 1024 * RM + (size_t)units * 256 * ((AR + 3) / 4) + 16;
+        p.lds = (size_t)nsw * 1024 * SR + (size_t)units * 256 * ((AR + 3) / 4) + 16;
         const size_t part = p.ks > 1 ? (size_t)RT * 16 * p.ks * p.sh.mt * NT * sizeof(float) : 0;
         if (p.lds <= d.lds && part <= kPartMax && (p.ks == 1 || p.tg <= kSplitCounters)) {
             *out = p;
