@@ -329,6 +329,49 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
     }
 
     // ---- epilogue: D[4g + r][j] of each 16 x 16 sub-tile ----------------------------
+    auto put = [&](int m, int n, float out) __attribute__((always_inline)) {
+        if (a.Yb)
+            a.Yb[(size_t)m * a.ldy + n] = __builtin_bit_cast(uint16_t, (__bf16)out);
+        else
+            a.Y[(size_t)m * a.ldy + n] = out;
+    };
+    if constexpr (NT == 2) {
+        // GLU: the float32 path inside the unrolled loop; the few values it
+        // cannot settle keep their (g, u) in LDS (free after the main loop)
+        // and are finished one at a time on the float64 path, so the unrolled
+        // code stays small and the accumulators stay in registers.
+        __syncthreads();
+        uint32_t* stash = reinterpret_cast<uint32_t*>(smem) + (size_t)tid * 64;
+        uint64_t miss = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = m0 + wm * 64 + i * 16 + 4 * g + r;
+                    const int n = n0 + wn * 64 + jj * 16 + j;
+                    if (m >= a.M || n >= a.N) continue;
+                    const float gb = bf16_round(acc[0][i][jj][r]), ub = bf16_round(acc[1][i][jj][r]);
+                    float v;
+                    if (glu_fast(gb, ub, a.act, &v)) {
+                        put(m, n, bf16_round(v));
+                    } else {
+                        const int e = (i * 4 + jj) * 4 + r;
+                        miss |= 1ull << e;
+                        stash[e] = (__builtin_bit_cast(uint32_t, gb) >> 16) | (__builtin_bit_cast(uint32_t, ub) & 0xFFFF0000u);
+                    }
+                }
+        while (miss) {
+            const int e = __builtin_ctzll(miss);
+            miss &= miss - 1;
+            const uint32_t pk = stash[e];
+            const float gb = __builtin_bit_cast(float, pk << 16), ub = __builtin_bit_cast(float, pk & 0xFFFF0000u);
+            const int i = e >> 4, jj = (e >> 2) & 3, r = e & 3;
+            put(m0 + wm * 64 + i * 16 + 4 * g + r, n0 + wn * 64 + jj * 16 + j, bf16_round(glu_exact(gb, ub, a.act)));
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -338,13 +381,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
                 const int m = m0 + wm * 64 + i * 16 + 4 * g + r;
                 const int n = n0 + wn * 64 + jj * 16 + j;
                 if (m >= a.M || n >= a.N) continue;
-                float out = acc[0][i][jj][r];
-                if constexpr (NT == 2)
-                    out = bf16_round(glu_act(bf16_round(acc[0][i][jj][r]), bf16_round(acc[1][i][jj][r]), a.act));
-                if (a.Yb)
-                    a.Yb[(size_t)m * a.ldy + n] = __builtin_bit_cast(uint16_t, (__bf16)out);
-                else
-                    a.Y[(size_t)m * a.ldy + n] = out;
+                put(m, n, acc[0][i][jj][r]);
             }
 }
 

@@ -101,6 +101,25 @@ extern "C" int alv_gemm_q(const uint8_t* W, const float* X, float* Y, int M, int
     return ALV_OK;
 }
 
+namespace {
+
+__global__ void __launch_bounds__(256) glu_kernel(const float* g, const float* u, float* out, int64_t n, int act) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = alv::bf16_round(alv::glu_act(g[i], u[i], act));
+}
+
+}  // namespace
+
+extern "C" int alv_glu(const float* g, const float* u, float* out, int64_t n, int act, void* stream) {
+    if (!g || !u || !out) return fail(ALV_ERR_ARG, "null pointer");
+    if (n < 0) return fail(ALV_ERR_ARG, "negative length");
+    if (act != ALV_ACT_GELU_TANH && act != ALV_ACT_SILU) return fail(ALV_ERR_ARG, "bad activation id %d", act);
+    if (n == 0) return ALV_OK;
+    const int grid = (int)std::min<int64_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(glu_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, g, u, out, n, act);
+    return hip_check(hipGetLastError(), "glu_kernel launch");
+}
+
 extern "C" int alv_dequant_q4(const uint8_t* W, uint16_t* out, int N, int K, void* stream) {
     if (int rc = check_common(W, out, out, N, K)) return rc;
     if (reinterpret_cast<uintptr_t>(out) % 16) return fail(ALV_ERR_ALIGN, "out needs 16-byte alignment");

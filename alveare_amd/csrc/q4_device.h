@@ -251,7 +251,20 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
 // np.sqrt(2/np.pi) is a float64 scalar so tanh and the two products are
 // float64, and the result reaches bf16 through fp32 (the caller rounds).
 // Contraction is off so every fp32 operation rounds where numpy's does.
-__device__ __forceinline__ float glu_act(float g, float u, int act) {
+//
+// GELU fast path, for results that reach the same bf16 value: with
+// z = sqrt(2/pi) * inner rounded to fp32, 1 + tanh(z) = 2 / (1 + e^(-2z)) has
+// no cancellation, and for z >= -7 (|2z| <= 14 where it matters) the fp32 value
+// v = (0.5 g) * that * u is within 2^-19 |V| of the reference's V (z's rounding
+// 14 * 2^-24 through the exponential, expf 1 ulp, the add, the divide and two
+// products 2^-24 each); the reference's own float64 1 + t loses at most
+// 2^-53 / (1 + tanh(-7)) < 2^-33 there. 2^-19 relative is at most 32 fp32 ulps
+// of v, so when v's bits are more than 64 ulps from the bf16 rounding midpoint
+// of its binade (low half 0x8000) and v is normal, bf16(f32(V)) = bf16(v).
+// Anything else -- z < -7, NaN, zero, tiny or huge v, near a midpoint (about
+// 0.2 % of values) -- takes the float64 path, which is the reference's.
+// The reference's arithmetic, float64 tanh and all.
+__device__ __forceinline__ float glu_exact(float g, float u, int act) {
 #pragma clang fp contract(off)
     if (act == ALV_ACT_GELU_TANH) {
         const float g3 = (g * g) * g;
@@ -260,8 +273,34 @@ __device__ __forceinline__ float glu_act(float g, float u, int act) {
         const double gl = (double)(0.5f * g) * (1.0 + t);
         return (float)(gl * (double)u);
     }
-    const float r = 1.0f / (1.0f + expf(-g));
+    // SiLU all in fp32 as numpy does it; exp(-g) correctly rounded to fp32
+    // (through float64) as the CPU's libm expf gives it, where the device's
+    // fp32 expf can be an ulp off.
+    const float e = (float)exp(-(double)g);
+    const float r = 1.0f / (1.0f + e);
     return (g * r) * u;
+}
+
+// The GELU fast path above: true (and *out) when v reaches the reference's
+// bf16 value; false for SiLU and for every case the float64 path must settle.
+__device__ __forceinline__ bool glu_fast(float g, float u, int act, float* out) {
+#pragma clang fp contract(off)
+    if (act != ALV_ACT_GELU_TANH) return false;
+    const float g3 = (g * g) * g;
+    const float inner = g + 0.044715f * g3;
+    const double zd = 0.7978845608028654 * (double)inner;
+    if (!(zd >= -7.0)) return false;
+    const float z = (float)zd;
+    const float v = ((0.5f * g) * (2.0f / (1.0f + expf(-2.0f * z)))) * u;
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const uint32_t mag = b & 0x7FFFFFFFu;
+    *out = v;
+    return mag >= 0x04000000u && mag < 0x7E800000u && (b & 0xFFFFu) - 0x7FC0u > 0x80u;
+}
+
+__device__ __forceinline__ float glu_act(float g, float u, int act) {
+    float v;
+    return glu_fast(g, u, act, &v) ? v : glu_exact(g, u, act);
 }
 
 }  // namespace alv

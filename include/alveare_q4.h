@@ -207,6 +207,14 @@ int alv_check_async(void* stream);
 int alv_dequant_q4(const uint8_t* W, uint16_t* out, int N, int K, void* stream);
 
 /*
+ * out[i] = bf16(act(g[i]) * u[i]) (as fp32) with the arithmetic of the FFN
+ * epilogue, act = ALV_ACT_GELU_TANH or ALV_ACT_SILU. Test / parity entry
+ * point: the reference evaluates this elementwise on the CPU
+ * (runtime/py/model.py:800-803 for GeGLU, :856 for SiLU).
+ */
+int alv_glu(const float* g, const float* u, float* out, int64_t n, int act, void* stream);
+
+/*
  * Read `bytes` at `buf` once with a plain streaming kernel and XOR-fold them
  * into sink[0], sink[32], ..., sink[32 * 63] (sink: 2048 words of device
  * memory; the XOR of those 64 words changes by the XOR of every word read).

@@ -544,3 +544,34 @@ def test_stream_read_probe(dev):
         assert rc == 0
         want = np.bitwise_xor.reduce(buf.cpu().numpy().view(np.uint32))
         assert np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32)[::32]) == want
+
+
+@pytest.mark.parametrize("act", [0, 1])
+def test_glu_bit_exact(orc, dev, act):
+    """The FFN epilogue's GLU (float32 fast path where it provably rounds like
+    the reference, float64 otherwise) equals the oracle's bit for bit: every
+    bf16 gate value with 2^-24 <= |g| < 2^8, both signs, against 256 up values
+    each, plus normally distributed pairs as the FFN produces them."""
+    import alveare_amd as aa
+
+    rng = np.random.default_rng(0xA1E0 + act)
+    mags = ((np.arange(127 - 24, 127 + 8, dtype=np.uint32)[:, None] << 7)
+            | np.arange(128, dtype=np.uint32)[None, :]).ravel() << 16
+    gs = np.concatenate([mags, mags | 0x80000000]).view(np.float32)
+    ug = orc.bf16_round((rng.standard_normal(256) * np.exp2(rng.integers(-8, 6, 256))).astype(np.float32))
+    g1 = np.repeat(gs, ug.size)
+    u1 = np.tile(ug, gs.size)
+    g2 = orc.bf16_round((rng.standard_normal(1 << 20) * 3.0).astype(np.float32))
+    u2 = orc.bf16_round((rng.standard_normal(1 << 20) * 3.0).astype(np.float32))
+    g = np.concatenate([g1, g2, np.zeros(4, np.float32)])
+    u = np.concatenate([u1, u2, np.array([1.0, -0.0, 0.0, 3.0], np.float32)])
+    out = torch.empty(g.size, dtype=torch.float32, device=dev)
+    gd, ud = to_dev(g, dev), to_dev(u, dev)
+    rc = aa.lib().alv_glu(gd.data_ptr(), ud.data_ptr(), out.data_ptr(), g.size, act,
+                          torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    got = out.cpu().numpy()
+    want = orc.glu(g, u, act)
+    bad = np.nonzero(got.view(np.uint32) != want.view(np.uint32))[0]
+    _say(f"  glu act={act}: {g.size} pairs, {bad.size} mismatches")
+    assert bad.size == 0, f"first mismatches at g={g[bad[:4]]}, u={u[bad[:4]]}: {got[bad[:4]]} vs {want[bad[:4]]}"
