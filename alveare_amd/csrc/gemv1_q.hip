@@ -1,4 +1,4 @@
-// Streaming Q4 GEMV on registered (tiled) weights for one to a few tokens,
+// Streaming Q4 GEMV on registered (tiled) weights for 1 to 16 tokens,
 // gfx950: the kernel behind alv_gemv_q / alv_gemv / alv_ffn_fused /
 // alv_chain_run for M <= 16 (the decode step of runtime/py/model.py:632-818,
 // where every projection and FFN half is a matrix-vector product, and the

@@ -157,8 +157,8 @@ __device__ __forceinline__ bf16x8 dequant8(uint32_t d, Scale s) {
     return r;
 }
 
-// The same eight weights with fewer instructions (the single-token kernel's
-// form; v_cvt_pk_f32_fp8 issues at a quarter of the fp32 rate). One v_bitop3
+// The same eight weights with fewer instructions (the streaming kernel's and
+// the prefill GEMM's form; v_cvt_pk_f32_fp8 issues at a quarter of the fp32 rate). One v_bitop3
 // builds two fp16 values at once, 1.0 with mantissa bits [p, p + 4) = q + 8 in
 // each half (p = 0 or 4), i.e. a = 1 + (q + 8) 2^(p - 10), and v_fma_mix_f32
 // widens a half exactly inside fma(a, S_p, C_p) with S_p = s 2^(10 - p),

@@ -55,14 +55,14 @@ def test_dequant_exhaustive_scales(orc, dev):
 
 
 def test_single_token_dequant_exact_scales(orc, dev):
-    """The single-token streaming kernel dequantizes with its own instruction
+    """The streaming kernel dequantizes with its own instruction
     sequence (q4_device.h::dequant8_mix): a one-hot x selects a dequantized
     column exactly, so every (code, scale) pair of its domain |s| < 2^112 --
     all 16 codes in both nibble positions, every such bf16 scale, subnormal
     ones included -- must match the oracle's dequant bit for bit."""
     import alveare_amd as aa
 
-    _say("single-token dequant: one-hot GEMV over all bf16 scales with |s| < 2^112")
+    _say("streaming-kernel dequant: one-hot GEMV over all bf16 scales with |s| < 2^112")
     s = np.arange(65536, dtype=np.uint32)
     exp_field = (s >> 7) & 0xFF
     s = s[exp_field <= 127 + 111]
