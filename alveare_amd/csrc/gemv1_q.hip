@@ -329,7 +329,7 @@ __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk
                 continue;
             }
             float out = y[m][0];
-            if constexpr (GLU) out = bf16_round(glu_act(bf16_round(y[m][0]), bf16_round(y[m][NT - 1]), a.act));
+            if constexpr (GLU) out = bf16_round(glu_exact(bf16_round(y[m][0]), bf16_round(y[m][NT - 1]), a.act));
             ystore<THROUGH>(a, m, row, out);
         }
     }
@@ -363,7 +363,7 @@ __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk
             for (int n = 0; n < NT; ++n)
                 y[n] += __builtin_bit_cast(float, buf_load4_sc1(rp, base + (uint32_t)(((size_t)kq * MT * NT + n) * 4)));
         float out = y[0];
-        if constexpr (GLU) out = bf16_round(glu_act(bf16_round(y[0]), bf16_round(y[NT - 1]), a.act));
+        if constexpr (GLU) out = bf16_round(glu_exact(bf16_round(y[0]), bf16_round(y[NT - 1]), a.act));
         ystore<THROUGH>(a, m, row, out);
     }
     if (tid == 0) __hip_atomic_store(&a.cnt[wk.tg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

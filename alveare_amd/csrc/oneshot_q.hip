@@ -273,7 +273,7 @@ __global__ void __launch_bounds__(kOneShotMaxThreads) q4_oneshot_kernel(OneShotA
             y[n] = yt;
         }
         float out = y[0];
-        if constexpr (GLU) out = bf16_round(glu_act(bf16_round(y[0]), bf16_round(y[NT - 1]), a.act));
+        if constexpr (GLU) out = bf16_round(glu_exact(bf16_round(y[0]), bf16_round(y[NT - 1]), a.act));
         if (a.Yb)
             a.Yb[(size_t)m * a.ldy + orow] = __builtin_bit_cast(uint16_t, (__bf16)out);
         else

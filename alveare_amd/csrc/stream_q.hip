@@ -431,7 +431,7 @@ __global__ void __launch_bounds__(kExecThreads) q4_exec_kernel(ExecArgs a) {
                                             : slot_sum_kw<1>(KW, scr, sl * KW, n, NT, m, jj);
                 // Final values, written through (a later op may read them).
                 float out = y[0];
-                if (d.glu) out = bf16_round(glu_act(bf16_round(y[0]), bf16_round(y[1]), d.act));
+                if (d.glu) out = bf16_round(glu_exact(bf16_round(y[0]), bf16_round(y[1]), d.act));
                 if (d.Yb)
                     __hip_atomic_store(&d.Yb[(size_t)m * d.ldy + row], __builtin_bit_cast(uint16_t, (__bf16)out),
                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
