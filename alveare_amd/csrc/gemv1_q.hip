@@ -1,16 +1,20 @@
-// Streaming Q4 GEMV on registered (tiled) weights for 1 to 16 tokens,
-// gfx950: the kernel behind alv_gemv_q / alv_gemv / alv_ffn_fused /
-// alv_chain_run for M <= 16 (the decode step of runtime/py/model.py:632-818,
-// where every projection and FFN half is a matrix-vector product, and the
-// small-M batches of speculative verification), up to 16 tokens per launch.
+// Streaming Q4 GEMV on registered (tiled) weights, gfx950: the kernel behind
+// alv_gemv_q / alv_gemv / alv_ffn_fused / alv_chain_run for M <= 16 (the
+// decode step of runtime/py/model.py:632-818, where every projection and FFN
+// half is a matrix-vector product, and the small-M batches of speculative
+// verification), up to 16 tokens per launch.
 //
 // HBM-bound: every weight byte is read once per launch, with 16-byte
 // nontemporal buffer loads, and dequantized in registers
 // (q4_device.h::dequant8_mix) straight into the B operand of
 // v_mfma_f32_16x16x32_bf16. The A operand holds the activations, each fp32
 // value split exactly into three bf16 terms (one term for bf16 activations),
-// token m in rows m * terms .. + terms - 1, staged once per workgroup in LDS in
-// operand order; the tokens of a launch share every dequantized weight.
+// token-major (token m in rows m * terms .. + terms - 1) or, for 8 and 16
+// tokens, term-major (see ARows), staged once per workgroup in LDS in operand
+// order; the tokens of a launch share every dequantized weight. When a
+// workgroup's activations outgrow the LDS, K is split over several workgroups
+// per row-tile group (partial sums in a per-stream scratch; the last
+// workgroup of the group adds them in split order).
 //
 // Work split. A unit is one (row tile, super-step[, matrix]) tile of the
 // registered layout: 16 rows x 512 columns, 5 KiB, read by one wave as five
