@@ -9,8 +9,8 @@
 // (q4_device.h::dequant8_mix) straight into the B operand of
 // v_mfma_f32_16x16x32_bf16. The A operand holds the activations, each fp32
 // value split exactly into three bf16 terms (one term for bf16 activations),
-// token-major (token m in rows m * terms .. + terms - 1) or, for 8 and 16
-// tokens, term-major (see ARows), staged once per workgroup in LDS in operand
+// token-major (token m in rows m * terms .. + terms - 1), in token quads
+// for 8 tokens or term-major for 16 (see ARows), staged once per workgroup in LDS in operand
 // order; the tokens of a launch share every dequantized weight. When a
 // workgroup's activations outgrow the LDS, K is split over several workgroups
 // per row-tile group (partial sums in a per-stream scratch; the last
@@ -131,11 +131,19 @@ __device__ __forceinline__ UnitPos unit_pos(const Gemv1Args& a, const WgWork& wk
 // block p = term p of every token, one MFMA per block into the same
 // accumulator, so D row m is already token m's sum. Lane l holds D rows
 // 4 (l / 16) .. + 3 of column l % 16; DL lanes hold the rows in use.
+//
+// Token quads (QUAD: 8 fp32 tokens, token-major): A block b holds tokens
+// 4b .. 4b + 3 at four rows each, the three terms and a zero row, so one
+// lane group of the D tile holds one token and each lane adds its token's
+// terms itself; two MFMAs per weight octet (term-major would take three), and
+// a unit's slot holds the token sums, MT x 16 floats.
 template <int R, int MT, bool TB>
 struct ARows {
-    static constexpr int RM = R * MT;        // rows per slot in LDS
-    static constexpr int AR = TB ? MT : RM;  // rows per A block
+    static constexpr bool QUAD = !TB && R == 3 && MT == 8;
+    static constexpr int RM = R * MT;                          // rows per slot in LDS
+    static constexpr int AR = QUAD ? 16 : (TB ? MT : RM);      // rows per A block
     static constexpr int DL = 16 * ((AR + 3) / 4);
+    static constexpr int US = QUAD ? MT * 4 : DL;              // f32x4 per unit slot
 };
 
 // Operand geometry of one phase: MT tokens x R activation terms, one or two
@@ -145,10 +153,13 @@ struct PhaseT {
     static constexpr int NT = GLU ? 2 : 1;
     static constexpr int ES = XB ? 2 : 4;  // activation element size
     static constexpr int RM = ARows<R, MT, TB>::RM, AR = ARows<R, MT, TB>::AR, DL = ARows<R, MT, TB>::DL;
+    static constexpr bool QUAD = ARows<R, MT, TB>::QUAD;
+    static constexpr int US = ARows<R, MT, TB>::US;
     // Rows per operand slot in LDS: term-major slots (24 or 48 rows, a
     // multiple of 256 bytes apart) take one row of padding so the four lane
-    // groups of an operand read fall on different banks.
-    static constexpr int SR = RM + (TB ? 1 : 0);
+    // groups of an operand read fall on different banks; token quads one zero
+    // row (row RM), which is also their padding.
+    static constexpr int SR = RM + ((TB || QUAD) ? 1 : 0);
     static_assert(AR <= 16, "MFMA row block");
     static_assert(!XB || R == 1, "bf16 activations take one term");
 };
@@ -190,6 +201,9 @@ __device__ __forceinline__ void stage_acts(const Gemv1Args& a, const WgWork& wk,
             }
         }
     }
+    if constexpr (Ph::QUAD)
+        for (int sl = tid; sl < wk.nsw * 64; sl += 64 * NW)
+            *reinterpret_cast<u32x4*>(xs + ((size_t)sl * Ph::SR + Ph::RM) * 8) = u32x4{0u, 0u, 0u, 0u};
 }
 
 // The five 16-byte pieces of unit u (u >= U: past the range, zeros and no
@@ -223,13 +237,24 @@ template <int R, bool GLU, int MT, bool TB>
 __device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& wk, const u32x4 (&q)[5], int u,
                                              const __bf16* xs, f32x4* part, int lane) {
     using Ph = PhaseT<R, false, GLU, MT, TB>;
-    constexpr int SR = Ph::SR, AR = Ph::AR, DL = Ph::DL;
+    constexpr int SR = Ph::SR, AR = Ph::AR, DL = Ph::DL, RM = Ph::RM;
+    constexpr bool QUAD = Ph::QUAD;
+    constexpr int NB = TB ? R : (QUAD ? MT / 4 : 1);  // A blocks per weight octet
+    constexpr int ND = QUAD ? NB : 1;                 // D tiles
     const int j = lane & 15;
     const int g = lane >> 4;
     const UnitPos p = unit_pos<Ph::NT>(a, wk, u);
     const bool valid = p.ss != a.nss - 1 || g < a.ng_last;
-    const __bf16* xu = xs + ((size_t)g * SR + min(j, AR - 1)) * 8 + (size_t)(p.ss - wk.s0) * 16 * 4 * SR * 8;
-    f32x4 t0 = {0.f, 0.f, 0.f, 0.f}, t1 = {0.f, 0.f, 0.f, 0.f};
+    const __bf16* xu = xs + (size_t)g * SR * 8 + (size_t)(p.ss - wk.s0) * 16 * 4 * SR * 8;
+    // This lane's A row in each block (rows >= AR read row AR - 1; their D rows
+    // are never used; a token quad's fourth row reads the zero row).
+    int arow[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+        arow[b] = QUAD ? ((j & 3) < 3 ? (4 * b + (j >> 2)) * 3 + (j & 3) : RM) : min(j, AR - 1) + (TB ? b * MT : 0);
+    f32x4 t0[ND], t1[ND];
+#pragma unroll
+    for (int d = 0; d < ND; ++d) t0[d] = t1[d] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int bl = 0; bl < 4; ++bl) {
         const int w4 = 5 * bl + 4;
@@ -240,16 +265,27 @@ __device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& w
             const int wi = 5 * bl + t;
             const bf16x8 bv = dequant8_mix((uint32_t)q[wi >> 2][wi & 3], sc);
 #pragma unroll
-            for (int pb = 0; pb < (TB ? R : 1); ++pb) {
-                const bf16x8 av = *reinterpret_cast<const bf16x8*>(xu + ((bl * 4 + t) * 4 * SR + pb * MT) * 8);
+            for (int b = 0; b < NB; ++b) {
+                const int d = QUAD ? b : 0;
+                const bf16x8 av = *reinterpret_cast<const bf16x8*>(xu + ((bl * 4 + t) * 4 * SR + arow[b]) * 8);
                 if (t & 1)
-                    t1 = mfma16x16x32(av, bv, t1);
+                    t1[d] = mfma16x16x32(av, bv, t1[d]);
                 else
-                    t0 = mfma16x16x32(av, bv, t0);
+                    t0[d] = mfma16x16x32(av, bv, t0[d]);
             }
         }
     }
-    if (lane < DL) part[(size_t)u * DL + lane] = t0 + t1;
+    if constexpr (QUAD) {
+        // Lane (g, j) of tile b: token 4b + g, terms in elements 0..2.
+        float* pf = reinterpret_cast<float*>(part + (size_t)u * Ph::US);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const f32x4 v = t0[b] + t1[b];
+            pf[(4 * b + g) * 16 + j] = (v[0] + v[1]) + v[2];
+        }
+    } else {
+        if (lane < DL) part[(size_t)u * DL + lane] = t0[0] + t1[0];
+    }
 }
 
 template <bool THROUGH>
@@ -282,7 +318,8 @@ template <int NW, int R, bool GLU, int MT, bool TB, bool THROUGH>
 __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk, const f32x4* part, int* flag,
                                             int tid) {
     using Ph = PhaseT<R, false, GLU, MT, TB>;
-    constexpr int NT = Ph::NT, DL = Ph::DL;
+    constexpr int NT = Ph::NT, DL = Ph::DL, US = Ph::US;
+    constexpr bool QUAD = Ph::QUAD;
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 3;
@@ -298,14 +335,18 @@ __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk
         for (int ss = c; ss < wk.nsw; ss += 4) {
 #pragma unroll
             for (int n = 0; n < NT; ++n) {
-                const f32x4* sl = part + ((size_t)(tl * wk.nsw + ss) * NT + n) * DL + jj;
+                const f32x4* sl = part + ((size_t)(tl * wk.nsw + ss) * NT + n) * US + (QUAD ? 0 : jj);
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
                     float v = 0.0f;
+                    if constexpr (QUAD) {
+                        v = reinterpret_cast<const float*>(sl)[m * 16 + jj];
+                    } else {
 #pragma unroll
-                    for (int p = 0; p < (TB ? 1 : R); ++p) {
-                        const int row = TB ? m : m * R + p;
-                        v += sl[(row >> 2) * 16][row & 3];
+                        for (int p = 0; p < (TB ? 1 : R); ++p) {
+                            const int row = TB ? m : m * R + p;
+                            v += sl[(row >> 2) * 16][row & 3];
+                        }
                     }
                     y[m][n] += v;
                 }
@@ -376,7 +417,7 @@ __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk
 template <int NW, int P, int R, bool XB, bool GLU, int MT, bool TB>
 __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     using Ph = PhaseT<R, XB, GLU, MT, TB>;
-    constexpr int NT = Ph::NT, SR = Ph::SR, DL = Ph::DL;
+    constexpr int NT = Ph::NT, SR = Ph::SR, US = Ph::US;
     extern __shared__ __align__(16) unsigned char smem[];
 
     const int tid = threadIdx.x;
@@ -389,7 +430,7 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     // Unit counter of the workgroup, after the unit slots: the first P * NW
     // units go to the waves statically, the rest to whichever wave frees a ring
     // slot first, so a wave whose loads come back late does fewer units.
-    int* next = reinterpret_cast<int*>(part + (size_t)U * DL);
+    int* next = reinterpret_cast<int*>(part + (size_t)U * US);
     if (tid == 0) *next = P * NW;
 
     // The activation is staged before any weight load: queued behind the
@@ -473,9 +514,10 @@ constexpr int kP = 1;
 
 // Token capacity of a launch, activation terms per token and row layout:
 // fp32 activations take the exact three-term split, token-major up to 5
-// tokens (15 A rows, one MFMA per weight octet), term-major for 8 and 16
-// (three MFMAs; 16 tokens fill every A row, and K splits until the 48 staged
-// rows fit the LDS); bf16 activations one term, up to 16 tokens.
+// tokens (15 A rows, one MFMA per weight octet), token quads for 8 (two
+// MFMAs), term-major for 16 (three MFMAs that fill every A row; K splits
+// until the 48 staged rows fit the LDS); bf16 activations one term, up to 16
+// tokens.
 struct Shape {
     int mt, r;
     bool tb;
@@ -490,7 +532,7 @@ Shape shape_for(const GemvLaunch& L, int m) {
     if (m <= 2) return {m, 3, false};
     if (m <= 4) return {4, 3, false};
     if (m <= 5) return {5, 3, false};
-    if (m <= 8) return {8, 3, true};
+    if (m <= 8) return {8, 3, false};
     return {16, 3, true};
 }
 
@@ -510,7 +552,7 @@ hipError_t launch_shape(const Gemv1Args& a, const GemvLaunch& L, Shape sh, int g
             case 2: return launch_k<kP, 3, false, true, 2>(a, groups, lds, s);
             case 4: return launch_k<kP, 3, false, true, 4>(a, groups, lds, s);
             case 5: return launch_k<kP, 3, false, true, 5>(a, groups, lds, s);
-            case 8: return launch_k<kP, 3, false, true, 8, true>(a, groups, lds, s);
+            case 8: return launch_k<kP, 3, false, true, 8>(a, groups, lds, s);
             default: return launch_k<kP, 3, false, true, 16, true>(a, groups, lds, s);
         }
     }
@@ -519,7 +561,7 @@ hipError_t launch_shape(const Gemv1Args& a, const GemvLaunch& L, Shape sh, int g
         case 2: return launch_k<kP, 3, false, false, 2>(a, groups, lds, s);
         case 4: return launch_k<kP, 3, false, false, 4>(a, groups, lds, s);
         case 5: return launch_k<kP, 3, false, false, 5>(a, groups, lds, s);
-        case 8: return launch_k<kP, 3, false, false, 8, true>(a, groups, lds, s);
+        case 8: return launch_k<kP, 3, false, false, 8>(a, groups, lds, s);
         default: return launch_k<kP, 3, false, false, 16, true>(a, groups, lds, s);
     }
 }
@@ -542,8 +584,10 @@ bool plan_gemv1(const GemvLaunch& L, int m, Gemv1Plan* out) {
     Gemv1Plan p;
     p.sh = shape_for(L, m);
     const int RM = p.sh.mt * p.sh.r;
+    const bool quad = !p.sh.tb && p.sh.r == 3 && p.sh.mt == 8;  // ARows::QUAD
     const int AR = p.sh.tb ? p.sh.mt : RM;
-    const int SR = RM + (p.sh.tb ? 1 : 0);  // rows per LDS operand slot (PhaseT::SR)
+    const int SR = RM + ((p.sh.tb || quad) ? 1 : 0);  // rows per LDS operand slot (PhaseT::SR)
+    const size_t slot_bytes = quad ? (size_t)p.sh.mt * 64 : (size_t)256 * ((AR + 3) / 4);  // ARows::US * 16
     for (p.ks = 1; p.ks <= 16 && p.ks <= tg.nss; p.ks *= 2) {
         p.tg = std::min(RT, std::max(1, d.cus / p.ks));
         p.rt_q = RT / p.tg;
@@ -551,7 +595,7 @@ bool plan_gemv1(const GemvLaunch& L, int m, Gemv1Plan* out) {
         const int tiles = p.rt_q + (p.rt_r ? 1 : 0);
         const int nsw = (tg.nss + p.ks - 1) / p.ks;
         const int units = tiles * nsw * NT;
-        p.lds = (size_t)nsw * 1024 * SR + (size_t)units * 256 * ((AR + 3) / 4) + 16;
+        p.lds = (size_t)nsw * 1024 * SR + (size_t)units * slot_bytes + 16;
         const size_t part = p.ks > 1 ? (size_t)RT * 16 * p.ks * p.sh.mt * NT * sizeof(float) : 0;
         if (p.lds <= d.lds && part <= kPartMax && (p.ks == 1 || p.tg <= kSplitCounters)) {
             *out = p;
