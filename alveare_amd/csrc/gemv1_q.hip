@@ -10,7 +10,7 @@
 // v_mfma_f32_16x16x32_bf16. The A operand holds the activations, each fp32
 // value split exactly into three bf16 terms (one term for bf16 activations),
 // token-major (token m in rows m * terms .. + terms - 1), in token quads
-// for 8 tokens or term-major for 16 (see ARows), staged once per workgroup in LDS in operand
+// (2 to 8 tokens) or term-major (9 to 16; see ARows), staged once per workgroup in LDS in operand
 // order; the tokens of a launch share every dequantized weight. When a
 // workgroup's activations outgrow the LDS, K is split over several workgroups
 // per row-tile group (partial sums in a per-stream scratch; the last
@@ -132,14 +132,15 @@ __device__ __forceinline__ UnitPos unit_pos(const Gemv1Args& a, const WgWork& wk
 // accumulator, so D row m is already token m's sum. Lane l holds D rows
 // 4 (l / 16) .. + 3 of column l % 16; DL lanes hold the rows in use.
 //
-// Token quads (QUAD: 8 fp32 tokens, token-major): A block b holds tokens
-// 4b .. 4b + 3 at four rows each, the three terms and a zero row, so one
-// lane group of the D tile holds one token and each lane adds its token's
-// terms itself; two MFMAs per weight octet (term-major would take three), and
-// a unit's slot holds the token sums, MT x 16 floats.
+// Token quads (QUAD: 2, 4 or 8 fp32 tokens, token-major): A block b holds
+// tokens 4b .. 4b + 3 at four rows each, the three terms and a zero row
+// (tokens past MT: zero rows), so one lane group of the D tile holds one token
+// and each lane adds its token's terms itself; a unit's slot holds the token
+// sums, MT x 16 floats. For 8 tokens two MFMAs per weight octet (term-major
+// would take three).
 template <int R, int MT, bool TB>
 struct ARows {
-    static constexpr bool QUAD = !TB && R == 3 && MT == 8;
+    static constexpr bool QUAD = !TB && R == 3 && (MT == 2 || MT == 4 || MT == 8);
     static constexpr int RM = R * MT;                          // rows per slot in LDS
     static constexpr int AR = QUAD ? 16 : (TB ? MT : RM);      // rows per A block
     static constexpr int DL = 16 * ((AR + 3) / 4);
@@ -239,7 +240,7 @@ __device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& w
     using Ph = PhaseT<R, false, GLU, MT, TB>;
     constexpr int SR = Ph::SR, AR = Ph::AR, DL = Ph::DL, RM = Ph::RM;
     constexpr bool QUAD = Ph::QUAD;
-    constexpr int NB = TB ? R : (QUAD ? MT / 4 : 1);  // A blocks per weight octet
+    constexpr int NB = TB ? R : (QUAD ? (MT + 3) / 4 : 1);  // A blocks per weight octet
     constexpr int ND = QUAD ? NB : 1;                 // D tiles
     const int j = lane & 15;
     const int g = lane >> 4;
@@ -251,7 +252,8 @@ __device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& w
     int arow[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
-        arow[b] = QUAD ? ((j & 3) < 3 ? (4 * b + (j >> 2)) * 3 + (j & 3) : RM) : min(j, AR - 1) + (TB ? b * MT : 0);
+        arow[b] = QUAD ? ((j & 3) < 3 && 4 * b + (j >> 2) < MT ? (4 * b + (j >> 2)) * 3 + (j & 3) : RM)
+                       : min(j, AR - 1) + (TB ? b * MT : 0);
     f32x4 t0[ND], t1[ND];
 #pragma unroll
     for (int d = 0; d < ND; ++d) t0[d] = t1[d] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -281,7 +283,7 @@ __device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& w
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             const f32x4 v = t0[b] + t1[b];
-            pf[(4 * b + g) * 16 + j] = (v[0] + v[1]) + v[2];
+            if (4 * b + g < MT) pf[(4 * b + g) * 16 + j] = (v[0] + v[1]) + v[2];
         }
     } else {
         if (lane < DL) part[(size_t)u * DL + lane] = t0[0] + t1[0];
@@ -513,11 +515,11 @@ hipError_t launch_k(const Gemv1Args& a, int groups, size_t lds, hipStream_t s) {
 constexpr int kP = 1;
 
 // Token capacity of a launch, activation terms per token and row layout:
-// fp32 activations take the exact three-term split, token-major up to 5
-// tokens (15 A rows, one MFMA per weight octet), token quads for 8 (two
-// MFMAs), term-major for 16 (three MFMAs that fill every A row; K splits
-// until the 48 staged rows fit the LDS); bf16 activations one term, up to 16
-// tokens.
+// fp32 activations take the exact three-term split: token quads for 2, 3-4
+// and 6-8 tokens (one MFMA per weight octet up to 4 tokens, two for 8),
+// token-major rows for 1 and 5 (3 and 15 A rows, one MFMA), term-major for
+// 9-16 (three MFMAs that fill every A row; K splits until the 48 staged rows
+// fit the LDS); bf16 activations one term, up to 16 tokens.
 struct Shape {
     int mt, r;
     bool tb;
@@ -584,7 +586,7 @@ bool plan_gemv1(const GemvLaunch& L, int m, Gemv1Plan* out) {
     Gemv1Plan p;
     p.sh = shape_for(L, m);
     const int RM = p.sh.mt * p.sh.r;
-    const bool quad = !p.sh.tb && p.sh.r == 3 && p.sh.mt == 8;  // ARows::QUAD
+    const bool quad = !p.sh.tb && p.sh.r == 3 && (p.sh.mt == 2 || p.sh.mt == 4 || p.sh.mt == 8);  // ARows::QUAD
     const int AR = p.sh.tb ? p.sh.mt : RM;
     const int SR = RM + ((p.sh.tb || quad) ? 1 : 0);  // rows per LDS operand slot (PhaseT::SR)
     const size_t slot_bytes = quad ? (size_t)p.sh.mt * 64 : (size_t)256 * ((AR + 3) / 4);  // ARows::US * 16
