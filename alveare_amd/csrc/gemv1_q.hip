@@ -320,7 +320,7 @@ template <int NW, int R, bool GLU, int MT, bool TB, bool THROUGH>
 __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk, const f32x4* part, int* flag,
                                             int tid) {
     using Ph = PhaseT<R, false, GLU, MT, TB>;
-    constexpr int NT = Ph::NT, DL = Ph::DL, US = Ph::US;
+    constexpr int NT = Ph::NT, US = Ph::US;
     constexpr bool QUAD = Ph::QUAD;
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
