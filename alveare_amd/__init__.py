@@ -6,12 +6,12 @@ for the three quantized matmuls of Alveare's runtime -- ``gemv_q``,
 and the ``runtime/py`` dispatch (``alveare_amd.runtime``) on top.
 """
 from ._lib import LibraryNotBuilt, Q4Error, Q4ValueError, lib
-from .ops import (FfnWeights, Q4Weight, chain_run, check_async, dequant_q4, ffn_fused, ffn_fused_npu,
+from .ops import (FfnWeights, Q4Weight, chain_run, dequant_q4, ffn_fused, ffn_fused_npu,
                   gemm_q, gemm_q_npu, gemv_q, gemv_q_npu, pack_ffn_fused_weights, q4_tile)
 from .runtime import LazyLayerWeights, Q4Dispatch, ResidentWeight
 
 __all__ = [
     "FfnWeights", "LazyLayerWeights", "LibraryNotBuilt", "Q4Dispatch", "Q4Error", "Q4ValueError",
-    "Q4Weight", "ResidentWeight", "chain_run", "check_async", "dequant_q4", "ffn_fused", "ffn_fused_npu", "gemm_q", "gemm_q_npu",
+    "Q4Weight", "ResidentWeight", "chain_run", "dequant_q4", "ffn_fused", "ffn_fused_npu", "gemm_q", "gemm_q_npu",
     "gemv_q", "gemv_q_npu", "lib", "pack_ffn_fused_weights", "q4_tile",
 ]

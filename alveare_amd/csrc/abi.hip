@@ -6,6 +6,8 @@
 #include <mutex>
 #include <tuple>
 #include <utility>
+#include <vector>
+#include <algorithm>
 
 #include "q4_host.h"
 
@@ -29,7 +31,7 @@ int hip_check(hipError_t e, const char* what) {
 }
 
 namespace {
-// Synchronisation words: one block per device holding
+// Split-K arrival counters: one block per device holding
 // kWsStreams sets, handed out to streams on first use. The blocks are
 // allocated (the words zeroed) at the first call on the device; a stream's
 // later first use takes a set without allocating, so it may happen during
@@ -54,25 +56,25 @@ int get_workspace(hipStream_t s, size_t counters, Workspace* out) {
         if (int rc = hip_check(hipStreamIsCapturing(s, &cs), "hipStreamIsCapturing")) return rc;
         if (cs != hipStreamCaptureStatusNone)
             return fail(ALV_ERR_ARG,
-                        "the synchronisation words of this device are allocated on its first call, which cannot "
+                        "the split-K counters of this device are allocated on its first call, which cannot "
                         "happen during graph capture: run one call on this device before capturing");
-        const size_t all = (size_t)kWsWords;
+        const size_t all = (size_t)kSplitCounters;
         const size_t words = counters > all ? counters : all;
         if (hipMalloc(&w.block, words * kWsStreams * sizeof(uint32_t)) != hipSuccess) {
             w.block = nullptr;
-            return fail(ALV_ERR_HIP, "hipMalloc of the synchronisation words failed");
+            return fail(ALV_ERR_HIP, "hipMalloc of the split-K counters failed");
         }
         if (int rc = hip_check(hipMemset(w.block, 0, words * kWsStreams * sizeof(uint32_t)), "hipMemset")) return rc;
         w.words = words;
     }
-    if (counters > w.words) return fail(ALV_ERR_ARG, "%zu synchronisation words requested, %zu available", counters, w.words);
+    if (counters > w.words) return fail(ALV_ERR_ARG, "%zu counters requested, %zu available", counters, w.words);
     auto it = w.slot.find(s);
     int idx;
     if (it != w.slot.end()) {
         idx = it->second;
     } else {
         if ((int)w.slot.size() >= kWsStreams)
-            return fail(ALV_ERR_ARG, "more than %d streams use chained ops on device %d", kWsStreams, dev);
+            return fail(ALV_ERR_ARG, "more than %d streams use split-K launches on device %d", kWsStreams, dev);
         idx = (int)w.slot.size();
         w.slot[s] = idx;
     }
@@ -82,9 +84,15 @@ int get_workspace(hipStream_t s, size_t counters, Workspace* out) {
 }
 
 namespace {
+// A slot's current block and the blocks it outgrew. An outgrown block is never
+// freed: a HIP graph captured while it was current keeps its address in the
+// captured kernel arguments and may be replayed at any later time. Capacity at
+// least doubles on each growth, so the retired blocks of a slot total less than
+// its current one.
 struct Scratch {
     void* p = nullptr;
     size_t cap = 0;
+    std::vector<void*> retired;
 };
 std::map<std::tuple<int, hipStream_t, int>, Scratch> g_scratch;
 }  // namespace
@@ -100,13 +108,16 @@ int get_scratch(hipStream_t s, int slot, size_t bytes, void** out) {
         if (cs != hipStreamCaptureStatusNone)
             return fail(ALV_ERR_ARG, "scratch of %zu bytes must grow, which cannot happen during graph capture: "
                         "run one call of this shape on this stream before capturing", bytes);
-        if (int rc = hip_check(hipStreamSynchronize(s), "hipStreamSynchronize")) return rc;
-        if (sc.p) (void)hipFree(sc.p);
-        sc.p = nullptr;
-        sc.cap = 0;
-        const size_t cap = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
-        if (int rc = hip_check(hipMalloc(&sc.p, cap), "hipMalloc(scratch)")) return rc;
-        if (int rc = hip_check(hipMemsetAsync(sc.p, 0, cap, s), "hipMemsetAsync(scratch)")) return rc;
+        size_t cap = std::max(bytes, 2 * sc.cap);
+        cap = (cap + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+        void* p = nullptr;
+        if (int rc = hip_check(hipMalloc(&p, cap), "hipMalloc(scratch)")) return rc;
+        if (int rc = hip_check(hipMemsetAsync(p, 0, cap, s), "hipMemsetAsync(scratch)")) {
+            (void)hipFree(p);
+            return rc;
+        }
+        if (sc.p) sc.retired.push_back(sc.p);
+        sc.p = p;
         sc.cap = cap;
     }
     *out = sc.p;

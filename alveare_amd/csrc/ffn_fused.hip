@@ -6,12 +6,14 @@
 //      against the same activation operands; the epilogue rounds both to
 //      bf16, applies the GLU and rounds the activation to bf16 -- the
 //      reference CPU path's three rounding points (runtime/py/model.py:798-803).
-//      The activation (M x I bf16) stays in the handle's scratch, which is
-//      L2/MALL-resident at these sizes.
+//      The activation (M x I bf16) stays in the handle's buffer (16 x I,
+//      allocated at registration and never moved), which is L2/MALL-resident
+//      at these sizes.
 //   2. down = Wd * a, with a single bf16 term per activation value (it is
 //      bf16 by construction), summed entirely on the device -- the reference
 //      sums per-core partials on the host (runtime/cpp/src/npu.cpp:360-377).
-// Prefill (M >= 32): the same two steps with the MFMA tiled kernel (gemm_q.hip).
+// Prefill (M >= 32): the same two steps with the MFMA tiled kernel (gemm_q.hip);
+// the M x I activation lives in the stream's prefill scratch (q4_host.h).
 #include <string.h>
 
 #include <algorithm>
@@ -33,16 +35,16 @@ using namespace alv;
 
 namespace alv {
 
-// The two ops of one FFN call: gate/up with the GLU epilogue into the handle's
-// bf16 activation, then down from it (op 1 waits for op 0 inside a chain).
-void ffn_ops(alv_ffn_t w, const float* X, int ldx, float* Y, int ldy, int M, ExecOp (&op)[2]) {
-    ExecOp& up = op[0];
-    up = ExecOp{};
+// The two launches of one FFN call: gate/up with the GLU epilogue into the
+// bf16 activation `act`, then down from it.
+void ffn_ops(alv_ffn_t w, uint16_t* act, const float* X, int ldx, float* Y, int ldy, int M, GemvLaunch (&op)[2]) {
+    GemvLaunch& up = op[0];
+    up = GemvLaunch{};
     up.W0 = w->w;
     up.W1 = w->w + w->gate_bytes;
     up.X = X;
     up.ldx = ldx;
-    up.Yb = w->a;
+    up.Yb = act;
     up.ldy = w->I;
     up.M = M;
     up.N = w->I;
@@ -51,11 +53,10 @@ void ffn_ops(alv_ffn_t w, const float* X, int ldx, float* Y, int ldy, int M, Exe
     up.glu = true;
     up.tiled = true;
     up.act = w->act;
-    up.dep = -1;
-    ExecOp& down = op[1];
-    down = ExecOp{};
+    GemvLaunch& down = op[1];
+    down = GemvLaunch{};
     down.W0 = w->w + 2 * w->gate_bytes;
-    down.Xb = w->a;
+    down.Xb = act;
     down.ldx = w->I;
     down.Y = Y;
     down.ldy = ldy;
@@ -64,7 +65,6 @@ void ffn_ops(alv_ffn_t w, const float* X, int ldx, float* Y, int ldy, int M, Exe
     down.K = w->I;
     down.parts = 1;
     down.tiled = true;
-    down.dep = 0;
 }
 
 }  // namespace alv
@@ -98,6 +98,7 @@ extern "C" int alv_ffn_register(const uint8_t* Wg, const uint8_t* Wu, const uint
     if (!rc) rc = launch_tile(Wd, h->w + 2 * gate_bytes, H, I, s);
     h->a_cap = (size_t)I * kGemvMaxM;
     if (!rc) rc = hip_check(hipMalloc(&h->a, h->a_cap * sizeof(uint16_t)), "hipMalloc(FFN activation)");
+    h->last_a = h->a;
     if (!rc) rc = hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
     if (rc) {
         if (h->w) (void)hipFree(h->w);
@@ -128,27 +129,26 @@ extern "C" int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int l
     if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
     if (dev != w->device) return fail(ALV_ERR_HANDLE, "FFN handle belongs to device %d, current device is %d", w->device, dev);
     hipStream_t s = (hipStream_t)stream;
-    const int chunk = M >= kTiledMinM ? M : std::min(M, kGemvMaxM);
-    const size_t need = (size_t)chunk * w->I;
-    if (need > w->a_cap) {
-        if (int rc = hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize")) return rc;
-        (void)hipFree(w->a);
-        w->a = nullptr;
-        w->a_cap = 0;
-        if (int rc = hip_check(hipMalloc(&w->a, need * sizeof(uint16_t)), "hipMalloc(FFN activation)")) return rc;
-        w->a_cap = need;
+    if (M >= kTiledMinM) {
+        // Prefill: the activation goes to the stream's scratch; the handle's
+        // decode buffer keeps its size and address (graphs may hold it).
+        void* act = nullptr;
+        if (int rc = get_scratch(s, kScratchAct, (size_t)M * w->I * sizeof(uint16_t), &act)) return rc;
+        GemvLaunch op[2];
+        ffn_ops(w, static_cast<uint16_t*>(act), X, ldx, Y, ldy, M, op);
+        if (int rc = launch_gemm_tiled(op[0], s)) return rc;
+        if (int rc = launch_gemm_tiled(op[1], s)) return rc;
+        w->last_a = static_cast<uint16_t*>(act);
+        w->a_rows = M;
+        return ALV_OK;
     }
-    for (int m0 = 0; m0 < M; m0 += chunk) {
-        const int mc = std::min(chunk, M - m0);
-        ExecOp op[2];
-        ffn_ops(w, X + (size_t)m0 * ldx, ldx, Y + (size_t)m0 * ldy, ldy, mc, op);
-        if (mc >= kTiledMinM) {
-            if (int rc = launch_gemm_tiled(op[0], s)) return rc;
-            if (int rc = launch_gemm_tiled(op[1], s)) return rc;
-        } else {
-            if (int rc = launch_gemv(op[0], s)) return rc;
-            if (int rc = launch_gemv(op[1], s)) return rc;
-        }
+    for (int m0 = 0; m0 < M; m0 += kGemvMaxM) {
+        const int mc = std::min(kGemvMaxM, M - m0);
+        GemvLaunch op[2];
+        ffn_ops(w, w->a, X + (size_t)m0 * ldx, ldx, Y + (size_t)m0 * ldy, ldy, mc, op);
+        if (int rc = launch_gemv(op[0], s)) return rc;
+        if (int rc = launch_gemv(op[1], s)) return rc;
+        w->last_a = w->a;
         w->a_rows = mc;
     }
     return ALV_OK;
@@ -162,9 +162,10 @@ extern "C" int alv_ffn_gate_up(alv_ffn_t w, const float* X, int M, int ldx, void
     int dev = -1;
     if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
     if (dev != w->device) return fail(ALV_ERR_HANDLE, "FFN handle belongs to device %d, current device is %d", w->device, dev);
-    ExecOp op[2];
-    ffn_ops(w, X, ldx, nullptr, w->H, M, op);
+    GemvLaunch op[2];
+    ffn_ops(w, w->a, X, ldx, nullptr, w->H, M, op);
     if (int rc = launch_gemv(op[0], (hipStream_t)stream)) return rc;
+    w->last_a = w->a;
     w->a_rows = M;
     return ALV_OK;
 }
@@ -184,7 +185,7 @@ extern "C" int alv_ffn_activation(alv_ffn_t w, float* out, int M, void* stream) 
     if (M < 1 || M > w->a_rows) return fail(ALV_ERR_ARG, "M=%d outside the %d tokens of the last call", M, w->a_rows);
     const int64_t n = (int64_t)M * w->I;
     const int grid = (int)std::min<int64_t>((n + 255) / 256, 4096);
-    hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, w->a, out, n);
+    hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, w->last_a, out, n);
     return hip_check(hipGetLastError(), "bf16_to_f32_kernel launch");
 }
 

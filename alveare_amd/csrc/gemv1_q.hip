@@ -1,8 +1,9 @@
-// Streaming Q4 GEMV on registered (tiled) weights, gfx950: the kernel behind
-// alv_gemv_q / alv_gemv / alv_ffn_fused / alv_chain_run for M <= 16 (the
-// decode step of runtime/py/model.py:632-818, where every projection and FFN
-// half is a matrix-vector product, and the small-M batches of speculative
-// verification), up to 16 tokens per launch.
+// Streaming Q4 GEMV, gfx950: the one kernel behind alv_gemv_q / alv_gemm_q /
+// alv_gemv / alv_ffn_fused / alv_chain_run for M <= 16 (the decode step of
+// runtime/py/model.py:632-818, where every projection and FFN half is a
+// matrix-vector product, and the small-M batches of speculative
+// verification), up to 16 tokens per launch, on registered (tiled) weights or
+// straight from the combined layout (per-call weights of alv_gemv_q).
 //
 // HBM-bound: every weight byte is read once per launch, with 16-byte
 // nontemporal buffer loads, and dequantized in registers
@@ -34,6 +35,7 @@
 // ascending, terms ascending), so results are deterministic whichever wave
 // computed which unit.
 #include <algorithm>
+#include <atomic>
 
 #include "q4_device.h"
 #include "q4_host.h"
@@ -43,7 +45,7 @@ namespace alv {
 namespace {
 
 struct Gemv1Args {
-    const uint8_t* W0;
+    const uint8_t* W0;  // tiled layout, or the combined layout (TL = false)
     const uint8_t* W1;  // up matrix of a GLU pair
     const void* X;      // fp32 or bf16 activations, token m at m * ldx
     float* Y;           // fp32 output, or
@@ -52,9 +54,10 @@ struct Gemv1Args {
     uint32_t pbytes;    // bytes of part
     uint32_t* cnt;      // split-K arrivals per tile group (zero between launches)
     uint32_t wbytes;    // bytes of one matrix (row tiles x rtb)
-    uint32_t rtb;       // bytes per row tile
+    uint32_t rtb;       // bytes per row tile (combined layout: 16 rows)
+    uint32_t rs;        // combined layout: bytes per row
     uint32_t xbytes;    // activation buffer range (M tokens)
-    int N, K, nss, ng_last;
+    int N, K, nb, nss, ng_last;
     int ldx, ldy, M;
     int rt_q, rt_r;  // tile group t owns rt_q + (t < rt_r) row tiles
     int ks;          // K splits: workgroup b is tile group b / ks, super-step range b % ks
@@ -113,16 +116,24 @@ struct UnitPos {
     int ss, n;
 };
 
-template <int NT>
+// Tiled layout: piece i of lane l at off + i * step + 16 l. Combined layout
+// (TL = false): lane (g, j) reads row 16 rt + j at byte 80 g of the
+// super-step's 320-byte run, piece i at + 16 i (lane_voff).
+template <int NT, bool TL>
 __device__ __forceinline__ UnitPos unit_pos(const Gemv1Args& a, const WgWork& wk, int u) {
     UnitPos p;
     const int t = NT == 2 ? u >> 1 : u;
     p.n = NT == 2 ? u & 1 : 0;
     const int tl = t / wk.nsw;
     p.ss = wk.s0 + t - tl * wk.nsw;
-    p.off = (uint32_t)(wk.rt0 + tl) * a.rtb + (uint32_t)p.ss * 5120u;
-    p.step = p.ss == a.nss - 1 ? 256u * (uint32_t)a.ng_last : 1024u;
+    p.off = (uint32_t)(wk.rt0 + tl) * a.rtb + (uint32_t)p.ss * (TL ? 5120u : 320u);
+    p.step = TL ? (p.ss == a.nss - 1 ? 256u * (uint32_t)a.ng_last : 1024u) : 16u;
     return p;
+}
+
+template <bool TL>
+__device__ __forceinline__ uint32_t lane_voff(const Gemv1Args& a, int lane) {
+    return TL ? 16u * (uint32_t)lane : (uint32_t)(lane & 15) * a.rs + 80u * (uint32_t)(lane >> 4);
 }
 
 // Activation rows of an operand slot (MT tokens x R terms) and how they meet
@@ -210,14 +221,14 @@ __device__ __forceinline__ void stage_acts(const Gemv1Args& a, const WgWork& wk,
 // The five 16-byte pieces of unit u (u >= U: past the range, zeros and no
 // memory traffic). Offsets are wave-uniform by construction; saying so keeps
 // the loads out of per-lane (waterfall) loops.
-template <bool GLU>
+template <bool GLU, bool TL>
 __device__ __forceinline__ void issue_unit(const Gemv1Args& a, const WgWork& wk, int U, __amdgpu_buffer_rsrc_t r0,
                                            __amdgpu_buffer_rsrc_t r1, uint32_t voff, u32x4 (&d)[5], int u) {
     constexpr int NT = GLU ? 2 : 1;
     uint32_t off = a.wbytes, step = 1024u;
     int n = 0;
     if (u < U) {
-        const UnitPos p = unit_pos<NT>(a, wk, u);
+        const UnitPos p = unit_pos<NT, TL>(a, wk, u);
         off = p.off;
         step = p.step;
         n = p.n;
@@ -231,10 +242,10 @@ __device__ __forceinline__ void issue_unit(const Gemv1Args& a, const WgWork& wk,
 
 // ---- 3. dequantize + MFMA unit u (held in q) into its LDS slot ----------------------
 // Lane base of the A operand: slot g, row j of the (first) block (rows >= AR
-// read row AR - 1; their D rows are never used). The last super-step holds
-// ng_last lanes of g per row; the other lanes read the next plane's bytes:
-// their scales are zeroed.
-template <int R, bool GLU, int MT, bool TB>
+// read row AR - 1; their D rows are never used). A block past the row's end
+// (the last super-step: the next plane's bytes, or the next row's in the
+// combined layout) gets a zero scale, so its weights are zero.
+template <int R, bool GLU, int MT, bool TB, bool TL>
 __device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& wk, const u32x4 (&q)[5], int u,
                                              const __bf16* xs, f32x4* part, int lane) {
     using Ph = PhaseT<R, false, GLU, MT, TB>;
@@ -244,8 +255,8 @@ __device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& w
     constexpr int ND = QUAD ? NB : 1;                 // D tiles
     const int j = lane & 15;
     const int g = lane >> 4;
-    const UnitPos p = unit_pos<Ph::NT>(a, wk, u);
-    const bool valid = p.ss != a.nss - 1 || g < a.ng_last;
+    const UnitPos p = unit_pos<Ph::NT, TL>(a, wk, u);
+    const int kb0 = p.ss * 16 + g * 4;
     const __bf16* xu = xs + (size_t)g * SR * 8 + (size_t)(p.ss - wk.s0) * 16 * 4 * SR * 8;
     // This lane's A row in each block (rows >= AR read row AR - 1; their D rows
     // are never used; a token quad's fourth row reads the zero row).
@@ -260,7 +271,7 @@ __device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& w
 #pragma unroll
     for (int bl = 0; bl < 4; ++bl) {
         const int w4 = 5 * bl + 4;
-        const uint32_t sd = valid ? (uint32_t)q[w4 >> 2][w4 & 3] : 0u;
+        const uint32_t sd = kb0 + bl < a.nb ? (uint32_t)q[w4 >> 2][w4 & 3] : 0u;
         const Scale2 sc = make_scale2(scale_of(sd));
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -416,7 +427,7 @@ __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk
     if (tid == 0) __hip_atomic_store(&a.cnt[wk.tg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int NW, int P, int R, bool XB, bool GLU, int MT, bool TB>
+template <int NW, int P, int R, bool XB, bool GLU, int MT, bool TB, bool TL>
 __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     using Ph = PhaseT<R, XB, GLU, MT, TB>;
     constexpr int NT = Ph::NT, SR = Ph::SR, US = Ph::US;
@@ -443,13 +454,13 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     // ---- 2. the first P units of this wave -----------------------------------------
     const __amdgpu_buffer_rsrc_t r0 = make_rsrc(a.W0, a.wbytes);
     const __amdgpu_buffer_rsrc_t r1 = make_rsrc(GLU ? a.W1 : a.W0, a.wbytes);
-    const uint32_t voff = 16u * (uint32_t)lane;
+    const uint32_t voff = lane_voff<TL>(a, lane);
     u32x4 q[P][5];
     int uk[P];  // the unit in each ring slot (>= U: none)
 #pragma unroll
     for (int k = 0; k < P; ++k) {
         uk[k] = w + k * NW;
-        issue_unit<GLU>(a, wk, U, r0, r1, voff, q[k], uk[k]);
+        issue_unit<GLU, TL>(a, wk, U, r0, r1, voff, q[k], uk[k]);
     }
 
     // ---- 3. stream: dequantize + MFMA one unit, refill its ring slot ---------------
@@ -463,8 +474,8 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
             int un = 0;
             if (lane == 0) un = __hip_atomic_fetch_add(next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             un = __builtin_amdgcn_readfirstlane(un);
-            if (uk[k] < U) compute_unit<R, GLU, MT, TB>(a, wk, q[k], uk[k], xs, part, lane);
-            issue_unit<GLU>(a, wk, U, r0, r1, voff, q[k], un);
+            if (uk[k] < U) compute_unit<R, GLU, MT, TB, TL>(a, wk, q[k], uk[k], xs, part, lane);
+            issue_unit<GLU, TL>(a, wk, U, r0, r1, voff, q[k], un);
             uk[k] = un;
             live |= un < U;
         }
@@ -495,17 +506,28 @@ const DevInfo& dev_info() {
 
 constexpr int kNW = 16;
 
-template <int P, int R, bool XB, bool GLU, int MT, bool TB = false>
-hipError_t launch_k(const Gemv1Args& a, int groups, size_t lds, hipStream_t s) {
-    auto k = q4_gemv1_kernel<kNW, P, R, XB, GLU, MT, TB>;
-    if (lds > 64 * 1024) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) {
-            (void)hipGetLastError();
-            return e;
-        }
+// The dynamic-LDS limit of kernel k on the current device, raised to `lds`
+// once per (kernel, device) rather than on every launch.
+inline hipError_t ensure_lds(const void* k, std::atomic<int> (&set)[64], size_t lds) {
+    if (lds <= 64 * 1024) return hipSuccess;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (set[dev].load(std::memory_order_relaxed) >= (int)lds) return hipSuccess;
+    const int want = (int)dev_info().lds;  // the whole per-workgroup limit: one call per kernel and device
+    const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, want);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return e;
     }
+    set[dev].store(want, std::memory_order_relaxed);
+    return hipSuccess;
+}
+
+template <int P, int R, bool XB, bool GLU, int MT, bool TB = false, bool TL = true>
+hipError_t launch_k(const Gemv1Args& a, int groups, size_t lds, hipStream_t s) {
+    auto k = q4_gemv1_kernel<kNW, P, R, XB, GLU, MT, TB, TL>;
+    static std::atomic<int> set[64];
+    if (const hipError_t e = ensure_lds(reinterpret_cast<const void*>(k), set, lds)) return e;
     hipLaunchKernelGGL(k, dim3(groups), dim3(64 * kNW), lds, s, a);
     return hipGetLastError();
 }
@@ -558,6 +580,16 @@ hipError_t launch_shape(const Gemv1Args& a, const GemvLaunch& L, Shape sh, int g
             default: return launch_k<kP, 3, false, true, 16, true>(a, groups, lds, s);
         }
     }
+    if (!L.tiled) {
+        switch (sh.mt) {
+            case 1: return launch_k<kP, 3, false, false, 1, false, false>(a, groups, lds, s);
+            case 2: return launch_k<kP, 3, false, false, 2, false, false>(a, groups, lds, s);
+            case 4: return launch_k<kP, 3, false, false, 4, false, false>(a, groups, lds, s);
+            case 5: return launch_k<kP, 3, false, false, 5, false, false>(a, groups, lds, s);
+            case 8: return launch_k<kP, 3, false, false, 8, false, false>(a, groups, lds, s);
+            default: return launch_k<kP, 3, false, false, 16, true, false>(a, groups, lds, s);
+        }
+    }
     switch (sh.mt) {
         case 1: return launch_k<kP, 3, false, false, 1>(a, groups, lds, s);
         case 2: return launch_k<kP, 3, false, false, 2>(a, groups, lds, s);
@@ -578,7 +610,8 @@ struct Gemv1Plan {
 // workgroup's activations and unit slots fit the LDS and the split's partial
 // sums fit their scratch. One split when it fits: no partial sums at all.
 bool plan_gemv1(const GemvLaunch& L, int m, Gemv1Plan* out) {
-    if (!L.tiled || L.parts != (L.Xb ? 1 : 3) || m < 1) return false;
+    if (L.parts != (L.Xb ? 1 : 3) || m < 1) return false;
+    if (!L.tiled && (L.Xb || L.glu)) return false;  // the combined layout serves alv_gemv_q / alv_gemm_q only
     const DevInfo& d = dev_info();
     const TileGeom tg = tile_geom(L.K);
     const int RT = (L.N + 15) / 16;
@@ -617,15 +650,14 @@ int max_tokens(const GemvLaunch& L) {
 
 }  // namespace
 
-bool gemv1_ok(const GemvLaunch& L) { return L.M >= 1 && max_tokens(L) > 0; }
-
 namespace {
 
 // Kernel arguments of tokens [m0, m0 + m) of L under plan p.
 int fill_args(const GemvLaunch& L, const Gemv1Plan& p, int m0, int m, hipStream_t s, Gemv1Args* out) {
     const TileGeom tg = tile_geom(L.K);
     const int RT = (L.N + 15) / 16;
-    const uint64_t wbytes = (uint64_t)RT * tg.rtb;
+    const uint64_t rs = (uint64_t)tg.nb * kBlockBytes;
+    const uint64_t wbytes = L.tiled ? (uint64_t)RT * tg.rtb : (uint64_t)L.N * rs;
     if (wbytes >= 0xFFFFE000ull)
         return fail(ALV_ERR_RANGE, "weight matrix of %llu bytes exceeds the 4 GiB buffer range", (unsigned long long)wbytes);
     const int ES = L.Xb ? 2 : 4;
@@ -634,8 +666,8 @@ int fill_args(const GemvLaunch& L, const Gemv1Plan& p, int m0, int m, hipStream_
     Gemv1Args a{};
     if (p.ks > 1) {
         Workspace ws;
-        if (int rc = get_workspace(s, kWsWords, &ws)) return rc;
-        a.cnt = ws.counters + kSyncWords;
+        if (int rc = get_workspace(s, kSplitCounters, &ws)) return rc;
+        a.cnt = ws.counters;
         const size_t pb = (size_t)RT * 16 * p.ks * p.sh.mt * (L.glu ? 2 : 1) * sizeof(float);
         void* part = nullptr;
         if (int rc = get_scratch(s, kScratchSplit, pb, &part)) return rc;
@@ -648,7 +680,9 @@ int fill_args(const GemvLaunch& L, const Gemv1Plan& p, int m0, int m, hipStream_
     a.Y = L.Y ? L.Y + (size_t)m0 * L.ldy : nullptr;
     a.Yb = L.Yb ? L.Yb + (size_t)m0 * L.ldy : nullptr;
     a.wbytes = (uint32_t)wbytes;
-    a.rtb = tg.rtb;
+    a.rtb = L.tiled ? tg.rtb : (uint32_t)(16 * rs);
+    a.rs = (uint32_t)rs;
+    a.nb = tg.nb;
     a.xbytes = (uint32_t)xbytes;
     a.N = L.N;
     a.K = L.K;
@@ -667,9 +701,12 @@ int fill_args(const GemvLaunch& L, const Gemv1Plan& p, int m0, int m, hipStream_
 
 }  // namespace
 
-int launch_gemv1(const GemvLaunch& L, hipStream_t s) {
-    const int mmax = L.M >= 1 ? max_tokens(L) : 0;
-    if (!mmax) return fail(ALV_ERR_ARG, "streaming GEMV: shape M=%d N=%d K=%d outside its plan", L.M, L.N, L.K);
+int launch_gemv(const GemvLaunch& L, hipStream_t s) {
+    if (L.M < 1 || L.M > kGemvMaxM) return fail(ALV_ERR_ARG, "streaming GEMV takes 1 <= M <= %d (got %d)", kGemvMaxM, L.M);
+    if (L.parts != (L.Xb ? 1 : 3)) return fail(ALV_ERR_ARG, "fp32 activations take 3 terms, bf16 activations 1");
+    if (L.Xb && L.glu) return fail(ALV_ERR_ARG, "bf16 activations take no GLU");
+    const int mmax = max_tokens(L);
+    if (!mmax) return fail(ALV_ERR_RANGE, "streaming GEMV: no launch plan for M=%d N=%d K=%d", L.M, L.N, L.K);
     // Groups of as equal a size as the capacity allows (16 tokens at a
     // capacity of 5: four groups of 4, not 5 + 5 + 5 + 1).
     const int ngroups = (L.M + mmax - 1) / mmax;

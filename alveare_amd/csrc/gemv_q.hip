@@ -1,6 +1,7 @@
-// Entry points on the combined layout: alv_gemv_q, alv_gemm_q (small M via the
-// streaming kernel of stream_q.hip, large M via the MFMA tiled kernel of
-// gemm_q.hip) and the dequant test kernel behind alv_dequant_q4.
+// Entry points on the combined layout: alv_gemv_q, alv_gemm_q (M < 32 via the
+// streaming kernel of gemv1_q.hip, larger M via the MFMA tiled kernel of
+// gemm_q.hip), the dequant and GLU parity kernels behind alv_dequant_q4 and
+// alv_glu.
 #include <algorithm>
 
 #include "q4_device.h"

@@ -15,11 +15,11 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 void clear_error();
 int hip_check(hipError_t e, const char* what);
 
-// Per-(device, stream) synchronisation words of the op-chain executor. They
-// are zero when a launch starts and every launch leaves them zero. A device's
-// words (a set for each of up to 64 streams) are allocated at its first call,
-// which synchronises the device; later calls, a stream's first included,
-// allocate nothing.
+// Per-(device, stream) arrival counters of the streaming GEMV's split-K
+// launches. They are zero when a launch starts and every launch leaves them
+// zero. A device's counters (a set for each of up to 64 streams) are
+// allocated at its first call, which synchronises the device; later calls, a
+// stream's first included, allocate nothing.
 struct Workspace {
     uint32_t* counters = nullptr;
     size_t counter_count = 0;
@@ -30,22 +30,27 @@ int get_workspace(hipStream_t s, size_t counters, Workspace* out);
 // allocated, for launches whose temporaries grow with their shape: slot 0 the
 // prefill GEMM's (counters, partial tiles, activation terms), slot 1 the
 // streaming GEMV's split-K partial sums (rewritten by every such launch before
-// it is read). Growing synchronises the stream and reallocates, so it cannot
-// happen during graph capture (an error then); a call that fits what the slot
-// already holds allocates nothing.
+// it is read), slot 2 the FFN activation of prefill-sized calls. A call that
+// fits what the slot holds allocates nothing. Growing allocates a new block
+// (at least twice the old capacity) and keeps the old one allocated for the
+// life of the process, since a HIP graph captured earlier may still use it;
+// growth is refused during graph capture. A graph captured on a stream uses
+// that stream's blocks, so its replays must not overlap other calls on it.
 constexpr int kScratchGemm = 0;
 constexpr int kScratchSplit = 1;
+constexpr int kScratchAct = 2;
 int get_scratch(hipStream_t s, int slot, size_t bytes, void** out);
 // Largest split-K partial-sum block of one streaming GEMV launch.
 constexpr size_t kPartMax = 256u << 20;
 
-// One launch of the streaming kernel (stream_q.hip):
+// One product on the streaming kernel (gemv1_q.hip), M <= kGemvMaxM tokens:
 //   out[m, n] = sum_k X[m, k] * dequant(W0)[n, k]            (glu == false)
 //   out[m, n] = act(bf16(X W0^T), bf16(X W1^T)) rounded to bf16 (glu == true)
 // parts = 3 splits fp32 X exactly into three bf16 terms; parts = 1 requires X
 // to hold bf16 values (the FFN's activation does). The activations are either
 // fp32 (X) or bf16 bit patterns (Xb, parts = 1, no GLU); the output is fp32
-// (Y) or bf16 bit patterns (Yb).
+// (Y) or bf16 bit patterns (Yb). Weights in the tiled layout (q4_device.h) or,
+// for fp32 activations without a GLU, the combined layout.
 struct GemvLaunch {
     const uint8_t* W0 = nullptr;
     const uint8_t* W1 = nullptr;
@@ -63,68 +68,8 @@ struct GemvLaunch {
 };
 int launch_gemv(const GemvLaunch& L, hipStream_t s);
 
-// ---- op chains (stream_q.hip) --------------------------------------------------
-// One op of a chain: a GemvLaunch plus the index of the earlier op whose output
-// is its input (-1: the input is ready when the launch starts).
-struct ExecOp : GemvLaunch {
-    int dep = -1;
-};
-constexpr int kMaxOps = 16;
-// Synchronisation words of a chain launch. Same-address device atomics
-// serialise (~8 ns each), so counters that many workgroups bump are spread over
-// kSyncSlots words: per op, "row tiles done" (workgroup b counts into slot
-// b % kSyncSlots); a two-level exit count (workgroup b into slot
-// b % kSyncSlots, the slot that completes into one word); and a sticky error
-// flag set when a wait timed out.
-constexpr int kSyncSlots = 64;
-constexpr int kSyncExit1 = kMaxOps * kSyncSlots;
-constexpr int kSyncExit2 = kSyncExit1 + kSyncSlots;
-constexpr int kSyncError = kSyncExit2 + 1;
-constexpr int kSyncWords = kSyncError + 1;
-// Split-K arrival counters of the streaming GEMV, after the executor's words
-// (one per tile group of a launch).
+// Arrival counters per stream: one per tile group of a split-K launch.
 constexpr int kSplitCounters = 1024;
-// Words of a stream's set: the executor's, then the split-K counters.
-constexpr int kWsWords = kSyncWords + kSplitCounters;
-
-// Device-side descriptor of one op (kernel argument; every field is
-// wave-uniform). Work split: a workgroup of 16 waves holds rtw row-tile slots
-// of (1 << kw_shift) waves each; wave kw of a slot takes super-steps
-// [kw * spw, kw * spw + spw) of its row tile, for each of the op's one or two
-// matrices. Round r, slot s of workgroup b is row tile (r * rtw + s) * grid + b;
-// workgroup b runs nr_full + (b < nr_rem) rounds.
-struct OpDesc {
-    const uint8_t* W0;
-    const uint8_t* W1;
-    const void* X;
-    float* Y;
-    uint16_t* Yb;
-    uint32_t wbytes, xbytes, rstride;
-    int ldx, ldy, M, N, K, parts, R, nb, nss, ng_last, RT, act;
-    int glu, xb, dep, signal;
-    int spw, kw_shift, rtw, nr_full, nr_rem;
-};
-struct ExecArgs {
-    OpDesc op[kMaxOps];
-    int nops;
-    uint32_t xs_bytes;  // LDS bytes of the staged activations (the reduction scratch follows)
-    uint32_t spin_limit;
-    int last_wait;  // the last op that waits for an earlier one (-1: none, no counters are used)
-    uint32_t* sync;
-};
-// Run ops[0..nops) on `s`: one launch per group of tokens that fits the LDS
-// (every op of a launch sees the same tokens). tiled: weights in the tiled
-// layout (required for chains longer than one op).
-int exec_chain(const ExecOp* ops, int nops, bool tiled, hipStream_t s);
-// Report (and clear) a timed-out chain wait on stream `s` (synchronises it).
-int check_async(hipStream_t s);
-
-// ---- streaming GEMV for few tokens (gemv1_q.hip) -----------------------------------
-// L on registered weights as launches of the streaming kernel, up to four
-// tokens each; gemv1_ok: the shape's activations and unit slots fit the LDS
-// for one token at least.
-bool gemv1_ok(const GemvLaunch& L);
-int launch_gemv1(const GemvLaunch& L, hipStream_t s);
 
 // Repack W (combined layout, N x K) into the tiled layout at `out`
 // (tile_bytes(N, K) bytes), on `s` (tile_q.hip).
@@ -141,8 +86,9 @@ int launch_gemm_tiled(const GemvLaunch& L, hipStream_t s);
 // M at and above which alv_gemm_q uses the tiled kernel.
 constexpr int kTiledMinM = 32;
 
-// The two ops of one FFN call on handle w (ffn_fused.hip).
-void ffn_ops(alv_ffn_t w, const float* X, int ldx, float* Y, int ldy, int M, ExecOp (&op)[2]);
+// The two launches of one FFN call on handle w (ffn_fused.hip): gate/up with
+// the GLU epilogue into the bf16 activation `act`, then down from it.
+void ffn_ops(alv_ffn_t w, uint16_t* act, const float* X, int ldx, float* Y, int ldy, int M, GemvLaunch (&op)[2]);
 
 }  // namespace alv
 
@@ -166,8 +112,9 @@ struct alv_ffn {
     int H, I, act;
     uint8_t* w;  // one allocation: gate | up | down, tiled layout (q4_device.h)
     size_t gate_bytes, down_bytes;
-    uint16_t* a;  // activation scratch (bf16 bit patterns), a_cap elements
+    uint16_t* a;  // decode activation (bf16 bit patterns), kGemvMaxM x I, fixed for the handle's life
     size_t a_cap;
-    int a_rows;  // tokens held in `a` after the last call
+    const uint16_t* last_a;  // activation of the last call: `a`, or the stream's prefill scratch
+    int a_rows;              // tokens held at last_a after the last call
 };
 

@@ -59,11 +59,30 @@ def _too_small(name: str, actual: int, expected: int) -> None:
 
 
 def _weight(W: torch.Tensor, N: int, K: int, name: str = "W") -> torch.Tensor:
+    """The (N, K/32*20) combined-layout matrix held by W. A 2-D W is read with
+    its own row stride: rows of W.shape[1] bytes, of which the first K/32*20
+    are used, and the first N rows (the reference's quantizer pads K and N
+    with zero weights, tools/quantize_gemma4.py:158-187); a padded W yields a
+    contiguous copy of that sub-matrix. A 1-D W is a flat row-major buffer
+    that may be larger than needed (runtime/py/model.py:12-21)."""
+    if not isinstance(W, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(W).__name__}")
     if W.dtype != torch.uint8:
         raise TypeError(f"{name} must be uint8 in the combined Q4 layout, got {W.dtype}")
+    rb = (K // 32) * 20
+    if W.dim() == 2:
+        if W.shape[1] < rb or W.shape[0] < N:
+            raise RuntimeError(f"Tensor too small. Actual: {tuple(W.shape)}, Expected: ({N}, {rb}) ({name})")
+        if W.shape[1] % 20:
+            raise ValueError(f"{name} rows of {W.shape[1]} bytes are not whole 20-byte Q4 blocks")
+        if W.shape[1] != rb or not W.is_contiguous():
+            return W[:N, :rb].contiguous()
+        return W
+    if W.dim() != 1:
+        raise ValueError(f"{name} must be 1-D (flat) or 2-D (rows, K/32*20), got shape {tuple(W.shape)}")
     if not W.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
-    _too_small(name, W.numel(), N * (K // 32) * 20)
+    _too_small(name, W.numel(), N * rb)
     return W
 
 
@@ -103,7 +122,7 @@ def gemv_q(W: torch.Tensor, X: torch.Tensor, Y: torch.Tensor, *, N: int, K: int,
     """Y[:N] = dequant(W)[N, K] @ X[:K] (tools/ref/gemv_q.py:73-80)."""
     _check_shape(N, K)
     _need_gpu(W, X, Y)
-    _weight(W, N, K)
+    W = _weight(W, N, K)
     x = _act_in(X, K, "X")
     y = _out_buffer(Y, N, "Y")
     with torch.cuda.device(W.device):
@@ -119,7 +138,7 @@ def gemm_q(W: torch.Tensor, X: torch.Tensor, Y: torch.Tensor, *, B: int, N: int,
     if B < 1:
         raise ValueError(f"bad batch B={B}")
     _need_gpu(W, X, Y)
-    _weight(W, N, K)
+    W = _weight(W, N, K)
     x = _act_in(X, B * K, "X")
     y = _out_buffer(Y, B * N, "Y")
     with torch.cuda.device(W.device):
@@ -133,7 +152,7 @@ def dequant_q4(W: torch.Tensor, N: int, K: int) -> torch.Tensor:
     """bf16 (N, K) = dequant(W) (tools/ref/gemv_q.py:39-62); parity entry point."""
     _check_shape(N, K)
     _need_gpu(W)
-    _weight(W, N, K)
+    W = _weight(W, N, K)
     out = torch.empty((N, K), dtype=torch.bfloat16, device=W.device)
     with torch.cuda.device(W.device):
         check(lib().alv_dequant_q4(W.data_ptr(), out.data_ptr(), N, K, _stream(W)), "alv_dequant_q4")
@@ -145,7 +164,7 @@ def q4_tile(W: torch.Tensor, N: int, K: int) -> torch.Tensor:
     parity entry point for the registration-time repack."""
     _check_shape(N, K)
     _need_gpu(W)
-    _weight(W, N, K)
+    W = _weight(W, N, K)
     out = torch.empty(int(lib().alv_q4_tiled_bytes(N, K)), dtype=torch.uint8, device=W.device)
     with torch.cuda.device(W.device):
         check(lib().alv_q4_tile(W.data_ptr(), out.data_ptr(), N, K, _stream(W)), "alv_q4_tile")
@@ -160,7 +179,7 @@ class Q4Weight:
     def __init__(self, W: torch.Tensor, N: int, K: int):
         _check_shape(N, K)
         dev = _need_gpu(W)
-        _weight(W, N, K)
+        W = _weight(W, N, K)
         self.N, self.K, self.device = N, K, dev
         self._h = ctypes.c_void_p()
         with torch.cuda.device(dev):
@@ -215,9 +234,9 @@ class FfnWeights:
         if H < 32 or I < 32 or H % 32 or I % 32:
             raise ValueError(f"bad FFN shape H={H} I={I}: both must be positive multiples of 32")
         dev = _need_gpu(w_gate, w_up, w_down)
-        _weight(w_gate, I, H, "w_gate")
-        _weight(w_up, I, H, "w_up")
-        _weight(w_down, H, I, "w_down")
+        w_gate = _weight(w_gate, I, H, "w_gate")
+        w_up = _weight(w_up, I, H, "w_up")
+        w_down = _weight(w_down, H, I, "w_down")
         self.H, self.I, self.activation, self.device = H, I, activation, dev
         self._h = ctypes.c_void_p()
         with torch.cuda.device(dev):
@@ -309,8 +328,8 @@ def ffn_fused(W_fused: FfnWeights, X: torch.Tensor, Y_partial: torch.Tensor, *, 
 
 
 def chain_run(ops, M: int = 1) -> None:
-    """Run a chain of registered ops on the device with as few launches as
-    possible (alv_chain_run). ``ops`` is a list of ``(handle, x, y, dep)`` with
+    """Enqueue a chain of registered ops with one call and no host waits
+    between them (alv_chain_run). ``ops`` is a list of ``(handle, x, y, dep)`` with
     handle a Q4Weight or FfnWeights, x/y float32 GPU tensors (x may be a view
     into an earlier op's y) and dep the index of the op whose output x reads
     (or -1). Equivalent to calling the ops one after another."""
@@ -337,18 +356,10 @@ def chain_run(ops, M: int = 1) -> None:
         check(lib().alv_chain_run(arr, len(ops), M, torch.cuda.current_stream(dev).cuda_stream), "alv_chain_run")
 
 
-def check_async(device=None) -> None:
-    """Synchronise the current stream and raise if a chained op timed out."""
-    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-    with torch.cuda.device(dev):
-        check(lib().alv_check_async(torch.cuda.current_stream(dev).cuda_stream), "alv_check_async")
-
-
 # The reference's names for the same ops.
 gemv_q_npu = gemv_q
 gemm_q_npu = gemm_q
 ffn_fused_npu = ffn_fused
 
 __all__ = ["gemv_q", "gemm_q", "ffn_fused", "dequant_q4", "q4_tile", "Q4Weight", "FfnWeights", "chain_run",
-           "check_async",
            "pack_ffn_fused_weights", "gemv_q_npu", "gemm_q_npu", "ffn_fused_npu"]

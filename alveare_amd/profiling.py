@@ -20,7 +20,7 @@ import statistics
 import sys
 from collections import defaultdict
 
-Q4_KERNELS = ("q4_gemv1_kernel", "q4_oneshot_kernel", "q4_exec_kernel", "gemm_tiled", "tile_kernel")
+Q4_KERNELS = ("q4_gemv1_kernel", "gemm_q4_kernel", "tile_kernel")
 CALIBRATION = "MulFunctor"  # the profile pass's copy: torch.mul(src, 1.0, out=dst)
 
 

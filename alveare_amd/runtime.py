@@ -9,12 +9,23 @@ three calls the model graph makes:
 * ``run_ffn_fused_npu(l, x_bf16)``      (model.py:363-397)
 * ``run_gemm_npu(W_combined, x_bf16)``  (model.py:399-485)
 
-Return values follow the reference: bf16 vectors (here torch.bfloat16 tensors
-on the GPU), computed in fp32 and rounded to nearest even once, with the
-padding rules of the reference (x shorter than K is zero-padded; y holds the
-first N rows). The NPU's per-shape limits (MAX_N/MAX_K chunking, N padded to
-256, batch chunks of 16) do not exist on the GPU, so no chunking happens and
-the results are the unchunked fp32 sums.
+Return values follow the reference: bf16 vectors, computed in fp32 and
+rounded to nearest even once, with the padding rules of the reference (x
+shorter than K is zero-padded; y holds the first N rows). By default they are
+torch.bfloat16 tensors on the GPU, so a device-resident caller keeps them
+there; ``Q4Dispatch(..., host_io=True)`` returns host NumPy arrays instead,
+as the reference's NumPy model graph expects (``ml_dtypes.bfloat16`` when
+that package is importable, else the same bits as ``uint16``). The NPU's
+per-shape limits (MAX_N/MAX_K chunking, N padded to 256, batch chunks of 16)
+do not exist on the GPU, so no chunking happens and the results are the
+unchunked fp32 sums.
+
+FFN weights may be the reference quantizer's padded arrays (gate/up
+(16384, 4096/32*20), down (4096, 16384/32*20) for a 3840/15360 model,
+tools/quantize_gemma4.py:177-187): registration reads the (I, H) and (H, I)
+sub-matrices with the arrays' own row stride, as the reference's Python packer
+slices them (kernels/ffn_fused/ffn_fused.py:356-392) and its CPU path zeroes
+the padded activations (runtime/py/model.py:795-806).
 """
 from __future__ import annotations
 
@@ -89,11 +100,12 @@ class Q4Dispatch:
     """The matmul dispatch of the reference model, on one GPU."""
 
     def __init__(self, hidden_size: int, intermediate_size: int, model_type: str = "gemma4",
-                 device: str | torch.device = "cuda"):
+                 device: str | torch.device = "cuda", host_io: bool = False):
         self.hidden_size = hidden_size
         self.intermediate_size = intermediate_size
         self.model_type = model_type
         self.device = torch.device(device)
+        self.host_io = host_io
         self.layer_ffn_fused_tensors: list[FfnWeights] = []
 
     # -- registration (model.py:176-194) ------------------------------------
@@ -101,7 +113,17 @@ class Q4Dispatch:
         return "silu" if self.model_type not in ("gemma3", "gemma4") else "gelu"
 
     def register_ffn(self, w_gate, w_up, w_down) -> int:
-        """Register one layer's FFN; returns its layer index."""
+        """Register one layer's FFN; returns its layer index. The arrays are
+        2-D combined-layout matrices at least (I, H/32*20) and (H, I/32*20);
+        larger (padded) arrays contribute their leading sub-matrices."""
+        for name, w, rows, K in (("w_gate", w_gate, self.intermediate_size, self.hidden_size),
+                                 ("w_up", w_up, self.intermediate_size, self.hidden_size),
+                                 ("w_down", w_down, self.hidden_size, self.intermediate_size)):
+            shp = tuple(w.shape)
+            if len(shp) != 2:
+                raise ValueError(f"{name} must be 2-D (rows, K/32*20) so its row stride is known, got {shp}")
+            if shp[0] < rows or shp[1] < K // 32 * 20:
+                raise ValueError(f"{name} of shape {shp} is smaller than ({rows}, {K // 32 * 20})")
         ffn = pack_ffn_fused_weights(w_gate, w_up, w_down, H=self.hidden_size,
                                      I=self.intermediate_size, activation=self.activation(),
                                      device=self.device)
@@ -127,8 +149,16 @@ class Q4Dispatch:
             x = torch.cat([x, pad], dim=-1)
         return x.contiguous()
 
+    def _out(self, y32: torch.Tensor):
+        """fp32 result -> the reference's bf16 (round to nearest even), on the
+        GPU or, with host_io, as a host NumPy array."""
+        yb = y32.to(torch.bfloat16)
+        if not self.host_io:
+            return yb
+        return bf16_to_numpy(yb)
+
     # -- the three entry points ---------------------------------------------
-    def run_gemv_npu(self, W_combined, x_bf16) -> torch.Tensor:
+    def run_gemv_npu(self, W_combined, x_bf16):
         rw = self.resident(W_combined)
         N, K = _shape_of(rw)
         x = self._x(x_bf16, K)
@@ -136,14 +166,14 @@ class Q4Dispatch:
         if isinstance(W_combined, ResidentWeight):
             rw.q4()(x.float(), y)
         else:  # a per-call array, as the reference's non-resident path uploads per call
-            gemv_q(rw.tensor, x, y, N=N, K=K)
-        return y.to(torch.bfloat16)
+            gemv_q(rw.tensor.view(rw.shape), x, y, N=N, K=K)
+        return self._out(y)
 
-    def run_ffn_fused_npu(self, l: int, x_bf16) -> torch.Tensor:
+    def run_ffn_fused_npu(self, l: int, x_bf16):
         ffn = self.layer_ffn_fused_tensors[l]
         x = self._x(x_bf16, self.hidden_size)
         y = ffn(x)
-        return y.to(torch.bfloat16)
+        return self._out(y)
 
     def run_gemm_npu(self, W_combined, x_bf16) -> torch.Tensor:
         rw = self.resident(W_combined)
@@ -156,8 +186,20 @@ class Q4Dispatch:
         if isinstance(W_combined, ResidentWeight):
             rw.q4()(X.float(), Y, M=B)
         else:
-            gemm_q(rw.tensor, X, Y, B=B, N=N, K=K)
-        return Y.to(torch.bfloat16)
+            gemm_q(rw.tensor.view(rw.shape), X, Y, B=B, N=N, K=K)
+        return self._out(Y)
+
+
+def bf16_to_numpy(t: torch.Tensor) -> np.ndarray:
+    """A bf16 torch tensor as a host NumPy array with the same bits: dtype
+    ml_dtypes.bfloat16 (the reference's array type) when ml_dtypes is
+    importable, else uint16 bit patterns."""
+    bits = t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    try:
+        import ml_dtypes
+    except ImportError:
+        return bits
+    return bits.view(ml_dtypes.bfloat16)
 
 
 def load_layer_weights(weights_dir, num_layers: int, device="cuda") -> list[LazyLayerWeights]:
@@ -165,4 +207,4 @@ def load_layer_weights(weights_dir, num_layers: int, device="cuda") -> list[Lazy
     return [LazyLayerWeights(weights_dir, l, device) for l in range(num_layers)]
 
 
-__all__ = ["ResidentWeight", "LazyLayerWeights", "Q4Dispatch", "load_layer_weights", "PROJECTIONS"]
+__all__ = ["ResidentWeight", "LazyLayerWeights", "Q4Dispatch", "load_layer_weights", "bf16_to_numpy", "PROJECTIONS"]

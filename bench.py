@@ -51,7 +51,7 @@ def layer_bytes() -> dict:
     return {k: w[k] + act[k] for k in w}
 
 
-ROOFLINE_KERNEL = "q4_gemv1_kernel<16, 1, 3, false, true, 1, false>"  # gate/up + GLU, one fp32 token, registered weights
+ROOFLINE_KERNEL = "q4_gemv1_kernel<16, 1, 3, false, true, 1, false, true>"  # gate/up + GLU, one fp32 token, registered weights
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "q4_gemv1_traffic_gemma12b_decode.txt")
 CALIBRATION_BYTES = 256 << 20

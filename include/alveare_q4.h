@@ -24,12 +24,17 @@
  *  - K must be a positive multiple of 32; N, M, H, I positive. Activations are
  *    dense fp32, row-major, with the given leading dimensions (in elements).
  *  - Calls on different streams may run concurrently; calls that share an FFN
- *    handle must be serialised on one stream (the handle owns its scratch).
- *  - Chained ops synchronise through words the library keeps per (device,
- *    stream). A device's words are allocated at the first call that needs
- *    them (synchronising the device); if that first call happens during HIP
- *    graph capture it fails with ALV_ERR_ARG, so run one call on the device
- *    before capturing. Up to 64 streams per device use them.
+ *    handle must be serialised on one stream (the handle owns its decode
+ *    activation buffer).
+ *  - Temporaries that grow with a call's shape (split-K partial sums and
+ *    arrival counters of multi-token decode launches, prefill activations and
+ *    partial tiles) live in buffers the library keeps per (device, stream).
+ *    A call that fits what its stream already holds allocates nothing; one
+ *    that does not allocates a larger buffer and keeps the old one allocated
+ *    (a HIP graph captured earlier may still use it). Allocation cannot
+ *    happen during HIP graph capture (ALV_ERR_ARG): run one call of each
+ *    shape on the stream before capturing. Up to 64 streams per device.
+ *    A captured graph uses the buffers of the stream it was captured on.
  */
 #ifndef ALVEARE_Q4_H
 #define ALVEARE_Q4_H
@@ -74,7 +79,8 @@ int alv_gemv_q(const uint8_t* W, const float* x, float* y, int N, int K, void* s
  * (kernels/gemm_q/gemm_q.py:28-39) and NpuRegistry::run_gemm
  * (runtime/cpp/include/alveare/npu.h:82-87, runtime/cpp/src/npu.cpp:290-310).
  * M is any positive token count (the reference's B=16 chunking is not needed).
- * Small M runs the streaming GEMV kernel, large M the MFMA tiled kernel.
+ * M < 32 runs the streaming GEMV kernel (16 tokens per launch), M >= 32 the
+ * MFMA tiled kernel, both reading the combined layout directly.
  */
 int alv_gemm_q(const uint8_t* W, const float* X, float* Y, int M, int N, int K,
                int ldx, int ldy, void* stream);
@@ -181,23 +187,15 @@ typedef struct {
 } alv_chain_op;
 
 /*
- * Run ops[0..n) in order on `stream` with as few launches as possible: each op
- * waits on the device for its dep instead of the host waiting between calls.
- * Results equal running the ops one after another through alv_gemv /
- * alv_ffn_fused. M is the token count (1..16). An FFN handle may appear more
- * than once (each use starts a new launch).
+ * Run ops[0..n) in order on `stream`, enqueued by one call with no host
+ * waits between them (stream order satisfies each dep). Results equal
+ * running the ops one after another through alv_gemv / alv_ffn_fused. M is
+ * the token count (1..16). An FFN handle may appear more than once.
  * Device-side counterpart of the reference's per-layer dispatch, which calls
  * NpuRegistry::run_gemv / run_ffn_fused one after another
  * (runtime/cpp/src/model.cpp:265-420, runtime/py/model.py:632-818).
  */
 int alv_chain_run(const alv_chain_op* ops, int n, int M, void* stream);
-
-/*
- * Synchronise `stream` and report whether a chained op on it timed out
- * waiting for its input (ALV_ERR_HIP; only possible when other work kept
- * part of the chain's grid from being resident). Clears the condition.
- */
-int alv_check_async(void* stream);
 
 /*
  * out[N,K] = bf16 bit patterns of dequant(W). Test / parity entry point: the

@@ -66,9 +66,18 @@ def _midpoint_dist(v: np.ndarray) -> np.ndarray:
     return np.minimum(np.abs(v - m1), np.abs(v - m0))
 
 
-def ffn_check(orc, Wg, Wu, Wd, x, H, I, act, y_test, a_test=None, tol=TOL):
+def ffn_check(orc, Wg, Wu, Wd, x, H, I, act, y_test, a_test=None, tol=TOL, cache=None):
     """Flip-aware FFN parity of one token (see module docstring). Returns a
-    dict with the end-to-end max-rel and the flip count."""
+    dict with the end-to-end max-rel and the flip count. `cache` (a dict kept
+    across the tokens of one weight set) holds the fp64 dequantized matrices."""
+    if cache is None:
+        cache = {}
+
+    def deq(name, W, N, K):
+        if name not in cache:
+            cache[name] = deq_f64(orc, W, N, K)
+        return cache[name]
+
     x = np.asarray(x, np.float32)
     g = orc.gemv_q(Wg, x, I, H)
     u = orc.gemv_q(Wu, x, I, H)
@@ -91,8 +100,8 @@ def ffn_check(orc, Wg, Wu, Wd, x, H, I, act, y_test, a_test=None, tol=TOL):
         g64 = orc.gemv_q_f64(Wg, x, I, H)[flips]
         u64 = orc.gemv_q_f64(Wu, x, I, H)[flips]
         xa = np.abs(x.astype(np.float64))
-        bg = (np.abs(deq_f64(orc, Wg, I, H)[flips]) @ xa) * 2 * H * U32
-        bu = (np.abs(deq_f64(orc, Wu, I, H)[flips]) @ xa) * 2 * H * U32
+        bg = (np.abs(deq("g", Wg, I, H)[flips]) @ xa) * 2 * H * U32
+        bu = (np.abs(deq("u", Wu, I, H)[flips]) @ xa) * 2 * H * U32
         near_g = _midpoint_dist(g64) <= bg
         near_u = _midpoint_dist(u64) <= bu
         # a's own rounding: the unrounded product in fp64
@@ -112,7 +121,7 @@ def ffn_check(orc, Wg, Wu, Wd, x, H, I, act, y_test, a_test=None, tol=TOL):
     da = np.abs(a_test.astype(np.float64) - a_ref)
     budget = np.zeros(H)
     if len(flips):
-        budget = np.abs(deq_f64(orc, Wd, H, I)[:, flips]) @ da[flips]
+        budget = np.abs(deq("d", Wd, H, I)[:, flips]) @ da[flips]
     bad = np.abs(y_test - y_ref) > tol * scale + budget
     assert not bad.any(), f"{bad.sum()} outputs outside tolerance + flip budget"
     return {"max_rel": max_rel(y_test, y_ref), "flips": int(len(flips)), "down_max_rel": e1}

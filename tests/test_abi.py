@@ -80,3 +80,37 @@ def test_python_layer_validates_before_the_abi():
         aa.gemv_q(W, x, y, N=16, K=48)
     with pytest.raises(ValueError, match="unknown activation"):
         aa.FfnWeights(W, W, W, 64, 64, activation="relu")
+
+
+def test_weight_row_stride_of_padded_arrays():
+    """A 2-D weight array is read with its own row stride: a padded array (the
+    reference quantizer pads K and N, tools/quantize_gemma4.py:177-187) yields
+    its leading (N, K/32*20) sub-matrix; an array too small, or with rows that
+    are not whole 20-byte blocks, or neither 1-D nor 2-D, is rejected; a flat
+    1-D buffer may be larger than needed."""
+    import torch
+
+    from alveare_amd.ops import _weight
+
+    N, K = 48, 256
+    rb = K // 32 * 20
+    P = torch.randint(0, 256, (64, 320), dtype=torch.uint8)  # padded to 64 rows, K = 512
+    W = _weight(P, N, K)
+    assert W.shape == (N, rb) and W.is_contiguous()
+    assert torch.equal(W, P[:N, :rb])
+    exact = P[:N, :rb].contiguous()
+    assert _weight(exact, N, K).data_ptr() == exact.data_ptr()  # no copy when nothing is padded
+    flat = P.reshape(-1)
+    assert _weight(flat, N, K).data_ptr() == flat.data_ptr()    # oversized flat buffers are allowed
+    with pytest.raises(RuntimeError, match="too small"):
+        _weight(P[:N - 1], N, K)
+    with pytest.raises(RuntimeError, match="too small"):
+        _weight(P[:, :rb - 20], N, K)
+    with pytest.raises(RuntimeError, match="too small"):
+        _weight(flat[: N * rb - 1], N, K)
+    with pytest.raises(ValueError, match="20-byte"):
+        _weight(P[:, :rb + 7], N, K)
+    with pytest.raises(ValueError, match="1-D"):
+        _weight(P.reshape(4, 16, 320), N, K)
+    with pytest.raises(TypeError, match="uint8"):
+        _weight(P.to(torch.int16), N, K)

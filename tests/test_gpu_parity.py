@@ -104,7 +104,7 @@ GEMV_SHAPES = [
     (8192, 3840, "syn"),      # fused QKV at the 12B-class shape
     (3840, 15360, "syn"),     # FFN down shape
     (100, 480, "syn"),        # K not a multiple of 128 (partial super-steps)
-    (64, 16896, "syn"),       # K past the one-shot plan (33 super-steps): executor fallback
+    (64, 16896, "syn"),       # 33 super-steps: K split over workgroups
 ]
 
 
@@ -296,22 +296,14 @@ def test_ffn_gate_up_alone(orc, dev):
 
 # ---- op chains ------------------------------------------------------------------------
 
-@pytest.fixture(params=["separate", "fused"])
-def chain_mode(request, monkeypatch):
-    """alv_chain_run in its default mode (one launch per op) and with the fused
-    op-chain executor (ALV_CHAIN_FUSED=1, read on every call)."""
-    monkeypatch.setenv("ALV_CHAIN_FUSED", "1" if request.param == "fused" else "0")
-    return request.param
-
-
-def test_chain_matches_separate_calls(orc, dev, chain_mode):
+def test_chain_matches_separate_calls(orc, dev):
     """A layer-shaped chain -- projection, projection reading a slice of the
     first output, FFN reading the second, projection reading the FFN output --
     run as one chain equals the same ops called one by one, and each op passes
     the oracle on the inputs it actually saw."""
     import alveare_amd as aa
 
-    _say(f"chain layer mode={chain_mode}")
+    _say("chain layer")
     H, I, NQ, KO = 1152, 3456, 2048, 1024
     Wq, Wo = orc.synth_q4(NQ, H, 61), orc.synth_q4(H, KO, 62)
     Wg, Wu, Wd = orc.synth_q4(I, H, 63), orc.synth_q4(I, H, 64), orc.synth_q4(H, I, 65)
@@ -326,7 +318,6 @@ def test_chain_matches_separate_calls(orc, dev, chain_mode):
     for rep in range(3):  # repeated launches reuse (and must reset) the chain counters
         yq.fill_(float("nan")); yo.fill_(float("nan")); yf.fill_(float("nan")); yn.fill_(float("nan"))
         aa.chain_run([(q, x, yq, -1), (o, yq[:KO], yo, 0), (f, yo, yf, 1), (n, yf, yn, 2)])
-        aa.check_async()
         got = [t.cpu().numpy().copy() for t in (yq, yo, yf, yn)]
         if rep == 0:
             first = got
@@ -349,12 +340,12 @@ def test_chain_matches_separate_calls(orc, dev, chain_mode):
         h.close()
 
 
-def test_chain_long_and_repeated_ffn(orc, dev, chain_mode):
+def test_chain_long_and_repeated_ffn(orc, dev):
     """A chain longer than one launch holds (the split is transparent) and an
     FFN handle used twice in a row."""
     import alveare_amd as aa
 
-    _say(f"chain long mode={chain_mode}")
+    _say("chain long")
     H, I = 512, 1024
     Wg, Wu, Wd = orc.synth_q4(I, H, 71), orc.synth_q4(I, H, 72), orc.synth_q4(H, I, 73)
     f = aa.pack_ffn_fused_weights(to_dev(Wg, dev), to_dev(Wu, dev), to_dev(Wd, dev), H, I)
@@ -367,7 +358,7 @@ def test_chain_long_and_repeated_ffn(orc, dev, chain_mode):
         h = f if i % 3 else p
         ops.append((h, x if i == 0 else ys[i - 1], ys[i], i - 1))
     aa.chain_run(ops)
-    aa.check_async()
+    torch.cuda.synchronize()
     cur = x
     for i in range(steps):
         h = f if i % 3 else p
@@ -430,8 +421,9 @@ def _ffn_inputs(orc, H, I, kind, seed):
 
 @pytest.mark.parametrize("H,I,M,act,kind", [(256, 512, 1, "gelu", "ref"), (1024, 2048, 1, "gelu", "syn"),
                                             (1152, 6912, 1, "gelu", "syn"), (1152, 6912, 1, "silu", "syn"),
-                                            (3840, 15360, 1, "gelu", "syn"), (3840, 15360, 4, "gelu", "syn"),
-                                            (3840, 15360, 8, "gelu", "syn"),
+                                            (3840, 15360, 1, "gelu", "syn"), (3840, 15360, 2, "gelu", "syn"),
+                                            (3840, 15360, 4, "gelu", "syn"), (3840, 15360, 8, "gelu", "syn"),
+                                            (3840, 15360, 16, "gelu", "syn"),
                                             (1152, 6912, 16, "gelu", "syn"), (1152, 6912, 64, "gelu", "syn")])
 def test_ffn_parity(orc, dev, H, I, M, act, kind):
     import alveare_amd as aa
@@ -448,14 +440,124 @@ def test_ffn_parity(orc, dev, H, I, M, act, kind):
     A = ffn.last_activation(M).cpu().numpy()
     Yc = Y.cpu().numpy()
     a_id = 0 if act == "gelu" else 1
-    worst = 0.0
+    worst, flips, cache = 0.0, 0, {}
     for m in range(M):
-        st = parity.ffn_check(orc, Wg, Wu, Wd, X[m], H, I, a_id, Yc[m], A[m])
+        st = parity.ffn_check(orc, Wg, Wu, Wd, X[m], H, I, a_id, Yc[m], A[m], cache=cache)
         worst = max(worst, st["max_rel"])
+        flips += st["flips"]
         if m == 0:
             _say(f"  token0 {st}")
-    _say(f"  worst end-to-end max-rel {worst:.2e}")
+    _say(f"  FFN-PARITY H={H} I={I} M={M} {act}: worst end-to-end max-rel {worst:.2e}, "
+         f"activation flips {flips} over {M} tokens")
     ffn.close()
+
+
+@pytest.mark.parametrize("xkind", ["bf16", "fp32"])
+def test_ffn_prefill_12b(orc, dev, xkind):
+    """Prefill FFN at M = 512 on the 12B-class shape (MFMA tiled kernel, GLU
+    epilogue with its second pass, down projection with K = 15360 split over
+    workgroups). bf16-valued activations are the reference's prefill input
+    (x_bf16); fp32 ones take the three-term passes. Sampled tokens: both ends
+    of the two 256-token tiles and eight more."""
+    import alveare_amd as aa
+
+    H, I, M = 3840, 15360, 512
+    _say(f"ffn prefill H={H} I={I} M={M} x={xkind}")
+    seed = orc.seed_for(5, 0)
+    Wg, Wu, Wd = orc.synth_q4(I, H, seed), orc.synth_q4(I, H, seed + 1), orc.synth_q4(H, I, seed + 2)
+    X = orc.synth_normal(M * H, seed + 3).reshape(M, H)
+    if xkind == "bf16":
+        X = orc.bf16_round(X).reshape(M, H)
+    ffn = aa.pack_ffn_fused_weights(to_dev(Wg, dev), to_dev(Wu, dev), to_dev(Wd, dev), H, I)
+    Y = torch.empty((M, H), dtype=torch.float32, device=dev)
+    ffn(to_dev(X, dev), Y, M)
+    A = ffn.last_activation(M).cpu().numpy()
+    Yc = Y.cpu().numpy()
+    rng = np.random.default_rng(seed)
+    toks = sorted({0, 255, 256, 511, *rng.choice(M, 8, replace=False).tolist()})
+    worst, flips, cache = 0.0, 0, {}
+    for m in toks:
+        st = parity.ffn_check(orc, Wg, Wu, Wd, X[m], H, I, 0, Yc[m], A[m], cache=cache)
+        worst = max(worst, st["max_rel"])
+        flips += st["flips"]
+    _say(f"  FFN-PARITY H={H} I={I} M={M} x={xkind} tokens {toks}: worst end-to-end max-rel {worst:.2e}, "
+         f"activation flips {flips} over {len(toks)} tokens")
+    ffn.close()
+
+
+def test_ffn_padded_arrays_dispatch(orc, dev):
+    """The reference quantizer's padded FFN arrays (K and N padded past the
+    model's H and I, tools/quantize_gemma4.py:177-187) registered through the
+    dispatch with the model's H and I: the kernels read the (I, H) and (H, I)
+    sub-matrices with the arrays' row stride, which is the reference's CPU
+    path (runtime/py/model.py:795-806: x zero-padded, padded activations
+    zeroed). The padding holds garbage here, so reading it would show."""
+    from alveare_amd.runtime import Q4Dispatch
+
+    H, I, Hp, Ip = 1152, 3456, 1280, 4096
+    seed = orc.seed_for(2, 9)
+    Wg, Wu, Wd = orc.synth_q4(I, H, seed), orc.synth_q4(I, H, seed + 1), orc.synth_q4(H, I, seed + 2)
+
+    def padded(W, N, K, Np, Kp, s):
+        P = orc.synth_q4(Np, Kp, s)  # garbage everywhere, then the real matrix in the corner
+        P = P.reshape(Np, Kp // 32 * 20)
+        P[:N, :K // 32 * 20] = W.reshape(N, K // 32 * 20)
+        return P
+
+    Pg, Pu, Pd = padded(Wg, I, H, Ip, Hp, seed + 3), padded(Wu, I, H, Ip, Hp, seed + 4), padded(Wd, H, I, Hp, Ip, seed + 5)
+    d = Q4Dispatch(H, I, "gemma3", dev)
+    l = d.register_ffn(Pg, Pu, Pd)
+    x = orc.bf16_round(orc.synth_normal(H, seed + 6))
+    y = d.run_ffn_fused_npu(l, torch.from_numpy(x).to(torch.bfloat16))
+    assert y.shape == (H,)
+    parity.ffn_check(orc, Wg, Wu, Wd, x, H, I, 0, y.float().cpu().numpy(),
+                     d.layer_ffn_fused_tensors[l].last_activation(1).cpu().numpy()[0], tol=2 ** -8)
+    # host NumPy in and out, as the reference's model graph uses it
+    dh = Q4Dispatch(H, I, "gemma3", dev, host_io=True)
+    dh.layer_ffn_fused_tensors = d.layer_ffn_fused_tensors
+    yh = dh.run_ffn_fused_npu(l, x)
+    assert isinstance(yh, np.ndarray) and yh.shape == (H,)
+    assert np.array_equal(yh.view(np.uint16), y.view(torch.int16).cpu().numpy().view(np.uint16))
+    with pytest.raises(ValueError, match="smaller than"):
+        d.register_ffn(Pg[:I - 16], Pu, Pd)
+    with pytest.raises(ValueError, match="2-D"):
+        d.register_ffn(Pg.reshape(-1), Pu, Pd)
+
+
+def test_ffn_graph_survives_prefill(orc, dev):
+    """A decode FFN captured in a HIP graph keeps working after prefill-sized
+    calls (which allocate larger per-stream buffers) and a multi-token decode
+    call: replays after them still equal the eager result."""
+    import alveare_amd as aa
+
+    H, I = 1152, 3456
+    Wg, Wu, Wd = orc.synth_q4(I, H, 91), orc.synth_q4(I, H, 92), orc.synth_q4(H, I, 93)
+    f = aa.pack_ffn_fused_weights(to_dev(Wg, dev), to_dev(Wu, dev), to_dev(Wd, dev), H, I)
+    s = torch.cuda.Stream()
+    x = to_dev(orc.synth_normal(H, 94), dev)
+    y = torch.empty(H, device=dev)
+    with torch.cuda.stream(s):
+        f(x, y)  # eager call on the capture stream first: its buffers exist before capture
+        torch.cuda.synchronize()
+        want = y.clone()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            f(x, y)
+    for M in (64, 300, 16):
+        xm = to_dev(orc.synth_normal(M * H, 95 + M), dev)
+        with torch.cuda.stream(s):
+            ym = f(xm, M=M)
+        torch.cuda.synchronize()
+        for m in (0, M - 1):
+            parity.ffn_check(orc, Wg, Wu, Wd, xm[m * H:(m + 1) * H].cpu().numpy(), H, I, 0, ym[m].cpu().numpy(),
+                             f.last_activation(M).cpu().numpy()[m])
+        for _ in range(2):
+            y.fill_(float("nan"))
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, want), f"graph replay after an M={M} call"
+    del g
+    f.close()
 
 
 def test_ffn_one_token_sequence(orc, dev):
@@ -480,7 +582,6 @@ def test_ffn_one_token_sequence(orc, dev):
     y = torch.empty((1, H), dtype=torch.float32, device=dev)
     ffn(to_dev(xs[0][None, :], dev), y, 1)
     assert torch.equal(y, outs[0])
-    aa.check_async()
     ffn.close()
 
 
