@@ -17,6 +17,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "q4_device.h"
 #include "q4_host.h"
@@ -151,6 +152,78 @@ extern "C" int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int l
         w->last_a = w->a;
         w->a_rows = mc;
     }
+    return ALV_OK;
+}
+
+// ---- alv_ffn_fused_noalloc ------------------------------------------------------
+// The decode FFN with its split-K temporaries (arrival counters, partial sums)
+// in `scratch`, a fixed array in device memory that every GPU the library runs
+// on holds until the process ends, instead of buffers allocated per stream:
+// no call allocates. `scratch` names a host-side stand-in in host code; the
+// device address comes from hipGetSymbolAddress, once per device.
+namespace {
+
+constexpr size_t kStaticCounterBytes = (size_t)kSplitCounters * sizeof(uint32_t);
+constexpr size_t kStaticPartBytes = (size_t)16 << 20;  // split-K partial sums
+static __device__ __align__(256) unsigned char scratch[kStaticCounterBytes + kStaticPartBytes];
+
+__global__ void __launch_bounds__(256) zero_words_kernel(uint32_t* p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+std::mutex g_static_mu;
+unsigned char* g_static_ptr[64];
+
+// This device's copy of `scratch`. Its first use on a device also clears the
+// counters, with a kernel on `s` (stream-ordered before the caller's launches).
+int static_split(int dev, hipStream_t s, SplitBuf* out) {
+    if (dev < 0 || dev >= 64) return fail(ALV_ERR_ARG, "device %d outside the 64 the library tracks", dev);
+    std::lock_guard<std::mutex> lk(g_static_mu);
+    if (!g_static_ptr[dev]) {
+        void* p = nullptr;
+        if (int rc = hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)")) return rc;
+        if (!p) return fail(ALV_ERR_HIP, "hipGetSymbolAddress(scratch) returned a null address");
+        hipLaunchKernelGGL(zero_words_kernel, dim3(4), dim3(256), 0, s, static_cast<uint32_t*>(p), (int)kSplitCounters);
+        if (int rc = hip_check(hipGetLastError(), "zero_words_kernel launch")) return rc;
+        g_static_ptr[dev] = static_cast<unsigned char*>(p);
+    }
+    out->counters = reinterpret_cast<uint32_t*>(g_static_ptr[dev]);
+    out->part = reinterpret_cast<float*>(g_static_ptr[dev] + kStaticCounterBytes);
+    out->part_bytes = kStaticPartBytes;
+    return ALV_OK;
+}
+
+}  // namespace
+
+extern "C" int alv_ffn_fused_noalloc(alv_ffn_t w, const float* X, float* Y, int M, int ldx, int ldy,
+                                     void* stream) {
+    if (int rc = check_handle(w)) return rc;
+    if (!X || !Y) return fail(ALV_ERR_ARG, "null activation pointer");
+    if (M < 1 || M > kGemvMaxM || ldx < w->H || ldy < w->H)
+        return fail(ALV_ERR_ARG, "bad M=%d ldx=%d ldy=%d for H=%d (1 <= M <= %d)", M, ldx, ldy, w->H, kGemvMaxM);
+    if (reinterpret_cast<uintptr_t>(X) % 4 || reinterpret_cast<uintptr_t>(Y) % 4)
+        return fail(ALV_ERR_ALIGN, "X and Y need 4-byte alignment");
+    int dev = -1;
+    if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    if (dev != w->device) return fail(ALV_ERR_HANDLE, "FFN handle belongs to device %d, current device is %d", w->device, dev);
+    GemvLaunch op[2];
+    ffn_ops(w, w->a, X, ldx, Y, ldy, M, op);
+    for (const GemvLaunch& L : op) {
+        const int64_t need = gemv_split_bytes(L);
+        if (need < 0) return fail(ALV_ERR_RANGE, "no launch plan for M=%d H=%d I=%d", M, w->H, w->I);
+        if ((size_t)need > kStaticPartBytes)
+            return fail(ALV_ERR_RANGE, "M=%d H=%d I=%d needs %lld bytes of split-K partial sums; the fixed scratch holds %zu",
+                        M, w->H, w->I, (long long)need, kStaticPartBytes);
+    }
+    hipStream_t s = (hipStream_t)stream;
+    SplitBuf sb;
+    if (int rc = static_split(dev, s, &sb)) return rc;
+    for (GemvLaunch& L : op) {
+        L.split = &sb;
+        if (int rc = launch_gemv(L, s)) return rc;
+    }
+    w->last_a = w->a;
+    w->a_rows = M;
     return ALV_OK;
 }
 

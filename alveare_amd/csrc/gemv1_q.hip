@@ -652,6 +652,13 @@ int max_tokens(const GemvLaunch& L) {
 
 namespace {
 
+// Split-K partial sums of one launch of m tokens under plan p:
+// [row][ks][token][matrix] floats.
+size_t split_part_bytes(const GemvLaunch& L, const Gemv1Plan& p) {
+    const int RT = (L.N + 15) / 16;
+    return (size_t)RT * 16 * p.ks * p.sh.mt * (L.glu ? 2 : 1) * sizeof(float);
+}
+
 // Kernel arguments of tokens [m0, m0 + m) of L under plan p.
 int fill_args(const GemvLaunch& L, const Gemv1Plan& p, int m0, int m, hipStream_t s, Gemv1Args* out) {
     const TileGeom tg = tile_geom(L.K);
@@ -665,13 +672,21 @@ int fill_args(const GemvLaunch& L, const Gemv1Plan& p, int m0, int m, hipStream_
     if (xbytes >= 0x7FFFFF00ull) return fail(ALV_ERR_RANGE, "activation buffer exceeds the 2 GiB range");
     Gemv1Args a{};
     if (p.ks > 1) {
-        Workspace ws;
-        if (int rc = get_workspace(s, kSplitCounters, &ws)) return rc;
-        a.cnt = ws.counters;
-        const size_t pb = (size_t)RT * 16 * p.ks * p.sh.mt * (L.glu ? 2 : 1) * sizeof(float);
-        void* part = nullptr;
-        if (int rc = get_scratch(s, kScratchSplit, pb, &part)) return rc;
-        a.part = static_cast<float*>(part);
+        const size_t pb = split_part_bytes(L, p);
+        if (L.split) {
+            if (pb > L.split->part_bytes)
+                return fail(ALV_ERR_RANGE, "split-K partial sums of %zu bytes exceed the %zu provided", pb,
+                            L.split->part_bytes);
+            a.cnt = L.split->counters;
+            a.part = L.split->part;
+        } else {
+            Workspace ws;
+            if (int rc = get_workspace(s, kSplitCounters, &ws)) return rc;
+            a.cnt = ws.counters;
+            void* part = nullptr;
+            if (int rc = get_scratch(s, kScratchSplit, pb, &part)) return rc;
+            a.part = static_cast<float*>(part);
+        }
         a.pbytes = (uint32_t)pb;
     }
     a.W0 = L.W0;
@@ -700,6 +715,22 @@ int fill_args(const GemvLaunch& L, const Gemv1Plan& p, int m0, int m, hipStream_
 }
 
 }  // namespace
+
+// Token groups of a launch: as equal a size as the capacity allows (16 tokens
+// at a capacity of 5: four groups of 4, not 5 + 5 + 5 + 1).
+int64_t gemv_split_bytes(const GemvLaunch& L) {
+    const int mmax = L.M >= 1 && L.M <= kGemvMaxM ? max_tokens(L) : 0;
+    if (!mmax) return -1;
+    const int ngroups = (L.M + mmax - 1) / mmax;
+    const int gsize = (L.M + ngroups - 1) / ngroups;
+    size_t most = 0;
+    for (int m0 = 0; m0 < L.M; m0 += gsize) {
+        Gemv1Plan p;
+        if (!plan_gemv1(L, std::min(gsize, L.M - m0), &p)) return -1;
+        if (p.ks > 1) most = std::max(most, split_part_bytes(L, p));
+    }
+    return (int64_t)most;
+}
 
 int launch_gemv(const GemvLaunch& L, hipStream_t s) {
     if (L.M < 1 || L.M > kGemvMaxM) return fail(ALV_ERR_ARG, "streaming GEMV takes 1 <= M <= %d (got %d)", kGemvMaxM, L.M);

@@ -43,6 +43,16 @@ int get_scratch(hipStream_t s, int slot, size_t bytes, void** out);
 // Largest split-K partial-sum block of one streaming GEMV launch.
 constexpr size_t kPartMax = 256u << 20;
 
+// Split-K temporaries a caller provides in place of the per-stream ones:
+// kSplitCounters arrival counters (zero between launches; every launch leaves
+// them zero) and `part_bytes` of partial sums. A launch whose partial sums do
+// not fit fails with ALV_ERR_RANGE before anything is enqueued.
+struct SplitBuf {
+    uint32_t* counters = nullptr;
+    float* part = nullptr;
+    size_t part_bytes = 0;
+};
+
 // One product on the streaming kernel (gemv1_q.hip), M <= kGemvMaxM tokens:
 //   out[m, n] = sum_k X[m, k] * dequant(W0)[n, k]            (glu == false)
 //   out[m, n] = act(bf16(X W0^T), bf16(X W1^T)) rounded to bf16 (glu == true)
@@ -65,8 +75,12 @@ struct GemvLaunch {
     bool glu = false;
     bool tiled = false;  // weights in the tiled layout (q4_device.h) instead of the combined one
     int act = ALV_ACT_GELU_TANH;
+    const SplitBuf* split = nullptr;  // caller's split-K temporaries (nullptr: the stream's)
 };
 int launch_gemv(const GemvLaunch& L, hipStream_t s);
+// The split-K partial-sum bytes launch_gemv(L) needs (0: no launch splits K),
+// or -1 when the shape has no launch plan.
+int64_t gemv_split_bytes(const GemvLaunch& L);
 
 // Arrival counters per stream: one per tile group of a split-K launch.
 constexpr int kSplitCounters = 1024;

@@ -147,6 +147,22 @@ int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int ldx, int ldy
                   void* stream);
 
 /*
+ * alv_ffn_fused for M <= 16 tokens (decode and small-M verification) that
+ * allocates nothing: the split-K partial sums and arrival counters of its two
+ * launches live in a fixed 16 MiB + 4 KiB array in device memory, one per GPU
+ * the library runs on, held until the process ends; X, Y and the handle are
+ * the caller's as in alv_ffn_fused. Calls no hipMalloc / hipFree, so it may run
+ * under HIP graph capture, inside tight serving loops and in harnesses that
+ * forbid allocation. Results are bit-identical to alv_ffn_fused. A shape whose
+ * partial sums exceed 16 MiB is rejected with ALV_ERR_RANGE before anything is
+ * enqueued; M > 16 is ALV_ERR_ARG. Every call on one GPU shares that array:
+ * calls that overlap on one GPU (concurrent streams, or replays of graphs that
+ * captured this call while other such calls run) race and must be serialised.
+ * No counterpart in the reference: it exists for callers that cannot allocate.
+ */
+int alv_ffn_fused_noalloc(alv_ffn_t w, const float* X, float* Y, int M, int ldx, int ldy, void* stream);
+
+/*
  * out[M, I] = the activation a = bf16(act(g) * u) of the handle's last
  * alv_ffn_fused call (fp32 holding bf16 values), for M up to that call's
  * token count (all tokens when it had M <= 16 or M >= 32; otherwise the last
