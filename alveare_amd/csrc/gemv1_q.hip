@@ -19,8 +19,10 @@
 //
 // Work split. A unit is one (row tile, super-step[, matrix]) tile of the
 // registered layout: 16 rows x 512 columns, 5 KiB, read by one wave as five
-// contiguous 1 KiB pieces. Workgroup b owns a contiguous run of row tiles;
-// its units are numbered tile-major, then super-step, then matrix (gate/up).
+// contiguous 1 KiB pieces. Row tiles are dealt to the workgroups in turn
+// (workgroup b: tiles b, b + G, ...), so the units in flight GPU-wide cover a
+// contiguous window of each matrix; a workgroup's units are numbered
+// tile-major, then super-step, then matrix (gate/up).
 // Wave w starts on units w, w + NW, ... (P of them, one per ring slot), so the
 // waves of a workgroup read neighbouring 5 KiB pieces of HBM; after that a
 // wave takes the next unit from a workgroup counter in LDS whenever it frees a
@@ -59,7 +61,8 @@ struct Gemv1Args {
     uint32_t xbytes;    // activation buffer range (M tokens)
     int N, K, nb, nss, ng_last;
     int ldx, ldy, M;
-    int rt_q, rt_r;  // tile group t owns rt_q + (t < rt_r) row tiles
+    int ntg;         // tile groups: group t owns row tiles t, t + ntg, t + 2 ntg, ...
+    int rt_q, rt_r;  // so group t owns rt_q + (t < rt_r) row tiles
     int ks;          // K splits: workgroup b is tile group b / ks, super-step range b % ks
     int act;
 };
@@ -92,21 +95,28 @@ __device__ __forceinline__ void stage_octet(const u32x4 (&v)[2], __bf16* dst) {
     }
 }
 
-// The work of workgroup b: row tiles [rt0, rt0 + nt) x super-steps [s0, s0 + nsw).
+// The work of workgroup b: row tiles tg, tg + ntg, ... (nt of them) x
+// super-steps [s0, s0 + nsw). Row tiles are dealt to the tile groups in turn,
+// so at any moment the workgroups stream neighbouring tiles: the bytes in
+// flight GPU-wide form one contiguous window per matrix (DRAM pages are read
+// whole while open), not one stream per workgroup.
 struct WgWork {
-    int tg, kq, rt0, nt, s0, nsw;
+    int tg, kq, ntg, nt, s0, nsw;
 };
 
 __device__ __forceinline__ WgWork wg_work(const Gemv1Args& a, int b) {
     WgWork w;
     w.tg = b / a.ks;
     w.kq = b - w.tg * a.ks;
-    w.rt0 = w.tg * a.rt_q + min(w.tg, a.rt_r);
+    w.ntg = a.ntg;
     w.nt = a.rt_q + (w.tg < a.rt_r ? 1 : 0);
     w.s0 = w.kq * a.nss / a.ks;
     w.nsw = (w.kq + 1) * a.nss / a.ks - w.s0;
     return w;
 }
+
+// Row tile of the workgroup's local tile tl.
+__device__ __forceinline__ int tile_row(const WgWork& wk, int tl) { return wk.tg + tl * wk.ntg; }
 
 // Byte offset of unit u's tile in its matrix, the plane step of its pieces,
 // its super-step (absolute) and matrix index. Units of a workgroup:
@@ -126,7 +136,7 @@ __device__ __forceinline__ UnitPos unit_pos(const Gemv1Args& a, const WgWork& wk
     p.n = NT == 2 ? u & 1 : 0;
     const int tl = t / wk.nsw;
     p.ss = wk.s0 + t - tl * wk.nsw;
-    p.off = (uint32_t)(wk.rt0 + tl) * a.rtb + (uint32_t)p.ss * (TL ? 5120u : 320u);
+    p.off = (uint32_t)tile_row(wk, tl) * a.rtb + (uint32_t)p.ss * (TL ? 5120u : 320u);
     p.step = TL ? (p.ss == a.nss - 1 ? 256u * (uint32_t)a.ng_last : 1024u) : 16u;
     return p;
 }
@@ -182,9 +192,7 @@ struct PhaseT {
 // block 4 g + bl with g = (o / 16) % 4, bl = (o / 4) % 4, dword t = o % 4
 // of the block -- rows m * R + p (token-major) or p * MT + m (term-major)
 // of the slot's RM rows. Tokens past M (a launch's last group) read zeros.
-// SC1: the activations were written earlier in the same launch by other
-// workgroups (agent-scope stores): read them past this XCD's L2.
-template <int NW, int R, bool XB, int MT, bool TB, bool SC1>
+template <int NW, int R, bool XB, int MT, bool TB>
 __device__ __forceinline__ void stage_acts(const Gemv1Args& a, const WgWork& wk, __bf16* xs, int tid) {
     using Ph = PhaseT<R, XB, false, MT, TB>;
     const int octs = wk.nsw * 64;
@@ -199,8 +207,8 @@ __device__ __forceinline__ void stage_acts(const Gemv1Args& a, const WgWork& wk,
             const int k = (wk.s0 * 64 + e - m * octs) * 8;
             const uint32_t off =
                 e < E && m < a.M && k < a.K ? (uint32_t)((m * a.ldx + k) * Ph::ES) : a.xbytes;  // past: zeros
-            xr[i][0] = SC1 ? buf_load16_sc1(rx, off) : buf_load16(rx, off);
-            xr[i][1] = XB ? u32x4{0u, 0u, 0u, 0u} : (SC1 ? buf_load16_sc1(rx, off + 16) : buf_load16(rx, off + 16));
+            xr[i][0] = buf_load16(rx, off);
+            xr[i][1] = XB ? u32x4{0u, 0u, 0u, 0u} : buf_load16(rx, off + 16);
         }
 #pragma unroll
         for (int i = 0; i < kXO; ++i) {
@@ -301,96 +309,101 @@ __device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& w
     }
 }
 
-template <bool THROUGH>
 __device__ __forceinline__ void ystore(const Gemv1Args& a, int m, int row, float out) {
-    if (a.Yb) {
-        const uint16_t b = __builtin_bit_cast(uint16_t, (__bf16)out);
-        if constexpr (THROUGH)
-            __hip_atomic_store(&a.Yb[(size_t)m * a.ldy + row], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else
-            a.Yb[(size_t)m * a.ldy + row] = b;
-    } else {
-        if constexpr (THROUGH)
-            __hip_atomic_store(&a.Y[(size_t)m * a.ldy + row], out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else
-            a.Y[(size_t)m * a.ldy + row] = out;
-    }
+    if (a.Yb)
+        a.Yb[(size_t)m * a.ldy + row] = __builtin_bit_cast(uint16_t, (__bf16)out);
+    else
+        a.Y[(size_t)m * a.ldy + row] = out;
+}
+
+// GLU of one output: the float64 arithmetic of the reference for one token
+// (a few values per lane: a wave with any lane on the float64 path would run
+// both), the float32 fast path with its float64 fallback for several.
+template <int MT>
+__device__ __forceinline__ float glu_out(float g, float u, int act) {
+    return bf16_round(MT == 1 ? glu_exact(bf16_round(g), bf16_round(u), act) : glu_act(bf16_round(g), bf16_round(u), act));
 }
 
 // ---- 4. per row: sum the unit slots in a fixed order --------------------------------
 // D row m * R + p (token m, term p; term-major: row m, terms summed) of
-// column jj sits in slot lane 16 * (row / 4) + jj, element row % 4. Wave w
-// takes rows 16 w .. 16 w + 15 of the workgroup (then 16 NW further on); four
-// lanes share a row: lane c sums super-steps c, c + 4, ... in ascending order
-// and the four partial sums combine in a fixed butterfly, so the result does
-// not depend on timing; lane c of the four finishes tokens c, c + 4, ...
-// Split K: this workgroup's shares go out instead, and the last workgroup of
-// the tile group adds them (section 5). THROUGH: the outputs are read later in
-// the same launch by other workgroups (agent-scope stores).
-template <int NW, int R, bool GLU, int MT, bool TB, bool THROUGH>
-__device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk, const f32x4* part, int* flag,
-                                            int tid) {
+// column jj sits in slot lane 16 * (row / 4) + jj, element row % 4. One wave
+// finishes the 16 rows of a row tile; four lanes share a row: lane c sums
+// super-steps c, c + 4, ... in ascending order and the four partial sums
+// combine in a fixed butterfly, so the result does not depend on timing;
+// lane c of the four finishes tokens c, c + 4, ... Split K: this workgroup's
+// shares go out instead, and the last workgroup of the tile group adds them
+// (section 5).
+template <int R, bool GLU, int MT, bool TB>
+__device__ __forceinline__ void finish_tile(const Gemv1Args& a, const WgWork& wk, const f32x4* part, int tl,
+                                            int lane) {
     using Ph = PhaseT<R, false, GLU, MT, TB>;
     constexpr int NT = Ph::NT, US = Ph::US;
     constexpr bool QUAD = Ph::QUAD;
-    const int lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 3;
-    const bool split = a.ks > 1;
-    for (int r0 = w * 16; r0 < wk.nt * 16; r0 += NW * 16) {
-        const int rid = r0 + (lane >> 2);
-        const int tl = rid >> 4, jj = rid & 15;
-        float y[MT][NT];
+    const int jj = lane >> 2;
+    float y[MT][NT];
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
+    for (int m = 0; m < MT; ++m)
 #pragma unroll
-            for (int n = 0; n < NT; ++n) y[m][n] = 0.0f;
-        for (int ss = c; ss < wk.nsw; ss += 4) {
+        for (int n = 0; n < NT; ++n) y[m][n] = 0.0f;
+    for (int ss = c; ss < wk.nsw; ss += 4) {
 #pragma unroll
-            for (int n = 0; n < NT; ++n) {
-                const f32x4* sl = part + ((size_t)(tl * wk.nsw + ss) * NT + n) * US + (QUAD ? 0 : jj);
+        for (int n = 0; n < NT; ++n) {
+            const f32x4* sl = part + ((size_t)(tl * wk.nsw + ss) * NT + n) * US + (QUAD ? 0 : jj);
 #pragma unroll
-                for (int m = 0; m < MT; ++m) {
-                    float v = 0.0f;
-                    if constexpr (QUAD) {
-                        v = reinterpret_cast<const float*>(sl)[m * 16 + jj];
-                    } else {
+            for (int m = 0; m < MT; ++m) {
+                float v = 0.0f;
+                if constexpr (QUAD) {
+                    v = reinterpret_cast<const float*>(sl)[m * 16 + jj];
+                } else {
 #pragma unroll
-                        for (int p = 0; p < (TB ? 1 : R); ++p) {
-                            const int row = TB ? m : m * R + p;
-                            v += sl[(row >> 2) * 16][row & 3];
-                        }
+                    for (int p = 0; p < (TB ? 1 : R); ++p) {
+                        const int row = TB ? m : m * R + p;
+                        v += sl[(row >> 2) * 16][row & 3];
                     }
-                    y[m][n] += v;
                 }
+                y[m][n] += v;
             }
-        }
-#pragma unroll
-        for (int m = 0; m < MT; ++m)
-#pragma unroll
-            for (int n = 0; n < NT; ++n) {
-                y[m][n] += __shfl_xor(y[m][n], 1);
-                y[m][n] += __shfl_xor(y[m][n], 2);
-            }
-        const int row = (wk.rt0 + tl) * 16 + jj;
-        if (row >= a.N) continue;
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            if ((m & 3) != c || m >= a.M) continue;
-            if (split) {
-                // This workgroup's share of K, written through for the last of
-                // the ks workgroups of the tile group to add up.
-                float* dst = a.part + (((size_t)row * a.ks + wk.kq) * MT + m) * NT;
-#pragma unroll
-                for (int n = 0; n < NT; ++n)
-                    __hip_atomic_store(dst + n, y[m][n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                continue;
-            }
-            float out = y[m][0];
-            if constexpr (GLU) out = bf16_round(glu_exact(bf16_round(y[m][0]), bf16_round(y[m][NT - 1]), a.act));
-            ystore<THROUGH>(a, m, row, out);
         }
     }
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            y[m][n] += __shfl_xor(y[m][n], 1);
+            y[m][n] += __shfl_xor(y[m][n], 2);
+        }
+    const int row = tile_row(wk, tl) * 16 + jj;
+    if (row >= a.N) return;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        if ((m & 3) != c || m >= a.M) continue;
+        if (a.ks > 1) {
+            // This workgroup's share of K, written through for the last of
+            // the ks workgroups of the tile group to add up.
+            float* dst = a.part + (((size_t)row * a.ks + wk.kq) * MT + m) * NT;
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+                __hip_atomic_store(dst + n, y[m][n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            continue;
+        }
+        float out = y[m][0];
+        if constexpr (GLU) out = glu_out<MT>(y[m][0], y[m][NT - 1], a.act);
+        ystore(a, m, row, out);
+    }
+}
+
+// Every tile of the workgroup (wave w: tiles w, w + NW, ...), then the split-K
+// fixup (section 5). Split-K launches finish here, after all their units.
+template <int NW, int R, bool GLU, int MT, bool TB>
+__device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk, const f32x4* part, int* flag,
+                                            int tid) {
+    using Ph = PhaseT<R, false, GLU, MT, TB>;
+    constexpr int NT = Ph::NT;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool split = a.ks > 1;
+    for (int tl = w; tl < wk.nt; tl += NW) finish_tile<R, GLU, MT, TB>(a, wk, part, tl, lane);
     if (!split) return;
 
     // ---- 5. split K: the last workgroup of the tile group adds the shares ---------
@@ -409,7 +422,7 @@ __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk
     const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.part, a.pbytes);
     for (int i = tid; i < wk.nt * 16 * MT; i += 64 * NW) {  // one (row, token) per thread
         const int r = i / MT, m = i - r * MT;
-        const int row = wk.rt0 * 16 + r;
+        const int row = tile_row(wk, r >> 4) * 16 + (r & 15);
         if (row >= a.N || m >= a.M) continue;
         const uint32_t base = (uint32_t)((((size_t)row * a.ks) * MT + m) * NT * sizeof(float));
         float y[NT];
@@ -421,8 +434,8 @@ __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk
             for (int n = 0; n < NT; ++n)
                 y[n] += __builtin_bit_cast(float, buf_load4_sc1(rp, base + (uint32_t)(((size_t)kq * MT * NT + n) * 4)));
         float out = y[0];
-        if constexpr (GLU) out = bf16_round(glu_exact(bf16_round(y[0]), bf16_round(y[NT - 1]), a.act));
-        ystore<THROUGH>(a, m, row, out);
+        if constexpr (GLU) out = glu_out<MT>(y[0], y[NT - 1], a.act);
+        ystore(a, m, row, out);
     }
     if (tid == 0) __hip_atomic_store(&a.cnt[wk.tg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -448,7 +461,7 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
 
     // The activation is staged before any weight load: queued behind the
     // weight loads of every CU it would wait for (bytes in flight) / bandwidth.
-    stage_acts<NW, R, XB, MT, TB, false>(a, wk, xs, tid);
+    stage_acts<NW, R, XB, MT, TB>(a, wk, xs, tid);
     lds_barrier();
 
     // ---- 2. the first P units of this wave -----------------------------------------
@@ -481,7 +494,7 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
         }
     }
     lds_barrier();
-    finish_rows<NW, R, GLU, MT, TB, false>(a, wk, part, next, tid);
+    finish_rows<NW, R, GLU, MT, TB>(a, wk, part, next, tid);
 }
 
 struct DevInfo {
@@ -706,6 +719,7 @@ int fill_args(const GemvLaunch& L, const Gemv1Plan& p, int m0, int m, hipStream_
     a.ldx = L.ldx;
     a.ldy = L.ldy;
     a.M = m;
+    a.ntg = p.tg;
     a.rt_q = p.rt_q;
     a.rt_r = p.rt_r;
     a.ks = p.ks;

@@ -272,7 +272,7 @@ def main() -> int:
     }
     breakdown = {}
     for k, (fn, per) in ops.items():
-        us = graph_us(torch, fn, 3, nl * per)
+        us = graph_us(torch, fn, 10, nl * per)
         breakdown[k] = {"us": round(us, 3), "GBps": round(lb[k] / us / 1e3, 1)}
 
     floor = read_floor(torch, aa, dev)
