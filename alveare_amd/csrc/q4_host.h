@@ -30,7 +30,8 @@ int get_workspace(hipStream_t s, size_t counters, Workspace* out);
 // allocated, for launches whose temporaries grow with their shape: slot 0 the
 // prefill GEMM's (counters, partial tiles, activation terms), slot 1 the
 // streaming GEMV's split-K partial sums (rewritten by every such launch before
-// it is read), slot 2 the FFN activation of prefill-sized calls. A call that
+// it is read), slot 2 the FFN activation of prefill-sized calls, slot 3 the
+// LM head's argmax pairs. A call that
 // fits what the slot holds allocates nothing. Growing allocates a new block
 // (at least twice the old capacity) and keeps the old one allocated for the
 // life of the process, since a HIP graph captured earlier may still use it;
@@ -39,6 +40,7 @@ int get_workspace(hipStream_t s, size_t counters, Workspace* out);
 constexpr int kScratchGemm = 0;
 constexpr int kScratchSplit = 1;
 constexpr int kScratchAct = 2;
+constexpr int kScratchHead = 3;  // the LM head's per-workgroup argmax pairs
 int get_scratch(hipStream_t s, int slot, size_t bytes, void** out);
 // Largest split-K partial-sum block of one streaming GEMV launch.
 constexpr size_t kPartMax = 256u << 20;

@@ -356,10 +356,36 @@ def chain_run(ops, M: int = 1) -> None:
         check(lib().alv_chain_run(arr, len(ops), M, torch.cuda.current_stream(dev).cuda_stream), "alv_chain_run")
 
 
+def lm_head(W: "Q4Weight", x: torch.Tensor, vocab: int | None = None, softcap: float = 30.0,
+            logits: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """LM head of a decode step (alv_lm_head): logits[:vocab] =
+    softcap * tanh(bf16(W x) / softcap) in float32 (softcap 0: the bf16
+    logits) and the greedy token, np.argmax of the logits, as a 1-element
+    int32 tensor on the device (runtime/py/model.py:904-916,
+    runtime/py/sampler.py:9; runtime/cpp/src/generator.cpp:15-52)."""
+    if not isinstance(W, Q4Weight):
+        raise TypeError("W must be a registered Q4Weight")
+    vocab = W.N if vocab is None else int(vocab)
+    xv = _act_in(x, W.K, "x")
+    if xv.device != W.device:
+        raise ValueError(f"x on {xv.device}, weights on {W.device}")
+    if logits is None:
+        logits = torch.empty(vocab, dtype=torch.float32, device=W.device)
+    _need_gpu(logits)
+    if logits.dtype != torch.float32 or not logits.is_contiguous():
+        raise TypeError("logits must be a contiguous float32 tensor")
+    _too_small("logits", logits.numel(), vocab)
+    token = torch.empty(1, dtype=torch.int32, device=W.device)
+    with torch.cuda.device(W.device):
+        check(lib().alv_lm_head(W.handle, xv.data_ptr(), logits.data_ptr(), vocab, float(softcap),
+                                token.data_ptr(), _stream(xv)), "alv_lm_head")
+    return logits, token
+
+
 # The reference's names for the same ops.
 gemv_q_npu = gemv_q
 gemm_q_npu = gemm_q
 ffn_fused_npu = ffn_fused
 
-__all__ = ["gemv_q", "gemm_q", "ffn_fused", "dequant_q4", "q4_tile", "Q4Weight", "FfnWeights", "chain_run",
+__all__ = ["gemv_q", "gemm_q", "ffn_fused", "dequant_q4", "q4_tile", "Q4Weight", "FfnWeights", "chain_run", "lm_head",
            "pack_ffn_fused_weights", "gemv_q_npu", "gemm_q_npu", "ffn_fused_npu"]

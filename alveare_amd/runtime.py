@@ -35,7 +35,7 @@ from pathlib import Path
 import numpy as np
 import torch
 
-from .ops import FfnWeights, Q4Weight, gemm_q, gemv_q, pack_ffn_fused_weights
+from .ops import FfnWeights, Q4Weight, gemm_q, gemv_q, lm_head, pack_ffn_fused_weights
 
 PROJECTIONS = ["attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"]
 
@@ -175,7 +175,23 @@ class Q4Dispatch:
         y = ffn(x)
         return self._out(y)
 
-    def run_gemm_npu(self, W_combined, x_bf16) -> torch.Tensor:
+    def run_lm_head(self, W_head, x_norm, vocab_size: int | None = None, softcap: float = 30.0):
+        """The head of the reference's decode step (runtime/py/model.py:904-916
+        for Gemma; softcap 0 for models without one): x_norm zero-padded to the
+        head's K, logits = bf16(W x) sliced to the vocabulary and softcapped in
+        float32, plus the greedy token (runtime/py/sampler.py:9). Returns
+        (logits, token): float32 logits on the GPU (host NumPy with host_io)
+        and the token as an int."""
+        rw = self.resident(W_head)
+        N, K = _shape_of(rw)
+        x = self._x(x_norm, K).float()
+        logits, token = lm_head(rw.q4(), x, vocab_size or N, softcap)
+        tok = int(token.item())
+        if self.host_io:
+            return logits.cpu().numpy(), tok
+        return logits, tok
+
+    def run_gemm_npu(self, W_combined, x_bf16):
         rw = self.resident(W_combined)
         N, K = _shape_of(rw)
         X = self._x(x_bf16, K)

@@ -322,6 +322,23 @@ def main() -> int:
     extra["prefill_ffn_m512"] = {"us": round(us, 2), "TFLOPs": round(flops / us / 1e6, 1),
                                  "mfma_frac_bf16_dense": round(flops / us / 1e6 / 2500.0, 4)}
 
+    # LM head: the reference's 262144 x 4096 Q4 head (671 MB, beyond the
+    # Infinity Cache), GEMV + softcap 30 + greedy argmax per call.
+    VOC, KH = 262144, 4096
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0xA1E00600)
+    head = aa.Q4Weight(synth_q4_dev(torch, VOC, KH, gen, dev), VOC, KH)
+    torch.cuda.empty_cache()
+    xh = torch.zeros(KH, device=dev)
+    xh[:H] = torch.randn(H, device=dev, generator=gen)
+    lh = torch.empty(VOC, device=dev)
+    us = graph_us(torch, lambda: [aa.lm_head(head, xh, VOC, 30.0, lh) for _ in range(8)], 5, 8)
+    hb = q4_bytes(VOC, KH) + 4 * KH + 4 * VOC
+    extra["lm_head_262144x4096"] = {"us": round(us, 2), "GBps": round(hb / us / 1e3, 1),
+                                    "pct_of_peak": round(100 * hb / us / 1e3 / HBM_PEAK_GBS, 1)}
+    head.close()
+    del head
+
     from alveare_amd import profiling
 
     out = {

@@ -112,6 +112,21 @@ int alv_gemv(alv_weight_t w, const float* X, float* Y, int M, int ldx, int ldy, 
 void alv_weight_release(alv_weight_t w);
 
 /*
+ * LM head of a decode step on a registered projection w (N rows >= vocab,
+ * K columns): logits[i] = softcap * tanh(bf16(W x)[i] / softcap) in float32
+ * for i < vocab (softcap = 0: the bf16 logits themselves), and *argmax = the
+ * first index of the largest logit, NaN counting as largest (np.argmax).
+ * x is K fp32 values; logits (vocab floats) and argmax (one int32) are device
+ * memory. Replaces the head GEMV chunks of Generator::run_lm_head
+ * (runtime/cpp/src/generator.cpp:28-52, weights uploaded at
+ * runtime/cpp/src/weights.cpp:198-224) with Generator::sample's greedy pick
+ * (generator.cpp:15-26), and the Python head with its softcap
+ * (runtime/py/model.py:904-916) and sampler (runtime/py/sampler.py:9).
+ */
+int alv_lm_head(alv_weight_t w, const float* x, float* logits, int vocab, float softcap, int32_t* argmax,
+                void* stream);
+
+/*
  * The kernels' tiled layout of a combined-layout matrix: byte size (0 for a
  * bad shape) and the repack itself into `out` (device, alv_q4_tiled_bytes
  * bytes). Test / parity entry points: registration performs this repack, the

@@ -10,6 +10,9 @@ numpy expressions, so numpy decides dtype promotion and the matmul order:
 * ``gemv_q_combined``       -- ``tools/ref/gemv_q.py:73-80`` (value before the cast)
 * ``ffn_cpu``               -- ``runtime/py/model.py:797-806`` (gelu) and
                               ``:853-860`` (silu)
+* ``lm_head_cpu``           -- ``runtime/py/model.py:904-916`` (bf16 logits,
+                              vocabulary slice, float32 softcap) and
+                              ``runtime/py/sampler.py:9`` (greedy np.argmax)
 """
 from __future__ import annotations
 
@@ -65,3 +68,19 @@ def ffn_cpu(Wg: np.ndarray, Wu: np.ndarray, Wd: np.ndarray, x: np.ndarray, act: 
     a = bf16_rne(np.asarray(geglu_out).astype(np.float32))
     y = dequantize_combined(Wd).astype(np.float32) @ a.astype(np.float32)
     return (y, a) if return_act else y
+
+
+def lm_head_cpu(y_fp32: np.ndarray, vocab: int, softcap: float = 30.0):
+    """The reference's head after its GEMV: y_fp32 is the GEMV's fp32 value
+    (the oracle's gemv_q); the GEMV returns bf16, the model slices to the
+    vocabulary and softcaps in float32 (numpy's own division and tanh), the
+    sampler takes np.argmax. softcap 0: the C++ generator's raw logits
+    (runtime/cpp/src/generator.cpp:48)."""
+    logits = bf16_rne(np.asarray(y_fp32, np.float32))
+    logits_unmasked = logits[:vocab].astype(np.float32)
+    if softcap:
+        out = softcap * np.tanh(logits_unmasked / softcap)
+    else:
+        out = logits_unmasked
+    out = np.asarray(out, np.float32)
+    return out, int(np.argmax(out))

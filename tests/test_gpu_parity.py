@@ -676,3 +676,116 @@ def test_glu_bit_exact(orc, dev, act):
     bad = np.nonzero(got.view(np.uint32) != want.view(np.uint32))[0]
     _say(f"  glu act={act}: {g.size} pairs, {bad.size} mismatches")
     assert bad.size == 0, f"first mismatches at g={g[bad[:4]]}, u={u[bad[:4]]}: {got[bad[:4]]} vs {want[bad[:4]]}"
+
+
+# ---- LM head ---------------------------------------------------------------------
+
+def _absdot(orc, W, x, N, K, chunk=4096):
+    """sum_k |w_ik x_k| per row in fp64 (the scale of row i's fp32 rounding
+    error), in row chunks so a 262144-row head fits in memory."""
+    W = np.asarray(W).reshape(N, K // 32 * 20)
+    xa = np.abs(np.asarray(x, np.float64))
+    out = np.empty(N)
+    for r0 in range(0, N, chunk):
+        n = min(chunk, N - r0)
+        out[r0:r0 + n] = np.abs(parity.deq_f64(orc, np.ascontiguousarray(W[r0:r0 + n]), n, K)) @ xa
+    return out
+
+
+def _head_check(orc, W, x, N, K, vocab, softcap, logits, token, y_ref=None):
+    """Logits of the GPU head against the reference's head evaluated by NumPy
+    (oracle/q4_numpy.py::lm_head_cpu on the oracle's fp32 GEMV). The two fp32
+    GEMVs add in different orders: each logit may differ by the fp32 bound
+    2 gamma_K sum|w x| of its row, plus one bf16 ulp where that difference
+    straddles a rounding midpoint (the softcap's slope is at most 1), plus
+    float32 ulps of NumPy's tanh (1 ulp from the correctly rounded one) and
+    the product. The token is NumPy's argmax unless the two candidates are
+    within those tolerances of each other."""
+    from oracle import q4_numpy
+
+    if y_ref is None:
+        y_ref = orc.gemv_q(W, x, N, K)
+    want, tok_ref = q4_numpy.lm_head_cpu(y_ref, vocab, softcap)
+    got = np.asarray(logits, np.float32)
+    assert got.shape == (vocab,)
+    nan_w, nan_g = np.isnan(want), np.isnan(got)
+    assert np.array_equal(nan_w, nan_g), "NaN logits differ"
+    ok = ~nan_w
+    gamma = K * parity.U32 / (1 - K * parity.U32)
+    tol_y = 2 * gamma * _absdot(orc, W, x, N, K)[:vocab]
+    yv = np.abs(np.asarray(y_ref[:vocab], np.float64))
+    tol = tol_y + (yv + tol_y) * 2.0 ** -7 + np.abs(want.astype(np.float64)) * 2.0 ** -21 + 1e-30
+    diff = np.abs(got[ok].astype(np.float64) - want[ok])
+    bad = diff > tol[ok]
+    if bad.any():
+        i = np.nonzero(ok)[0][np.argmax(bad)]
+        raise AssertionError(f"{bad.sum()} logits outside tolerance, first {i}: got {got[i]!r} want {want[i]!r} "
+                             f"y_ref {y_ref[i]!r} tol {tol[i]:.3e}")
+    exact = np.mean(got[ok] == want[ok])
+    if token != tok_ref:
+        assert not np.isnan(want[tok_ref]) and want[token] >= want[tok_ref] - tol[tok_ref] - tol[token], \
+            f"token {token} vs reference {tok_ref}: {want[token]} vs {want[tok_ref]}"
+    return exact, tok_ref
+
+
+@pytest.mark.parametrize("softcap", [30.0, 0.0])
+def test_lm_head_reduced_vocab(orc, dev, softcap):
+    """A head of 20000 x 4096 (K padded as the reference pads it, x zero past
+    3840) sliced to a 19990-token vocabulary; then a row duplicated before the
+    maximum (the first index of equal logits wins) and a NaN row (NaN wins,
+    the first one)."""
+    import alveare_amd as aa
+
+    N, K, vocab = 20000, 4096, 19990
+    seed = orc.seed_for(6, 0)
+    W = orc.synth_q4(N, K, seed)
+    x = np.zeros(K, np.float32)
+    x[:3840] = orc.synth_normal(3840, seed + 1)
+    w = aa.Q4Weight(to_dev(W, dev), N, K)
+    logits, tok = aa.lm_head(w, to_dev(x, dev), vocab, softcap)
+    exact, tref = _head_check(orc, W, x, N, K, vocab, softcap, logits.cpu().numpy(), int(tok.item()))
+    _say(f"  head softcap={softcap}: token {int(tok.item())} (reference {tref}), {exact:.4%} logits bit-equal")
+    w.close()
+
+    best = int(tok.item())
+    W2 = W.copy().reshape(N, K // 32 * 20)
+    W2[best // 2] = W2[best]          # an earlier row with the same logit wins
+    W2[vocab - 3, 16:18] = [0xC0, 0x7F]  # a NaN scale: NaN logit near the end ...
+    W2[vocab - 7, 16:18] = [0xC0, 0x7F]  # ... and an earlier one, which wins
+    w2 = aa.Q4Weight(to_dev(W2, dev), N, K)
+    logits2, tok2 = aa.lm_head(w2, to_dev(x, dev), vocab, softcap)
+    _head_check(orc, W2, x, N, K, vocab, softcap, logits2.cpu().numpy(), int(tok2.item()))
+    assert int(tok2.item()) == vocab - 7
+    W2[vocab - 3, 16:18] = W2[vocab - 7, 16:18] = 0x00
+    w2.close()
+    w3 = aa.Q4Weight(to_dev(W2, dev), N, K)
+    _, tok3 = aa.lm_head(w3, to_dev(x, dev), vocab, softcap)
+    assert int(tok3.item()) == best // 2
+    w3.close()
+
+
+def test_lm_head_full_vocab(orc, dev):
+    """The reference's head shape: 262144 x 4096 (671 MB of Q4 weights, the
+    largest GEMV of a decode step), softcap 30, whole vocabulary; then through
+    the dispatch with host NumPy output, as the reference's model graph takes
+    it."""
+    import alveare_amd as aa
+    from alveare_amd.runtime import Q4Dispatch, ResidentWeight
+
+    N, K = 262144, 4096
+    seed = orc.seed_for(6, 1)
+    W = orc.synth_q4(N, K, seed)
+    x = np.zeros(K, np.float32)
+    x[:3840] = orc.bf16_round(orc.synth_normal(3840, seed + 1))
+    Wd = to_dev(W, dev)
+    w = aa.Q4Weight(Wd, N, K)
+    logits, tok = aa.lm_head(w, to_dev(x, dev), N, 30.0)
+    y_ref = orc.gemv_q(W, x, N, K)
+    exact, tref = _head_check(orc, W, x, N, K, N, 30.0, logits.cpu().numpy(), int(tok.item()), y_ref)
+    _say(f"  head 262144x4096: token {int(tok.item())} (reference {tref}), {exact:.4%} logits bit-equal")
+    w.close()
+    d = Q4Dispatch(3840, 15360, "gemma4", dev, host_io=True)
+    rw = ResidentWeight(Wd.reshape(-1), (N, K // 32 * 20))
+    lh, th = d.run_lm_head(rw, x[:3840], N)
+    assert isinstance(lh, np.ndarray) and th == int(tok.item())
+    assert np.array_equal(lh, logits.cpu().numpy())

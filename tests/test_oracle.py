@@ -337,3 +337,31 @@ def test_synth_deterministic_and_distributed(orc):
     assert abs(x.mean()) < 0.02 and abs(x.std() - 1) < 0.02
     # Counter-based SplitMix64 (Steele et al.): first outputs for seed 0.
     assert orc.lib().orc_splitmix64_at(0, 0) == 0xE220A8397B1DCDAF
+
+
+def test_lm_head_restatement_pins():
+    """oracle/q4_numpy.py::lm_head_cpu against what the mathematics fixes:
+    bf16 logits first (a value rounds before the softcap), 30 tanh(l / 30)
+    within 4 float32 ulps of the float64 value (three float32 roundings), |logit| < 30, odd, ~l for
+    small l; softcap 0 leaves the bf16 logits; the token is the first index of
+    the maximum, NaN first."""
+    from oracle import q4_numpy
+
+    rng = np.random.default_rng(11)
+    y = (rng.standard_normal(5000) * 40).astype(np.float32)
+    out, tok = q4_numpy.lm_head_cpu(y, 4000, 30.0)
+    lb = q4_numpy.bf16_rne(y[:4000]).astype(np.float64)
+    exact = 30.0 * np.tanh(lb / 30.0)
+    assert out.dtype == np.float32 and out.shape == (4000,)
+    assert np.all(np.abs(out - exact) <= 4 * np.spacing(np.abs(exact).astype(np.float32)))
+    assert np.all(np.abs(out) <= 30.0)
+    assert tok == int(np.argmax(exact))
+    o2, _ = q4_numpy.lm_head_cpu(-y, 4000, 30.0)
+    assert np.array_equal(o2, -out)
+    small, _ = q4_numpy.lm_head_cpu(np.array([2.0 ** -10], np.float32), 1, 30.0)
+    assert small[0] == np.float32(2.0 ** -10)
+    raw, t0 = q4_numpy.lm_head_cpu(y, 4000, 0.0)
+    assert np.array_equal(raw, q4_numpy.bf16_rne(y[:4000])) and t0 == int(np.argmax(lb))
+    ties = np.array([1.0, 5.0, 5.0, np.float32(5.0009765625)], np.float32)  # the last rounds to 5.0 in bf16
+    assert q4_numpy.lm_head_cpu(ties, 4, 30.0)[1] == 1
+    assert q4_numpy.lm_head_cpu(np.array([1.0, np.nan, 9.0, np.nan], np.float32), 4, 30.0)[1] == 1
