@@ -1,6 +1,7 @@
 // Error reporting and per-stream workspace of libalveare_q4.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <map>
 #include <mutex>
@@ -122,6 +123,13 @@ int get_scratch(hipStream_t s, int slot, size_t bytes, void** out) {
     }
     *out = sc.p;
     return ALV_OK;
+}
+
+int tiled_min_m() {
+    const char* e = getenv("ALV_TILED_MIN_M");
+    if (!e || !*e) return kTiledMinM;
+    const long v = strtol(e, nullptr, 10);
+    return v >= 1 && v <= (1 << 30) ? (int)v : kTiledMinM;
 }
 
 }  // namespace alv

@@ -12,7 +12,7 @@
 //   2. down = Wd * a, with a single bf16 term per activation value (it is
 //      bf16 by construction), summed entirely on the device -- the reference
 //      sums per-core partials on the host (runtime/cpp/src/npu.cpp:360-377).
-// Prefill (M >= 32): the same two steps with the MFMA tiled kernel (gemm_q.hip);
+// Prefill (M >= 64): the same two steps with the MFMA tiled kernel (gemm_q.hip);
 // the M x I activation lives in the stream's prefill scratch (q4_host.h).
 #include <string.h>
 
@@ -130,7 +130,7 @@ extern "C" int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int l
     if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
     if (dev != w->device) return fail(ALV_ERR_HANDLE, "FFN handle belongs to device %d, current device is %d", w->device, dev);
     hipStream_t s = (hipStream_t)stream;
-    if (M >= kTiledMinM) {
+    if (M >= tiled_min_m()) {
         // Prefill: the activation goes to the stream's scratch; the handle's
         // decode buffer keeps its size and address (graphs may hold it).
         void* act = nullptr;

@@ -1,4 +1,4 @@
-// MFMA Q4 GEMM for prefill-sized batches (gfx950): the M >= 32 path of
+// MFMA Q4 GEMM for prefill-sized batches (gfx950): the M >= 64 path of
 // alv_gemm_q, alv_gemv and alv_ffn_fused (gate/up with the GLU epilogue, then
 // down).
 //

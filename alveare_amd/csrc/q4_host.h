@@ -99,8 +99,15 @@ constexpr int kGemvMaxM = 16;
 // GemvLaunch (glu pairs W0/W1 into the activation).
 int launch_gemm_tiled(const GemvLaunch& L, hipStream_t s);
 
-// M at and above which alv_gemm_q uses the tiled kernel.
-constexpr int kTiledMinM = 32;
+// M at and above which the tiled kernel runs a product (below it the
+// streaming kernel, 16 tokens per launch): kTiledMinM, or the positive value
+// of the environment variable ALV_TILED_MIN_M, read at each call (a tuning
+// knob; the benchmark times both kernels at small M with it). Measured on the
+// 12B-class FFN: the tiled kernel takes about 300 us for any M up to one
+// 256-token tile, the streaming kernel about 88 us per 16 tokens, so the
+// streaming kernel is faster up to 48 tokens.
+constexpr int kTiledMinM = 64;
+int tiled_min_m();
 
 // The two launches of one FFN call on handle w (ffn_fused.hip): gate/up with
 // the GLU epilogue into the bf16 activation `act`, then down from it.

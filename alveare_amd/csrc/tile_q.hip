@@ -141,7 +141,7 @@ extern "C" int alv_gemv(alv_weight_t w, const float* X, float* Y, int M, int ldx
     L.parts = 3;
     L.tiled = true;
     hipStream_t s = (hipStream_t)stream;
-    if (M >= kTiledMinM) {
+    if (M >= tiled_min_m()) {
         L.X = X;
         L.Y = Y;
         L.M = M;

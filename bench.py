@@ -72,50 +72,89 @@ def synth_q4_dev(torch, N: int, K: int, gen, dev):
     return W.view(N, nb * 20)
 
 
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(threads: int) -> dict:
-    """The oracle (a C restatement of the reference's CPU path) on one layer."""
+    """The oracle (a C restatement of the reference's CPU path) timed on this
+    host: one 12B-class layer per call as the reference computes it (per call
+    dequantize each matrix to fp32, fp32 matvec, the FFN's bf16 rounding
+    points) with `threads` OpenMP threads and with one; the pre-dequantized
+    variant of small models (weights dequantized at load, matvecs per call);
+    and the 2048 x 2048 gemv_q the reference publishes a CPU time for
+    (47.91 ms, tests/bench/gemv_q_bench.txt:3). Median of 10 after 2
+    warm-ups (median of 3 after 1 for the one-thread layer, to bound the
+    sample to seconds)."""
+    import ctypes
+
     import numpy as np
 
     import oracle
 
     L = oracle.lib()
-    ptr = lambda a, t: a.ctypes.data_as(t)  # noqa: E731
-    import ctypes
-
     u8, f32 = ctypes.POINTER(ctypes.c_uint8), ctypes.POINTER(ctypes.c_float)
+    ptr = lambda a, t: a.ctypes.data_as(t)  # noqa: E731
     Wq = oracle.synth_q4(N_QKV, H, oracle.seed_for(3, 0))
     Wo = oracle.synth_q4(H, K_O, oracle.seed_for(3, 1))
     Wg = oracle.synth_q4(I_FF, H, oracle.seed_for(3, 2))
     Wu = oracle.synth_q4(I_FF, H, oracle.seed_for(3, 3))
     Wd = oracle.synth_q4(H, I_FF, oracle.seed_for(3, 4))
     x = oracle.synth_normal(K_O, oracle.seed_for(3, 5))
-    yq = np.empty(N_QKV, np.float32)
-    yo = np.empty(H, np.float32)
-    yf = np.empty(H, np.float32)
+    yq, yo, yf = np.empty(N_QKV, np.float32), np.empty(H, np.float32), np.empty(H, np.float32)
 
-    def one_layer() -> float:
-        t = L.orc_time_gemv_faithful(ptr(Wq, u8), ptr(x, f32), ptr(yq, f32), N_QKV, H, 1, threads)
-        t += L.orc_time_gemv_faithful(ptr(Wo, u8), ptr(x, f32), ptr(yo, f32), H, K_O, 1, threads)
-        t += L.orc_time_ffn_faithful(ptr(Wg, u8), ptr(Wu, u8), ptr(Wd, u8), ptr(x, f32), ptr(yf, f32),
-                                     H, I_FF, 1, threads)
+    def layer(th: int, pre: bool = False) -> float:
+        g = L.orc_time_gemv_predequant if pre else L.orc_time_gemv_faithful
+        f = L.orc_time_ffn_predequant if pre else L.orc_time_ffn_faithful
+        t = g(ptr(Wq, u8), ptr(x, f32), ptr(yq, f32), N_QKV, H, 1, th)
+        t += g(ptr(Wo, u8), ptr(x, f32), ptr(yo, f32), H, K_O, 1, th)
+        t += f(ptr(Wg, u8), ptr(Wu, u8), ptr(Wd, u8), ptr(x, f32), ptr(yf, f32), H, I_FF, 1, th)
         return t
 
-    one_layer()  # warm-up
-    t1 = one_layer()
-    iters = max(1, min(10, int(12.0 / max(t1, 1e-3))))
-    ts = [t1] + [one_layer() for _ in range(iters - 1)]
-    t = statistics.median(ts)
+    def med(fn, warm: int, n: int) -> float:
+        for _ in range(warm):
+            fn()
+        return statistics.median(fn() for _ in range(n))
+
     lb = sum(layer_bytes().values())
+    t_all = med(lambda: layer(threads), 2, 10)
+    t_one = med(lambda: layer(1), 1, 3)
+    # The pre-dequantized variant holds 224 M fp32 weights (0.9 GB) per call.
+    t_pre = med(lambda: layer(threads, True), 2, 10)
+    W1 = oracle.synth_q4(2048, 2048, oracle.seed_for(1, 0))
+    x1 = oracle.synth_normal(2048, oracle.seed_for(1, 1))
+    y1 = np.empty(2048, np.float32)
+    c1 = lambda th: L.orc_time_gemv_faithful(ptr(W1, u8), ptr(x1, f32), ptr(y1, f32), 2048, 2048, 1, th)  # noqa: E731
+    c1_all, c1_one = med(lambda: c1(threads), 2, 10), med(lambda: c1(1), 2, 10)
     return {
-        "value": round(lb / t / 1e9, 4),
+        "value": round(lb / t_all / 1e9, 4),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "us_per_layer": round(t * 1e6, 1),
+        "us_per_layer": round(t_all * 1e6, 1),
+        "nproc": os.cpu_count(),
+        "cpu_model": _cpu_model(),
+        "rows": {
+            "layer_faithful_all_threads": {"threads": threads, "ms": round(t_all * 1e3, 2), "GBps": round(lb / t_all / 1e9, 3)},
+            "layer_faithful_1_thread": {"threads": 1, "ms": round(t_one * 1e3, 2), "GBps": round(lb / t_one / 1e9, 3)},
+            "layer_predequantized_all_threads": {"threads": threads, "ms": round(t_pre * 1e3, 2),
+                                                  "GBps_q4_equiv": round(lb / t_pre / 1e9, 3)},
+            "c1_gemv_2048x2048": {"ms_all_threads": round(c1_all * 1e3, 3), "ms_1_thread": round(c1_one * 1e3, 3),
+                                  "reference_numpy_ms": 47.91},
+        },
         "sample": (f"1 layer (QKV {N_QKV}x{H} + O {H}x{K_O} + FFN {H}x{I_FF}) through the oracle's "
                    f"restatement of the reference CPU path (per call: dequantize to an fp32 matrix, "
-                   f"fp32 matvec; FFN bf16 rounding points), median of {len(ts)} after 1 warm-up, "
-                   f"{threads} OpenMP threads"),
+                   f"fp32 matvec; FFN bf16 rounding points), median of 10 after 2 warm-ups, {threads} "
+                   f"OpenMP threads (the box's CPU share; nproc {os.cpu_count()}); rows: 1 thread "
+                   f"(median of 3), pre-dequantized weights, C1 2048x2048"),
     }
 
 
@@ -322,6 +361,60 @@ def main() -> int:
     extra["prefill_ffn_m512"] = {"us": round(us, 2), "TFLOPs": round(flops / us / 1e6, 1),
                                  "mfma_frac_bf16_dense": round(flops / us / 1e6 / 2500.0, 4)}
 
+    # Where the streaming kernel should hand over to the MFMA tiled kernel
+    # (small-M decode against the 12B-class FFN): both kernels at M = 8 ... 64,
+    # selected with the library's ALV_TILED_MIN_M knob.
+    cross = {"streaming": {}, "tiled": {}}
+    xm = torch.randn(64 * H, device=dev)
+    ym = torch.empty(64 * H, device=dev)
+    ncross = min(nl, 16)
+    prev = os.environ.get("ALV_TILED_MIN_M")
+    try:
+        for kind, knob in (("streaming", "1000000"), ("tiled", "1")):
+            os.environ["ALV_TILED_MIN_M"] = knob
+            for M in (8, 16, 32, 48, 64):
+                us = graph_us(torch, lambda: [ffn(xm, ym, M=M) for _, _, ffn in layers[:ncross]], 2, ncross)
+                cross[kind][str(M)] = round(us, 2)
+    finally:
+        if prev is None:
+            os.environ.pop("ALV_TILED_MIN_M", None)
+        else:
+            os.environ["ALV_TILED_MIN_M"] = prev
+    extra["small_m_crossover_ffn_us"] = cross
+
+    # C1 and C2 as HBM numbers: 128 distinct 2048 x 2048 weights (336 MB) and
+    # 32 distinct Gemma-3-1B-like FFNs 1152 <-> 6912 (478 MB), rotated so the
+    # working set exceeds the Infinity Cache.
+    g1 = torch.Generator(device=dev)
+    g1.manual_seed(0xA1E00100)
+    c1w = [aa.Q4Weight(synth_q4_dev(torch, 2048, 2048, g1, dev), 2048, 2048) for _ in range(128)]
+    x1 = torch.randn(2048, device=dev, generator=g1)
+    y1 = torch.empty(2048, device=dev)
+    us = graph_us(torch, lambda: [w(x1, y1) for w in c1w], 5, 128)
+    b1 = q4_bytes(2048, 2048) + 4 * 2048 * 2
+    extra["c1_gemv_2048x2048_x128"] = {"us": round(us, 3), "GBps": round(b1 / us / 1e3, 1)}
+    for w in c1w:
+        w.close()
+    del c1w
+    H2, I2 = 1152, 6912
+    g2 = torch.Generator(device=dev)
+    g2.manual_seed(0xA1E00200)
+    c2f = []
+    for _ in range(32):
+        wg, wu, wd = (synth_q4_dev(torch, I2, H2, g2, dev), synth_q4_dev(torch, I2, H2, g2, dev),
+                      synth_q4_dev(torch, H2, I2, g2, dev))
+        c2f.append(aa.FfnWeights(wg, wu, wd, H2, I2, "gelu"))
+        del wg, wu, wd
+    x2 = torch.randn(H2, device=dev, generator=g2)
+    y2 = torch.empty(H2, device=dev)
+    us = graph_us(torch, lambda: [f(x2, y2) for f in c2f], 5, 32)
+    b2 = 3 * q4_bytes(I2, H2) + 4 * H2 * 2
+    extra["c2_ffn_1152x6912_x32"] = {"us": round(us, 3), "GBps": round(b2 / us / 1e3, 1)}
+    for f in c2f:
+        f.close()
+    del c2f
+    torch.cuda.empty_cache()
+
     # LM head: the reference's 262144 x 4096 Q4 head (671 MB, beyond the
     # Infinity Cache), GEMV + softcap 30 + greedy argmax per call.
     VOC, KH = 262144, 4096
@@ -381,7 +474,7 @@ def main() -> int:
         "extra_configs": extra,
     }
     if not args.no_cpu_baseline:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        threads = args.cpu_threads or int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
         try:
             out["cpu_baseline"] = cpu_baseline(threads)
         except Exception as e:  # the baseline is reported, never required

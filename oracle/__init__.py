@@ -63,6 +63,7 @@ def lib() -> ctypes.CDLL:
         "orc_time_gemv_faithful": (ctypes.c_double, [_u8p, _f32p, _f32p, _i64, _i64, ctypes.c_int, ctypes.c_int]),
         "orc_time_gemv_predequant": (ctypes.c_double, [_u8p, _f32p, _f32p, _i64, _i64, ctypes.c_int, ctypes.c_int]),
         "orc_time_ffn_faithful": (ctypes.c_double, [_u8p, _u8p, _u8p, _f32p, _f32p, _i64, _i64, ctypes.c_int, ctypes.c_int]),
+        "orc_time_ffn_predequant": (ctypes.c_double, [_u8p, _u8p, _u8p, _f32p, _f32p, _i64, _i64, ctypes.c_int, ctypes.c_int]),
         "orc_max_threads": (ctypes.c_int, []),
     }
     for name, (res, args) in sig.items():

@@ -433,3 +433,46 @@ double orc_time_ffn_faithful(const uint8_t* Wg, const uint8_t* Wu, const uint8_t
     free(a);
     return t;
 }
+
+/* The pre-dequantized FFN (runtime/py/model.py:134-145 keeps small models'
+ * matrices dequantized at load): per call only the fp32 matvecs and the
+ * activation's rounding points (:797-806). The dequantization is outside
+ * the timed region. */
+double orc_time_ffn_predequant(const uint8_t* Wg, const uint8_t* Wu, const uint8_t* Wd,
+                               const float* x, float* y, int64_t H, int64_t I, int iters,
+                               int threads) {
+    float* wg = (float*)malloc(sizeof(float) * (size_t)(I * H));
+    float* wu = (float*)malloc(sizeof(float) * (size_t)(I * H));
+    float* wd = (float*)malloc(sizeof(float) * (size_t)(I * H));
+    float* g = (float*)malloc(sizeof(float) * (size_t)I);
+    float* u = (float*)malloc(sizeof(float) * (size_t)I);
+    float* a = (float*)malloc(sizeof(float) * (size_t)I);
+    if (!wg || !wu || !wd || !g || !u || !a) return -1.0;
+    const int64_t rh = (H / 32) * 20, ri = (I / 32) * 20;
+#pragma omp parallel for schedule(static) num_threads(threads)
+    for (int64_t r = 0; r < I; ++r) {
+        dequant_row_f32(Wg + r * rh, H, wg + r * H);
+        dequant_row_f32(Wu + r * rh, H, wu + r * H);
+    }
+#pragma omp parallel for schedule(static) num_threads(threads)
+    for (int64_t r = 0; r < H; ++r) dequant_row_f32(Wd + r * ri, I, wd + r * I);
+    double t0 = now_s();
+    for (int it = 0; it < iters; ++it) {
+#pragma omp parallel for schedule(static) num_threads(threads)
+        for (int64_t r = 0; r < I; ++r) {
+            g[r] = bf16_round(dot_f32(wg + r * H, x, H));
+            u[r] = bf16_round(dot_f32(wu + r * H, x, H));
+        }
+        orc_glu(g, u, a, I, 0);
+#pragma omp parallel for schedule(static) num_threads(threads)
+        for (int64_t r = 0; r < H; ++r) y[r] = dot_f32(wd + r * I, a, I);
+    }
+    double t = now_s() - t0;
+    free(wg);
+    free(wu);
+    free(wd);
+    free(g);
+    free(u);
+    free(a);
+    return t;
+}

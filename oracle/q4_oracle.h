@@ -77,6 +77,9 @@ double orc_time_gemv_predequant(const uint8_t* W, const float* x, float* y, int6
 double orc_time_ffn_faithful(const uint8_t* Wg, const uint8_t* Wu, const uint8_t* Wd,
                              const float* x, float* y, int64_t H, int64_t I, int iters,
                              int threads);
+double orc_time_ffn_predequant(const uint8_t* Wg, const uint8_t* Wu, const uint8_t* Wd,
+                               const float* x, float* y, int64_t H, int64_t I, int iters,
+                               int threads);
 int orc_max_threads(void);
 
 #ifdef __cplusplus

@@ -789,3 +789,33 @@ def test_lm_head_full_vocab(orc, dev):
     lh, th = d.run_lm_head(rw, x[:3840], N)
     assert isinstance(lh, np.ndarray) and th == int(tok.item())
     assert np.array_equal(lh, logits.cpu().numpy())
+
+
+@pytest.mark.parametrize("M", [1, 8, 16])
+def test_tiled_kernel_at_small_m(orc, dev, monkeypatch, M):
+    """The MFMA tiled kernel at decode-sized M (ALV_TILED_MIN_M=1 routes every
+    product to it, as the benchmark's crossover measurement does): GEMM rows
+    and FFN tokens pass the oracle."""
+    import alveare_amd as aa
+
+    monkeypatch.setenv("ALV_TILED_MIN_M", "1")
+    N, K = 3840, 15360
+    W = orc.synth_q4(N, K, 7000 + M)
+    X = orc.synth_normal(M * K, 7100 + M).reshape(M, K)
+    w = aa.Q4Weight(to_dev(W, dev), N, K)
+    Y = w(to_dev(X, dev), M=M).reshape(M, N).cpu().numpy()
+    for m in sorted({0, M - 1}):
+        parity.gemv_check(orc, W, X[m], Y[m], N, K)
+    w.close()
+    H, I = 3840, 15360
+    seed = orc.seed_for(4, 7)
+    Wg, Wu, Wd = orc.synth_q4(I, H, seed), orc.synth_q4(I, H, seed + 1), orc.synth_q4(H, I, seed + 2)
+    Xf = orc.synth_normal(M * H, seed + 3).reshape(M, H)
+    f = aa.pack_ffn_fused_weights(to_dev(Wg, dev), to_dev(Wu, dev), to_dev(Wd, dev), H, I)
+    Yf = torch.empty((M, H), device=dev)
+    f(to_dev(Xf, dev), Yf, M)
+    A = f.last_activation(M).cpu().numpy()
+    cache = {}
+    for m in sorted({0, M - 1}):
+        parity.ffn_check(orc, Wg, Wu, Wd, Xf[m], H, I, 0, Yf.cpu().numpy()[m], A[m], cache=cache)
+    f.close()
