@@ -30,8 +30,14 @@
 // Workgroups are numbered token-tile fastest: with the round-robin placement
 // of workgroups on the 8 XCDs, the workgroups of one XCD share token tiles, so
 // their activation reads hit that XCD's L2.
-// LDS rows are padded to 72 bf16 (144 bytes) so the 16-byte operand reads of
-// 16 lanes spread over the banks.
+// LDS layout (conflict-free 16-byte operand reads, measured): each tile is
+// split into 8 planes, one per 8-column octet of the step's 64 k, and a plane
+// holds 16 bytes per row. A wave's operand read (16 consecutive rows x 4
+// octets) then touches 16 consecutive 16-byte slots in each of 4 planes, and
+// the weight stores (row per lane) are contiguous. Activation rows sit at
+// slot token ^ (2 * plane) inside their aligned group of 16, so the
+// 8 lanes that store one token's 8 octets (row-major global loads) hit 8
+// different banks, and so do the stores of the next token.
 #include <algorithm>
 
 #include "q4_device.h"
@@ -44,8 +50,12 @@ namespace {
 constexpr int TM = 256;  // tokens per tile
 constexpr int TN = 128;  // weight rows per tile
 constexpr int TK = 64;   // k per step (two Q4 blocks)
-constexpr int LDR = TK + 8;  // padded LDS row length in bf16
+constexpr int KP = TK / 8;    // octet planes per step
 constexpr int kGemmThreads = 512;
+
+// bf16 offset of 16-byte slot `row` of plane p in a tile of `rows` rows.
+__device__ __forceinline__ size_t wslot(int p, int row) { return ((size_t)p * TN + row) * 8; }
+__device__ __forceinline__ size_t xslot(int p, int token) { return ((size_t)p * TM + (token ^ (2 * p))) * 8; }
 
 struct GemmArgs {
     const uint8_t* W0;
@@ -71,9 +81,9 @@ struct GemmArgs {
 template <int NT, bool TILED, bool XF32>
 __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    // [buffer][matrix][row][LDR] weights, then [buffer][token][LDR] activations.
+    // [buffer][matrix][plane][row] weights, then [buffer][plane][token] activations.
     __bf16* wsm = reinterpret_cast<__bf16*>(smem);
-    __bf16* xsm = wsm + 2 * NT * TN * LDR;
+    __bf16* xsm = wsm + (size_t)2 * NT * KP * TN * 8;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -167,16 +177,16 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
     auto store_w = [&](int b, const uint32_t (&wreg)[5]) __attribute__((always_inline)) {
         if (wstage) {
             const Scale2 sc = make_scale2(bf16_bits_to_f32(wreg[4] & 0xFFFFu));
-            __bf16* dst = wsm + ((size_t)(b * NT + wmat) * TN + wr) * LDR + 32 * wb;
+            __bf16* tile = wsm + (size_t)(b * NT + wmat) * KP * TN * 8;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) *reinterpret_cast<bf16x8*>(dst + 8 * t) = dequant8_mix(wreg[t], sc);
+            for (int t = 0; t < 4; ++t) *reinterpret_cast<bf16x8*>(tile + wslot(4 * wb + t, wr)) = dequant8_mix(wreg[t], sc);
         }
     };
     auto store_x = [&](int b, int p, const u32x4 (&xreg)[4][XV]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int r = (tid >> 3) + 64 * i, c = (tid & 7) * 8;
-            u32x4* dst = reinterpret_cast<u32x4*>(xsm + ((size_t)b * TM + r) * LDR + c);
+            const int r = (tid >> 3) + 64 * i, o = tid & 7;
+            u32x4* dst = reinterpret_cast<u32x4*>(xsm + (size_t)b * KP * TM * 8 + xslot(o, r));
             if constexpr (XF32) {
                 bf16x8 t;
 #pragma unroll
@@ -216,11 +226,11 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj)
                     bv[n][jj] = *reinterpret_cast<const bf16x8*>(
-                        wsm + ((size_t)(b * NT + n) * TN + wn * 64 + jj * 16 + j) * LDR + kk * 32 + 8 * g);
+                        wsm + (size_t)(b * NT + n) * KP * TN * 8 + wslot(kk * 4 + g, wn * 64 + jj * 16 + j));
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const bf16x8 av = *reinterpret_cast<const bf16x8*>(
-                    xsm + ((size_t)b * TM + wm * 64 + i * 16 + j) * LDR + kk * 32 + 8 * g);
+                    xsm + (size_t)b * KP * TM * 8 + xslot(kk * 4 + g, wm * 64 + i * 16 + j));
 #pragma unroll
                 for (int n = 0; n < NT; ++n)
 #pragma unroll
@@ -283,22 +293,26 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
     // reads all of them (sc1) and sums them in split order, so the result does
     // not depend on which came last, then resets the count.
     if (a.ks > 1) {
+        // Each thread's accumulators go out as whole 16-byte pieces, thread
+        // tid's f32x4 (n, i, jj) at ((n * 16 + 4 i + jj) * 512 + tid) * 16 bytes
+        // of the split's partial tile, so a wave writes 1 KiB contiguous with
+        // write-through (sc1) stores -- single-float write-through stores cost
+        // a partial-line write each -- and the last workgroup's thread tid
+        // reads back exactly the pieces it adds to its own accumulators.
         const size_t tile = (size_t)blockIdx.y * gridDim.x + blockIdx.x;
         const size_t tsz = (size_t)NT * TM * TN;
-        auto at = [&](int n, int i, int jj, int r) -> size_t {
-            return ((size_t)n * TM + wm * 64 + i * 16 + 4 * g + r) * TN + wn * 64 + jj * 16 + j;
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.part + tile * a.ks * tsz, (uint32_t)(a.ks * tsz * sizeof(float)));
+        auto piece = [&](int q, int n, int i, int jj) -> uint32_t {
+            return (uint32_t)(((((size_t)q * NT + n) * 16 + 4 * i + jj) * kGemmThreads + tid) * 16);
         };
-        float* mine = a.part + (tile * a.ks + kq) * tsz;
 #pragma unroll
         for (int n = 0; n < NT; ++n)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        __hip_atomic_store(mine + at(n, i, jj, r), acc[n][i][jj][r], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[n][i][jj]), rp,
+                                                           piece(kq, n, i, jj), 0, 16);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __shared__ int last;
         __syncthreads();
@@ -307,7 +321,6 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
                    (uint32_t)(a.ks - 1);
         __syncthreads();
         if (!last) return;
-        const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.part + tile * a.ks * tsz, (uint32_t)(a.ks * tsz * sizeof(float)));
 #pragma unroll
         for (int n = 0; n < NT; ++n)
 #pragma unroll
@@ -321,10 +334,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
                 for (int i = 0; i < 4; ++i)
 #pragma unroll
                     for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            acc[n][i][jj][r] += __builtin_bit_cast(
-                                float, buf_load4_sc1(rp, (uint32_t)((q * tsz + at(n, i, jj, r)) * sizeof(float))));
+                        acc[n][i][jj] += __builtin_bit_cast(f32x4, buf_load16_sc1(rp, piece(q, n, i, jj)));
         if (tid == 0) __hip_atomic_store(&a.cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
@@ -409,7 +419,7 @@ __global__ void __launch_bounds__(256) split_x_kernel(const float* X, int ldx, i
 
 template <int NT, bool TILED, bool XF32>
 hipError_t launch_gemm(const GemmArgs& a, dim3 grid, hipStream_t s) {
-    const size_t lds = (size_t)2 * (NT * TN + TM) * LDR * sizeof(uint16_t);
+    const size_t lds = (size_t)2 * KP * (NT * TN + TM) * 8 * sizeof(uint16_t);
     static bool attr[64] = {};
     int dev = 0;
     if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;

@@ -177,11 +177,10 @@ struct PhaseT {
     static constexpr int RM = ARows<R, MT, TB>::RM, AR = ARows<R, MT, TB>::AR, DL = ARows<R, MT, TB>::DL;
     static constexpr bool QUAD = ARows<R, MT, TB>::QUAD;
     static constexpr int US = ARows<R, MT, TB>::US;
-    // Rows per operand slot in LDS: term-major slots (24 or 48 rows, a
-    // multiple of 256 bytes apart) take one row of padding so the four lane
-    // groups of an operand read fall on different banks; token quads one zero
-    // row (row RM), which is also their padding.
-    static constexpr int SR = RM + ((TB || QUAD) ? 1 : 0);
+    // Rows per operand slot in LDS: token quads add one zero row (row RM).
+    // Term-major slots (48 rows) take no padding: slots a multiple of 256
+    // bytes apart read conflict-free (measured; 784 bytes apart they conflict).
+    static constexpr int SR = RM + (QUAD ? 1 : 0);
     static_assert(AR <= 16, "MFMA row block");
     static_assert(!XB || R == 1, "bf16 activations take one term");
 };
@@ -192,6 +191,10 @@ struct PhaseT {
 // block 4 g + bl with g = (o / 16) % 4, bl = (o / 4) % 4, dword t = o % 4
 // of the block -- rows m * R + p (token-major) or p * MT + m (term-major)
 // of the slot's RM rows. Tokens past M (a launch's last group) read zeros.
+// Threads walk the slots in order (tokens fastest), so neighbouring lanes
+// store neighbouring rows of LDS (slots in octet order would put them whole
+// slots apart, on the same banks); the four lanes that load a cache line's
+// four octets sit in one instruction, so the global loads stay whole-line.
 template <int NW, int R, bool XB, int MT, bool TB>
 __device__ __forceinline__ void stage_acts(const Gemv1Args& a, const WgWork& wk, __bf16* xs, int tid) {
     using Ph = PhaseT<R, XB, false, MT, TB>;
@@ -203,8 +206,10 @@ __device__ __forceinline__ void stage_acts(const Gemv1Args& a, const WgWork& wk,
 #pragma unroll
         for (int i = 0; i < kXO; ++i) {
             const int e = e0 + tid + i * 64 * NW;
-            const int m = MT == 1 ? 0 : e / octs;
-            const int k = (wk.s0 * 64 + e - m * octs) * 8;
+            const int m = MT == 1 ? 0 : e % MT;
+            const int sl = MT == 1 ? e : e / MT;  // slot, relative to super-step s0
+            const int o = (sl >> 6) * 64 + (sl & 3) * 16 + ((sl >> 2) & 15);
+            const int k = (wk.s0 * 64 + o) * 8;
             const uint32_t off =
                 e < E && m < a.M && k < a.K ? (uint32_t)((m * a.ldx + k) * Ph::ES) : a.xbytes;  // past: zeros
             xr[i][0] = buf_load16(rx, off);
@@ -213,12 +218,9 @@ __device__ __forceinline__ void stage_acts(const Gemv1Args& a, const WgWork& wk,
 #pragma unroll
         for (int i = 0; i < kXO; ++i) {
             const int e = e0 + tid + i * 64 * NW;
-            const int m = MT == 1 ? 0 : e / octs;
-            const int o = e - m * octs;  // relative to super-step s0
-            if (e < E) {
-                const int slot = ((o >> 6) * 16 + (o & 15)) * 4 + ((o >> 4) & 3);
-                stage_octet<R, TB ? MT * 8 : 8>(xr[i], xs + ((size_t)slot * Ph::SR + (TB ? m : m * R)) * 8);
-            }
+            const int m = MT == 1 ? 0 : e % MT;
+            const int sl = MT == 1 ? e : e / MT;
+            if (e < E) stage_octet<R, TB ? MT * 8 : 8>(xr[i], xs + ((size_t)sl * Ph::SR + (TB ? m : m * R)) * 8);
         }
     }
     if constexpr (Ph::QUAD)
@@ -375,18 +377,35 @@ __device__ __forceinline__ void finish_tile(const Gemv1Args& a, const WgWork& wk
         }
     const int row = tile_row(wk, tl) * 16 + jj;
     if (row >= a.N) return;
+    if (a.ks > 1) {
+        // This workgroup's share of K, written through (sc1 stores, as
+        // agent-scope stores are) for the last of the ks workgroups of the
+        // tile group to add up: the row's MT x NT floats are contiguous, and
+        // its four lanes store them as whole 16-byte pieces, one line per row
+        // (single-float write-through stores cost a partial-line write each).
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.part, a.pbytes);
+        const uint32_t base = (uint32_t)((((size_t)row * a.ks + wk.kq) * MT) * NT * sizeof(float));
+        constexpr int F = MT * NT;
+        if constexpr (F % 4 == 0) {
+#pragma unroll
+            for (int ch = 0; ch < F / 4; ++ch) {
+                if ((ch & 3) != c) continue;
+                u32x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = __builtin_bit_cast(uint32_t, y[(4 * ch + e) / NT][(4 * ch + e) % NT]);
+                __builtin_amdgcn_raw_buffer_store_b128(v, rp, base + 16u * ch, 0, 16);
+            }
+        } else if (c == 0) {
+#pragma unroll
+            for (int f = 0; f < F; ++f)
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y[f / NT][f % NT]), rp, base + 4u * f,
+                                                      0, 16);
+        }
+        return;
+    }
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         if ((m & 3) != c || m >= a.M) continue;
-        if (a.ks > 1) {
-            // This workgroup's share of K, written through for the last of
-            // the ks workgroups of the tile group to add up.
-            float* dst = a.part + (((size_t)row * a.ks + wk.kq) * MT + m) * NT;
-#pragma unroll
-            for (int n = 0; n < NT; ++n)
-                __hip_atomic_store(dst + n, y[m][n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            continue;
-        }
         float out = y[m][0];
         if constexpr (GLU) out = glu_out<MT>(y[m][0], y[m][NT - 1], a.act);
         ystore(a, m, row, out);
@@ -420,22 +439,50 @@ __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk
     __syncthreads();
     if (!*flag) return;
     const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.part, a.pbytes);
-    for (int i = tid; i < wk.nt * 16 * MT; i += 64 * NW) {  // one (row, token) per thread
-        const int r = i / MT, m = i - r * MT;
-        const int row = tile_row(wk, r >> 4) * 16 + (r & 15);
-        if (row >= a.N || m >= a.M) continue;
-        const uint32_t base = (uint32_t)((((size_t)row * a.ks) * MT + m) * NT * sizeof(float));
-        float y[NT];
-#pragma unroll
-        for (int n = 0; n < NT; ++n) y[n] = 0.0f;
+    constexpr int F = MT * NT;
+    if constexpr (F % 4 == 0) {
+        // One (row, 16-byte piece) per thread: the piece of every split, in
+        // split order, then the piece's tokens (two (gate, up) pairs, or four
+        // outputs).
+        for (int i = tid; i < wk.nt * 16 * (F / 4); i += 64 * NW) {
+            const int r = i / (F / 4), ch = i - r * (F / 4);
+            const int row = tile_row(wk, r >> 4) * 16 + (r & 15);
+            if (row >= a.N) continue;
+            const uint32_t base = (uint32_t)(((size_t)row * a.ks * F + 4 * ch) * sizeof(float));
+            float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 4
-        for (int kq = 0; kq < a.ks; ++kq)
+            for (int kq = 0; kq < a.ks; ++kq) {
+                const u32x4 v = buf_load16_sc1(rp, base + (uint32_t)((size_t)kq * F * sizeof(float)));
 #pragma unroll
-            for (int n = 0; n < NT; ++n)
-                y[n] += __builtin_bit_cast(float, buf_load4_sc1(rp, base + (uint32_t)(((size_t)kq * MT * NT + n) * 4)));
-        float out = y[0];
-        if constexpr (GLU) out = glu_out<MT>(y[0], y[NT - 1], a.act);
-        ystore(a, m, row, out);
+                for (int e = 0; e < 4; ++e) y[e] += __builtin_bit_cast(float, (uint32_t)v[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e += NT) {
+                const int m = (4 * ch + e) / NT;
+                if (m >= a.M) continue;
+                float out = y[e];
+                if constexpr (GLU) out = glu_out<MT>(y[e], y[e + NT - 1], a.act);
+                ystore(a, m, row, out);
+            }
+        }
+    } else {
+        for (int i = tid; i < wk.nt * 16 * MT; i += 64 * NW) {  // one (row, token) per thread
+            const int r = i / MT, m = i - r * MT;
+            const int row = tile_row(wk, r >> 4) * 16 + (r & 15);
+            if (row >= a.N || m >= a.M) continue;
+            const uint32_t base = (uint32_t)((((size_t)row * a.ks) * MT + m) * NT * sizeof(float));
+            float y[NT];
+#pragma unroll
+            for (int n = 0; n < NT; ++n) y[n] = 0.0f;
+#pragma unroll 4
+            for (int kq = 0; kq < a.ks; ++kq)
+#pragma unroll
+                for (int n = 0; n < NT; ++n)
+                    y[n] += __builtin_bit_cast(float, buf_load4_sc1(rp, base + (uint32_t)(((size_t)kq * MT * NT + n) * 4)));
+            float out = y[0];
+            if constexpr (GLU) out = glu_out<MT>(y[0], y[NT - 1], a.act);
+            ystore(a, m, row, out);
+        }
     }
     if (tid == 0) __hip_atomic_store(&a.cnt[wk.tg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -634,7 +681,7 @@ bool plan_gemv1(const GemvLaunch& L, int m, Gemv1Plan* out) {
     const int RM = p.sh.mt * p.sh.r;
     const bool quad = !p.sh.tb && p.sh.r == 3 && (p.sh.mt == 2 || p.sh.mt == 4 || p.sh.mt == 8);  // ARows::QUAD
     const int AR = p.sh.tb ? p.sh.mt : RM;
-    const int SR = RM + ((p.sh.tb || quad) ? 1 : 0);  // rows per LDS operand slot (PhaseT::SR)
+    const int SR = RM + (quad ? 1 : 0);  // rows per LDS operand slot (PhaseT::SR)
     const size_t slot_bytes = quad ? (size_t)p.sh.mt * 64 : (size_t)256 * ((AR + 3) / 4);  // ARows::US * 16
     for (p.ks = 1; p.ks <= 16 && p.ks <= tg.nss; p.ks *= 2) {
         p.tg = std::min(RT, std::max(1, d.cus / p.ks));

@@ -65,6 +65,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                              0x00020000);
 }
 
+// Read a loaded vector's elements through a scalar, `(uint32_t)v[e]`: this
+// clang lowers __builtin_bit_cast(float, v[e]) on a vector element to a read
+// of element 0.
 __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }

@@ -80,6 +80,19 @@ def traffic(fetch_dir: str, write_dir: str, copy_bytes: int) -> str:
     return "\n".join(out)
 
 
+def counters(d: str) -> str:
+    """Mean per dispatch of every counter of a --pmc run, per Q4 kernel, plus
+    the ratios that matter here (LDS conflicts per access, MFMA and VALU busy
+    fractions of the wave cycles' CU share)."""
+    names = sorted({r["Counter_Name"] for r in csv.DictReader(open(_find(d, "counter_collection.csv")))})
+    means = {c: _counter_means(d, c) for c in names}
+    kernels = sorted({k for m in means.values() for k in m if any(q in k for q in Q4_KERNELS)})
+    out = ["kernel | " + " | ".join(names)]
+    for k in kernels:
+        out.append(f"{k} | " + " | ".join(f"{means[c].get(k, float('nan')):.4g}" for c in names))
+    return "\n".join(out)
+
+
 def read_traffic(path: str, kernel: str):
     """The scaled traffic of `kernel` from a committed traffic summary, or None."""
     if not os.path.exists(path):
@@ -94,6 +107,9 @@ def read_traffic(path: str, kernel: str):
 def main(argv) -> int:
     if len(argv) >= 2 and argv[0] == "stats":
         print(stats(argv[1]))
+        return 0
+    if len(argv) >= 2 and argv[0] == "counters":
+        print(counters(argv[1]))
         return 0
     if len(argv) >= 4 and argv[0] == "traffic":
         print(traffic(argv[1], argv[2], int(argv[3])))

@@ -180,7 +180,7 @@ def build_layers(torch, aa, nl, dev):
 def profile_pass(torch, aa, dev) -> int:
     """Eager launches for counter collection: a calibration copy of known size
     (torch.mul reading and writing CALIBRATION_BYTES), then 8 layers of each op
-    and the gate/up launch alone."""
+    and the gate/up launch alone, 4 FFN calls of 16 tokens and 4 of 512."""
     src = torch.ones(CALIBRATION_BYTES // 4, device=dev)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -193,6 +193,13 @@ def profile_pass(torch, aa, dev) -> int:
         wo(xs["o"], ys["o"])
         ffn.gate_up(xs["ffn"])
         ffn(xs["ffn"], ys["ffn"])
+    # 16-token decode and the M = 512 prefill (bf16-valued activations).
+    x16, y16 = torch.randn(16 * H, device=dev), torch.empty(16 * H, device=dev)
+    xp = torch.randn(512 * H, device=dev).bfloat16().float()
+    yp = torch.empty(512 * H, device=dev)
+    for _, _, ffn in layers[:4]:
+        ffn(x16, y16, M=16)
+        ffn(xp, yp, M=512)
     torch.cuda.synchronize()
     for _, _, ffn in layers:
         ffn.close()
