@@ -3,6 +3,10 @@
     python -m alveare_amd.profiling stats <dir>
         per-kernel calls / average / min / max duration from a
         ``rocprofv3 --kernel-trace --stats`` output directory.
+    python -m alveare_amd.profiling launches <dir>
+        the same run's Q4 dispatches grouped by launch shape (grid, LDS).
+    python -m alveare_amd.profiling counters <dir>
+        mean per dispatch of every counter of a ``--pmc`` run, per Q4 kernel.
     python -m alveare_amd.profiling traffic <fetch_dir> <write_dir> <copy_bytes>
         HBM bytes per dispatch of every q4 kernel from one ``--pmc FETCH_SIZE``
         and one ``--pmc WRITE_SIZE`` run of ``bench.py --profile-pass``, each
@@ -45,6 +49,25 @@ def stats(d: str) -> str:
     for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
         out.append(f"{_short(r['Name'])} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.3f} | "
                    f"{float(r['MinNs']) / 1e3:.3f} | {float(r['MaxNs']) / 1e3:.3f} | {float(r['Percentage']):.2f}")
+    return "\n".join(out)
+
+
+def launches(d: str) -> str:
+    """Q4 kernel dispatches of a --kernel-trace run grouped by launch shape
+    (kernel, grid, LDS bytes): one kernel instance serves several matrix
+    shapes, and each shape has its own duration."""
+    per = defaultdict(list)
+    for r in csv.DictReader(open(_find(d, "kernel_trace.csv"))):
+        name = _short(r["Kernel_Name"])
+        if not any(q in name for q in Q4_KERNELS):
+            continue
+        grid = "x".join(str(int(r[f"Grid_Size_{a}"]) // max(1, int(r[f"Workgroup_Size_{a}"]))) for a in "XYZ")
+        key = (name, grid, int(r["Workgroup_Size_X"]), int(r["LDS_Block_Size"]))
+        per[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    out = ["kernel | workgroups (x*y*z) | threads | LDS B | calls | avg us | median us | min us"]
+    for key, v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        out.append(f"{key[0]} | {key[1]} | {key[2]} | {key[3]} | {len(v)} | {statistics.mean(v):.3f} | "
+                   f"{statistics.median(v):.3f} | {min(v):.3f}")
     return "\n".join(out)
 
 
@@ -107,6 +130,9 @@ def read_traffic(path: str, kernel: str):
 def main(argv) -> int:
     if len(argv) >= 2 and argv[0] == "stats":
         print(stats(argv[1]))
+        return 0
+    if len(argv) >= 2 and argv[0] == "launches":
+        print(launches(argv[1]))
         return 0
     if len(argv) >= 2 and argv[0] == "counters":
         print(counters(argv[1]))

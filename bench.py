@@ -278,6 +278,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--profile-pass", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="only the headline workload (no extra_configs): the run profiled for the roofline kernel")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -347,97 +349,103 @@ def main() -> int:
     gu_us = breakdown["ffn_gate_up"]["us"]
     gu_gbs = lb["ffn_gate_up"] / (gu_us * 1e-6) / 1e9
 
-    # Small-M decode against the 12B-class FFN (M tokens share one weight
-    # read) and prefill at M = 512 (MFMA tiled kernel, GeGLU fused): per call
-    # over distinct layers.
-    extra = {"small_m_ffn": {}, "prefill_ffn_m512": None}
-    for M in (2, 4, 8, 16):
-        xm = torch.randn(M * H, device=dev)
-        ym = torch.empty(M * H, device=dev)
-        us = graph_us(torch, lambda: [ffn(xm, ym, M=M) for _, _, ffn in layers], 2, nl)
-        byts = 3 * q4_bytes(I_FF, H) + M * (4 * H + 4 * H)
-        extra["small_m_ffn"][str(M)] = {"us": round(us, 3), "GBps": round(byts / us / 1e3, 1)}
-    Mp = 512
-    # bf16-valued activations, as the reference's prefill passes them (x_bf16):
-    # one activation term per token tile.
-    xp = torch.randn(Mp * H, device=dev).bfloat16().float()
-    yp = torch.empty(Mp * H, device=dev)
-    npf = min(nl, 8)
-    us = graph_us(torch, lambda: [ffn(xp, yp, M=Mp) for _, _, ffn in layers[:npf]], 2, npf)
-    flops = 2.0 * Mp * 3 * I_FF * H
-    extra["prefill_ffn_m512"] = {"us": round(us, 2), "TFLOPs": round(flops / us / 1e6, 1),
-                                 "mfma_frac_bf16_dense": round(flops / us / 1e6 / 2500.0, 4)}
+    extra = {}
+    if not args.no_extra:
+        # Small-M decode against the 12B-class FFN (M tokens share one weight
+        # read) and prefill at M = 512 (MFMA tiled kernel, GeGLU fused): per call
+        # over distinct layers.
+        extra = {"small_m_ffn": {}, "prefill_ffn_m512": None}
+        for M in (2, 4, 8, 16):
+            xm = torch.randn(M * H, device=dev)
+            ym = torch.empty(M * H, device=dev)
+            us = graph_us(torch, lambda: [ffn(xm, ym, M=M) for _, _, ffn in layers], 2, nl)
+            byts = 3 * q4_bytes(I_FF, H) + M * (4 * H + 4 * H)
+            extra["small_m_ffn"][str(M)] = {"us": round(us, 3), "GBps": round(byts / us / 1e3, 1)}
+        Mp = 512
+        # bf16-valued activations, as the reference's prefill passes them (x_bf16):
+        # one activation term per token tile.
+        xp = torch.randn(Mp * H, device=dev).bfloat16().float()
+        yp = torch.empty(Mp * H, device=dev)
+        npf = min(nl, 8)
+        us = graph_us(torch, lambda: [ffn(xp, yp, M=Mp) for _, _, ffn in layers[:npf]], 2, npf)
+        flops = 2.0 * Mp * 3 * I_FF * H
+        extra["prefill_ffn_m512"] = {"us": round(us, 2), "TFLOPs": round(flops / us / 1e6, 1),
+                                     "mfma_frac_bf16_dense": round(flops / us / 1e6 / 2500.0, 4)}
 
-    # Where the streaming kernel should hand over to the MFMA tiled kernel
-    # (small-M decode against the 12B-class FFN): both kernels at M = 8 ... 64,
-    # selected with the library's ALV_TILED_MIN_M knob.
-    cross = {"streaming": {}, "tiled": {}}
-    xm = torch.randn(64 * H, device=dev)
-    ym = torch.empty(64 * H, device=dev)
-    ncross = min(nl, 16)
-    prev = os.environ.get("ALV_TILED_MIN_M")
-    try:
-        for kind, knob in (("streaming", "1000000"), ("tiled", "1")):
-            os.environ["ALV_TILED_MIN_M"] = knob
-            for M in (8, 16, 32, 48, 64):
-                us = graph_us(torch, lambda: [ffn(xm, ym, M=M) for _, _, ffn in layers[:ncross]], 2, ncross)
-                cross[kind][str(M)] = round(us, 2)
-    finally:
-        if prev is None:
-            os.environ.pop("ALV_TILED_MIN_M", None)
-        else:
-            os.environ["ALV_TILED_MIN_M"] = prev
-    extra["small_m_crossover_ffn_us"] = cross
+        # Where the streaming kernel should hand over to the MFMA tiled kernel
+        # (small-M decode against the 12B-class FFN): both kernels at M = 8 ... 128,
+        # selected with the library's ALV_TILED_MIN_M knob, for fp32 activations
+        # (three bf16 terms on the tiled kernel) and bf16-valued ones (one term).
+        cross = {}
+        xm32 = torch.randn(128 * H, device=dev)
+        xm16 = xm32.bfloat16().float()
+        ym = torch.empty(128 * H, device=dev)
+        ncross = min(nl, 16)
+        prev = os.environ.get("ALV_TILED_MIN_M")
+        try:
+            for xname, xm in (("x_fp32", xm32), ("x_bf16_valued", xm16)):
+                for kind, knob in (("streaming", "1000000"), ("tiled", "1")):
+                    os.environ["ALV_TILED_MIN_M"] = knob
+                    row = cross.setdefault(f"{kind}_{xname}", {})
+                    for M in (8, 16, 32, 48, 64, 96, 128):
+                        us = graph_us(torch, lambda: [ffn(xm, ym, M=M) for _, _, ffn in layers[:ncross]], 2, ncross)
+                        row[str(M)] = round(us, 2)
+        finally:
+            if prev is None:
+                os.environ.pop("ALV_TILED_MIN_M", None)
+            else:
+                os.environ["ALV_TILED_MIN_M"] = prev
+        extra["small_m_crossover_ffn_us"] = cross
 
-    # C1 and C2 as HBM numbers: 128 distinct 2048 x 2048 weights (336 MB) and
-    # 32 distinct Gemma-3-1B-like FFNs 1152 <-> 6912 (478 MB), rotated so the
-    # working set exceeds the Infinity Cache.
-    g1 = torch.Generator(device=dev)
-    g1.manual_seed(0xA1E00100)
-    c1w = [aa.Q4Weight(synth_q4_dev(torch, 2048, 2048, g1, dev), 2048, 2048) for _ in range(128)]
-    x1 = torch.randn(2048, device=dev, generator=g1)
-    y1 = torch.empty(2048, device=dev)
-    us = graph_us(torch, lambda: [w(x1, y1) for w in c1w], 5, 128)
-    b1 = q4_bytes(2048, 2048) + 4 * 2048 * 2
-    extra["c1_gemv_2048x2048_x128"] = {"us": round(us, 3), "GBps": round(b1 / us / 1e3, 1)}
-    for w in c1w:
-        w.close()
-    del c1w
-    H2, I2 = 1152, 6912
-    g2 = torch.Generator(device=dev)
-    g2.manual_seed(0xA1E00200)
-    c2f = []
-    for _ in range(32):
-        wg, wu, wd = (synth_q4_dev(torch, I2, H2, g2, dev), synth_q4_dev(torch, I2, H2, g2, dev),
-                      synth_q4_dev(torch, H2, I2, g2, dev))
-        c2f.append(aa.FfnWeights(wg, wu, wd, H2, I2, "gelu"))
-        del wg, wu, wd
-    x2 = torch.randn(H2, device=dev, generator=g2)
-    y2 = torch.empty(H2, device=dev)
-    us = graph_us(torch, lambda: [f(x2, y2) for f in c2f], 5, 32)
-    b2 = 3 * q4_bytes(I2, H2) + 4 * H2 * 2
-    extra["c2_ffn_1152x6912_x32"] = {"us": round(us, 3), "GBps": round(b2 / us / 1e3, 1)}
-    for f in c2f:
-        f.close()
-    del c2f
-    torch.cuda.empty_cache()
+        # C1 and C2 as HBM numbers: 128 distinct 2048 x 2048 weights (336 MB) and
+        # 32 distinct Gemma-3-1B-like FFNs 1152 <-> 6912 (478 MB), rotated so the
+        # working set exceeds the Infinity Cache.
+        g1 = torch.Generator(device=dev)
+        g1.manual_seed(0xA1E00100)
+        c1w = [aa.Q4Weight(synth_q4_dev(torch, 2048, 2048, g1, dev), 2048, 2048) for _ in range(128)]
+        x1 = torch.randn(2048, device=dev, generator=g1)
+        y1 = torch.empty(2048, device=dev)
+        us = graph_us(torch, lambda: [w(x1, y1) for w in c1w], 5, 128)
+        b1 = q4_bytes(2048, 2048) + 4 * 2048 * 2
+        extra["c1_gemv_2048x2048_x128"] = {"us": round(us, 3), "GBps": round(b1 / us / 1e3, 1)}
+        for w in c1w:
+            w.close()
+        del c1w
+        H2, I2 = 1152, 6912
+        g2 = torch.Generator(device=dev)
+        g2.manual_seed(0xA1E00200)
+        c2f = []
+        for _ in range(32):
+            wg, wu, wd = (synth_q4_dev(torch, I2, H2, g2, dev), synth_q4_dev(torch, I2, H2, g2, dev),
+                          synth_q4_dev(torch, H2, I2, g2, dev))
+            c2f.append(aa.FfnWeights(wg, wu, wd, H2, I2, "gelu"))
+            del wg, wu, wd
+        x2 = torch.randn(H2, device=dev, generator=g2)
+        y2 = torch.empty(H2, device=dev)
+        us = graph_us(torch, lambda: [f(x2, y2) for f in c2f], 5, 32)
+        b2 = 3 * q4_bytes(I2, H2) + 4 * H2 * 2
+        extra["c2_ffn_1152x6912_x32"] = {"us": round(us, 3), "GBps": round(b2 / us / 1e3, 1)}
+        for f in c2f:
+            f.close()
+        del c2f
+        torch.cuda.empty_cache()
 
-    # LM head: the reference's 262144 x 4096 Q4 head (671 MB, beyond the
-    # Infinity Cache), GEMV + softcap 30 + greedy argmax per call.
-    VOC, KH = 262144, 4096
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(0xA1E00600)
-    head = aa.Q4Weight(synth_q4_dev(torch, VOC, KH, gen, dev), VOC, KH)
-    torch.cuda.empty_cache()
-    xh = torch.zeros(KH, device=dev)
-    xh[:H] = torch.randn(H, device=dev, generator=gen)
-    lh = torch.empty(VOC, device=dev)
-    us = graph_us(torch, lambda: [aa.lm_head(head, xh, VOC, 30.0, lh) for _ in range(8)], 5, 8)
-    hb = q4_bytes(VOC, KH) + 4 * KH + 4 * VOC
-    extra["lm_head_262144x4096"] = {"us": round(us, 2), "GBps": round(hb / us / 1e3, 1),
-                                    "pct_of_peak": round(100 * hb / us / 1e3 / HBM_PEAK_GBS, 1)}
-    head.close()
-    del head
+        # LM head: the reference's 262144 x 4096 Q4 head (671 MB, beyond the
+        # Infinity Cache), GEMV + softcap 30 + greedy argmax per call.
+        VOC, KH = 262144, 4096
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(0xA1E00600)
+        head = aa.Q4Weight(synth_q4_dev(torch, VOC, KH, gen, dev), VOC, KH)
+        torch.cuda.empty_cache()
+        xh = torch.zeros(KH, device=dev)
+        xh[:H] = torch.randn(H, device=dev, generator=gen)
+        lh = torch.empty(VOC, device=dev)
+        us = graph_us(torch, lambda: [aa.lm_head(head, xh, VOC, 30.0, lh) for _ in range(8)], 5, 8)
+        hb = q4_bytes(VOC, KH) + 4 * KH + 4 * VOC
+        extra["lm_head_262144x4096"] = {"us": round(us, 2), "GBps": round(hb / us / 1e3, 1),
+                                        "pct_of_peak": round(100 * hb / us / 1e3 / HBM_PEAK_GBS, 1)}
+        head.close()
+        del head
 
     from alveare_amd import profiling
 
