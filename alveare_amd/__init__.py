@@ -7,11 +7,12 @@ and the ``runtime/py`` dispatch (``alveare_amd.runtime``) on top.
 """
 from ._lib import LibraryNotBuilt, Q4Error, Q4ValueError, lib
 from .ops import (FfnWeights, Q4Weight, chain_run, dequant_q4, ffn_fused, ffn_fused_npu,
-                  gemm_q, gemm_q_npu, gemv_q, gemv_q_npu, lm_head, pack_ffn_fused_weights, q4_tile)
+                  gemm_q, gemm_q_npu, gemv_q, gemv_q_npu, lm_head, pack_ffn_fused_weights, q4_tile,
+                  quantize_q4)
 from .runtime import LazyLayerWeights, Q4Dispatch, ResidentWeight
 
 __all__ = [
     "FfnWeights", "LazyLayerWeights", "LibraryNotBuilt", "Q4Dispatch", "Q4Error", "Q4ValueError",
     "Q4Weight", "ResidentWeight", "chain_run", "dequant_q4", "ffn_fused", "ffn_fused_npu", "gemm_q", "gemm_q_npu",
-    "gemv_q", "gemv_q_npu", "lib", "lm_head", "pack_ffn_fused_weights", "q4_tile",
+    "gemv_q", "gemv_q_npu", "lib", "lm_head", "pack_ffn_fused_weights", "q4_tile", "quantize_q4",
 ]

@@ -43,6 +43,8 @@ SIGNATURES: dict[str, tuple] = {
     "alv_gemv": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "alv_weight_release": (None, [_vp]),
     "alv_lm_head": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _vp, _vp]),
+    "alv_quantize_q4": (_i, [_vp, _i, _i, _i, _vp, _i, _i, _vp]),
+    "alv_weight_quantize": (_i, [_vp, _i, _i, _i, _i, _i, ctypes.POINTER(_vp), _vp]),
     "alv_q4_tiled_bytes": (ctypes.c_uint64, [_i, _i]),
     "alv_q4_tile": (_i, [_vp, _vp, _i, _i, _vp]),
     "alv_chain_run": (_i, [_vp, _i, _i, _vp]),

@@ -171,10 +171,51 @@ def q4_tile(W: torch.Tensor, N: int, K: int) -> torch.Tensor:
     return out
 
 
+def _float_source(W: torch.Tensor, N: int | None, K: int | None):
+    if W.dim() != 2 or W.dtype != torch.float32:
+        raise ValueError(f"W must be a 2-D float32 tensor (got {tuple(W.shape)} {W.dtype})")
+    _need_gpu(W)
+    if W.stride(1) != 1:
+        W = W.contiguous()
+    n_src, k_src = W.shape
+    N = n_src if N is None else N
+    K = k_src if K is None else K
+    if N < n_src or K < k_src:
+        raise ValueError(f"target {N} x {K} smaller than the source {n_src} x {k_src}")
+    _check_shape(N, K)
+    return W, n_src, k_src, N, K
+
+
+def quantize_q4(W: torch.Tensor, N: int | None = None, K: int | None = None) -> torch.Tensor:
+    """quantize_to_q4_0 + pack_to_combined (tools/convert/gemv_q_convert.py:5-85)
+    on the GPU: float32 W (n, k) -> uint8 (N, K/32*20), zero-padded to N x K
+    as quantize_and_pack_tensor does (tools/quantize_gemma4.py:26-41)."""
+    W, n_src, k_src, N, K = _float_source(W, N, K)
+    out = torch.empty((N, K // 32 * 20), dtype=torch.uint8, device=W.device)
+    with torch.cuda.device(W.device):
+        check(lib().alv_quantize_q4(W.data_ptr(), n_src, k_src, W.stride(0), out.data_ptr(), N, K, _stream(W)),
+              "alv_quantize_q4")
+    return out
+
+
 class Q4Weight:
     """A registered projection (runtime/cpp/src/npu.cpp:241-253
     create_gemv_weight): a device copy in the kernels' tiled layout, used by
-    ``gemv``/``__call__``. Released on ``close()`` or garbage collection."""
+    ``gemv``/``__call__``. Released on ``close()`` or garbage collection.
+    ``Q4Weight.quantize(W_fp32, N, K)`` quantizes float32 weights on the GPU
+    straight into this layout."""
+
+    @classmethod
+    def quantize(cls, W: torch.Tensor, N: int | None = None, K: int | None = None) -> "Q4Weight":
+        W, n_src, k_src, N, K = _float_source(W, N, K)
+        self = cls.__new__(cls)
+        self.N, self.K, self.device = N, K, W.device
+        self._h = ctypes.c_void_p()
+        with torch.cuda.device(W.device):
+            check(lib().alv_weight_quantize(W.data_ptr(), n_src, k_src, W.stride(0), N, K, ctypes.byref(self._h),
+                                            _stream(W)), "alv_weight_quantize")
+        self.shape = (N, K // 32 * 20)
+        return self
 
     def __init__(self, W: torch.Tensor, N: int, K: int):
         _check_shape(N, K)

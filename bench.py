@@ -447,6 +447,25 @@ def main() -> int:
         head.close()
         del head
 
+        # GPU quantizer on the LM head's float32 weights (262144 x 3840, 4.03 GB)
+        # zero-padded to 4096 columns, as the reference's quantizer pads it
+        # (tools/quantize_gemma4.py:130-133): bytes = fp32 read + Q4 written.
+        wq = torch.randn(VOC, H, device=dev, generator=gen).mul_(0.02)
+        qout = torch.empty((VOC, KH // 32 * 20), dtype=torch.uint8, device=dev)
+        L = aa.lib()
+
+        def quant():
+            st = torch.cuda.current_stream().cuda_stream
+            rc = L.alv_quantize_q4(wq.data_ptr(), VOC, H, H, qout.data_ptr(), VOC, KH, st)
+            if rc:
+                raise RuntimeError(f"alv_quantize_q4 failed ({rc})")
+
+        us = graph_us(torch, quant, 5, 1)
+        qb = 4 * VOC * H + q4_bytes(VOC, KH)
+        extra["quantize_262144x3840_to_4096"] = {"us": round(us, 1), "GBps": round(qb / us / 1e3, 1)}
+        del wq, qout
+        torch.cuda.empty_cache()
+
     from alveare_amd import profiling
 
     out = {

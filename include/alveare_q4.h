@@ -127,6 +127,29 @@ int alv_lm_head(alv_weight_t w, const float* x, float* logits, int vocab, float 
                 void* stream);
 
 /*
+ * Quantize float32 weights to the Q4 combined layout on the GPU:
+ * quantize_to_q4_0 + pack_to_combined (tools/convert/gemv_q_convert.py:5-85)
+ * with the zero padding of quantize_and_pack_tensor
+ * (tools/quantize_gemma4.py:26-41). W holds n_src rows of ldw floats (the
+ * first k_src of each are read); out receives the (N, K/32*20) combined
+ * matrix, N >= n_src, K >= k_src, K a multiple of 32, weights past the source
+ * quantized as zeros. Per block: scale = max|w| / 7 (float32; 0 -> 1.0; NaN
+ * if the block holds a NaN), codes clip(round-half-even(w / scale), -8, 7)
+ * with a NaN quotient -> -8 (numpy on x86-64), bf16 scale round-to-nearest-even.
+ * W and out need 4-byte alignment. Asynchronous on `stream`.
+ */
+int alv_quantize_q4(const float* W, int n_src, int k_src, int ldw, uint8_t* out, int N, int K, void* stream);
+
+/*
+ * alv_quantize_q4 straight into a registered projection (the kernels' tiled
+ * layout; a temporary combined copy is allocated and freed). The counterpart
+ * of quantizing on the host and registering with create_gemv_weight
+ * (runtime/cpp/src/weights.cpp:192-330). Synchronises `stream`.
+ */
+int alv_weight_quantize(const float* W, int n_src, int k_src, int ldw, int N, int K, alv_weight_t* out,
+                        void* stream);
+
+/*
  * The kernels' tiled layout of a combined-layout matrix: byte size (0 for a
  * bad shape) and the repack itself into `out` (device, alv_q4_tiled_bytes
  * bytes). Test / parity entry points: registration performs this repack, the

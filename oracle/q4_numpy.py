@@ -10,6 +10,8 @@ numpy expressions, so numpy decides dtype promotion and the matmul order:
 * ``gemv_q_combined``       -- ``tools/ref/gemv_q.py:73-80`` (value before the cast)
 * ``ffn_cpu``               -- ``runtime/py/model.py:797-806`` (gelu) and
                               ``:853-860`` (silu)
+* ``quantize_to_q4_0``      -- ``tools/convert/gemv_q_convert.py:5-51`` and
+                              ``pack_to_combined`` ``:53-85``
 * ``lm_head_cpu``           -- ``runtime/py/model.py:904-916`` (bf16 logits,
                               vocabulary slice, float32 softcap) and
                               ``runtime/py/sampler.py:9`` (greedy np.argmax)
@@ -84,3 +86,25 @@ def lm_head_cpu(y_fp32: np.ndarray, vocab: int, softcap: float = 30.0):
         out = logits_unmasked
     out = np.asarray(out, np.float32)
     return out, int(np.argmax(out))
+
+
+def quantize_to_q4_0(W: np.ndarray) -> np.ndarray:
+    """The reference quantizer followed by pack_to_combined, in the
+    reference's numpy expressions: (N, K/32*20) uint8. bf16 scales by
+    bf16_rne (ml_dtypes' float32 -> bfloat16 is round-to-nearest-even)."""
+    W = np.asarray(W, dtype=np.float32)
+    N, K = W.shape
+    W_blocks = W.reshape(N, K // 32, 32)
+    max_vals = np.max(np.abs(W_blocks), axis=2)
+    scales = max_vals / 7.0
+    scales[scales == 0.0] = 1.0
+    with np.errstate(invalid="ignore"):
+        q_blocks = np.round(W_blocks / np.expand_dims(scales, axis=2)).astype(np.int32)
+    q = np.clip(q_blocks, -8, 7).reshape(N, K)
+    w_q4 = ((q[:, 0::2] & 0x0F) | ((q[:, 1::2] & 0x0F) << 4)).astype(np.uint8)
+    sb = (bf16_rne(scales).view(np.uint32) >> 16).astype(np.uint16)
+    out = np.zeros((N, K // 32, 20), np.uint8)
+    out[:, :, :16] = w_q4.reshape(N, K // 32, 16)
+    out[:, :, 16] = sb & 0xFF
+    out[:, :, 17] = sb >> 8
+    return out.reshape(N, K // 32 * 20)

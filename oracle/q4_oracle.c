@@ -26,7 +26,10 @@
  *                      g=0 / u=0 special cases, fp64 brute force.
  *   orc_gemm_q         every row equals orc_gemv_q (runtime/cpp/src/main.cpp:98-108).
  *   orc_quantize_q4_0  hand-computed blocks (ties to even, clipping, zero
- *                      block -> scale 1.0) and |dequant(quant(W)) - W| <= s/2.
+ *                      block -> scale 1.0), |dequant(quant(W)) - W| <= s/2, and
+ *                      byte equality with the reference's numpy expressions
+ *                      (oracle/q4_numpy.py) on random, tie, subnormal, NaN
+ *                      and inf blocks.
  */
 #include "q4_oracle.h"
 
@@ -271,19 +274,23 @@ void orc_quantize_q4_0(const float* Wf, int64_t N, int64_t K, uint8_t* out) {
     for (int64_t r = 0; r < N; ++r)
         for (int64_t b = 0; b < nb; ++b) {
             const float* w = Wf + r * K + b * 32;
-            /* :24-25: scale = max|w| / 7 in float32. */
+            /* :24-25: scale = max|w| / 7 in float32; np.max propagates NaN. */
             float mx = 0.0f;
+            int nan = 0;
             for (int i = 0; i < 32; ++i) {
                 float a = fabsf(w[i]);
+                if (a != a) nan = 1;
                 if (a > mx) mx = a;
             }
-            float s = mx / 7.0f;
+            float s = nan ? NAN : mx / 7.0f;
             if (s == 0.0f) s = 1.0f; /* :28 */
             int q[32];
             for (int i = 0; i < 32; ++i) {
-                /* :34-37: np.round (half to even) of a float32 quotient, clip. */
+                /* :34-37: np.round (half to even) of a float32 quotient,
+                 * astype(int32), clip. A NaN quotient (a NaN block, or inf / inf)
+                 * converts to INT32_MIN on x86-64 (cvttss2si) and clips to -8. */
                 float v = rintf(w[i] / s);
-                int qi = (int)v;
+                int qi = v != v ? -8 : (int)v;
                 q[i] = qi < -8 ? -8 : (qi > 7 ? 7 : qi);
             }
             uint8_t* blk = out + r * rs + b * 20;

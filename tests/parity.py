@@ -151,3 +151,23 @@ def tile_layout_np(W: np.ndarray, N: int, K: int) -> np.ndarray:
                     dst = rt * rtb + ss * 5120 + i * 256 * ng + g * 256
                     out[dst:dst + 256] = runs[:, 16 * i:16 * i + 16].reshape(-1)
     return out
+
+
+def quant_cases():
+    """Random blocks plus the edge cases of quantize_to_q4_0: exact ties of
+    w / s at +-0.5, 1.5, ... (np.round to even), all-zero blocks, subnormal
+    blocks whose max / 7 underflows to 0 (scale 1.0), a NaN and an inf block."""
+    rng = np.random.default_rng(7)
+    w = rng.normal(0.0, 0.05, size=(24, 256)).astype(np.float32)
+    w[0, :32] = np.array([7.0, 0.5, 1.5, 2.5, 3.5, -0.5, -2.5, -3.5] + [0.25] * 24, np.float32)  # s = 1: ties
+    w[1, :32] = np.arange(-16, 16, dtype=np.float32) * np.float32(0.5)  # max 8 -> s = 8/7
+    w[2, :64] = 0.0
+    w[3, :32] = np.float32(1e-45) * np.arange(32, dtype=np.float32)  # subnormals
+    w[4, :32] = np.float32(3e-38)
+    w[5, 32:64] = np.nan
+    w[6, 64] = np.nan
+    w[7, 96] = np.inf
+    w[8, 128:160] = -np.inf
+    w[9, :32] = -0.0
+    w[10, :32] = np.float32(1e-45) * np.array([0, 1, 2, 3] * 8, np.float32)  # max / 7 underflows to 0
+    return w

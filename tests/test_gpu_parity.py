@@ -819,3 +819,54 @@ def test_tiled_kernel_at_small_m(orc, dev, monkeypatch, M):
     for m in sorted({0, M - 1}):
         parity.ffn_check(orc, Wg, Wu, Wd, Xf[m], H, I, 0, Yf.cpu().numpy()[m], A[m], cache=cache)
     f.close()
+
+
+# ---- quantizer (tools/convert/gemv_q_convert.py:5-85) ----------------------------
+
+def test_quantize_matches_oracle(orc, dev):
+    import alveare_amd as aa
+
+    _say("quantize: edge-case blocks (ties, zeros, subnormals, NaN, inf) and 512 x 4096 N(0, 0.02)")
+    w = parity.quant_cases()
+    got = aa.quantize_q4(to_dev(w, dev)).cpu().numpy()
+    assert np.array_equal(got, orc.quantize_q4_0(w))
+    rng = np.random.default_rng(11)
+    w2 = rng.normal(0.0, 0.02, size=(512, 4096)).astype(np.float32)
+    got2 = aa.quantize_q4(to_dev(w2, dev)).cpu().numpy()
+    assert np.array_equal(got2, orc.quantize_q4_0(w2))
+
+
+def test_quantize_padded_source(orc, dev):
+    """quantize_and_pack_tensor (tools/quantize_gemma4.py:26-41): a 300 x 3800
+    view with row stride 3840 zero-padded to 320 x 4096, as the reference pads
+    the Gemma-4 projections before quantizing."""
+    import alveare_amd as aa
+
+    rng = np.random.default_rng(12)
+    big = rng.normal(0.0, 0.02, size=(300, 3840)).astype(np.float32)
+    src = to_dev(big, dev)[:, :3800]
+    assert src.stride(0) == 3840
+    got = aa.quantize_q4(src, 320, 4096).cpu().numpy()
+    pad = np.zeros((320, 4096), np.float32)
+    pad[:300, :3800] = big[:, :3800]
+    assert np.array_equal(got, orc.quantize_q4_0(pad))
+
+
+def test_quantize_into_registered_weight(orc, dev):
+    """Q4Weight.quantize gives the weight registering the quantized bytes
+    gives: the same GEMV output, bit for bit, and that output passes the GEMV
+    bar against the oracle on the oracle's quantization."""
+    import alveare_amd as aa
+
+    rng = np.random.default_rng(13)
+    N, K = 1000, 2048
+    w = rng.normal(0.0, 0.02, size=(N, K)).astype(np.float32)
+    x = orc.synth_normal(K, 14)
+    wd, xd = to_dev(w, dev), to_dev(x, dev)
+    a = aa.Q4Weight.quantize(wd)
+    b = aa.Q4Weight(aa.quantize_q4(wd), N, K)
+    ya, yb = a(xd).cpu().numpy(), b(xd).cpu().numpy()
+    a.close()
+    b.close()
+    assert np.array_equal(ya, yb)
+    parity.gemv_check(orc, orc.quantize_q4_0(w), x, ya, N, K)

@@ -365,3 +365,19 @@ def test_lm_head_restatement_pins():
     ties = np.array([1.0, 5.0, 5.0, np.float32(5.0009765625)], np.float32)  # the last rounds to 5.0 in bf16
     assert q4_numpy.lm_head_cpu(ties, 4, 30.0)[1] == 1
     assert q4_numpy.lm_head_cpu(np.array([1.0, np.nan, 9.0, np.nan], np.float32), 4, 30.0)[1] == 1
+
+
+def test_quantize_matches_numpy_restatement(orc):
+    w = parity.quant_cases()
+    a = orc.quantize_q4_0(w)
+    b = q4_numpy.quantize_to_q4_0(w)
+    assert np.array_equal(a, b)
+    # NaN blocks: every code -8, scale the quiet NaN 0x7FC0; an inf block: its
+    # finite weights quantize to 0, the inf (inf / inf) to -8, scale 0x7F80.
+    q = orc.unpack_q4(a, 24, 256)
+    s = orc.scales_q4(a, 24, 256)
+    assert np.all(q[5, 32:64] == -8) and s[5, 1] == 0x7FC0
+    assert q[6, 64] == -8 and np.all(q[6, 65:96] == -8) and s[6, 2] == 0x7FC0
+    assert q[7, 96] == -8 and np.all(q[7, 97:128] == 0) and s[7, 3] == 0x7F80
+    assert np.all(q[10, :32] == 0) and s[10, 0] == 0x3F80
+    assert q[3, 31] == 7 and s[3, 0] == 0  # subnormal scale 3 * 2^-149 rounds to bf16 +0
