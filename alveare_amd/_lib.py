@@ -44,6 +44,14 @@ SIGNATURES: dict[str, tuple] = {
     "alv_weight_release": (None, [_vp]),
     "alv_lm_head": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _vp, _vp]),
     "alv_quantize_q4": (_i, [_vp, _i, _i, _i, _vp, _i, _i, _vp]),
+    "alv_gemv_bf16": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "alv_ffn_fused_bf16": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "alv_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, ctypes.c_float, _vp]),
+    "alv_qkv_post": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _i, ctypes.c_float, _vp, _i, _i, _i, _i,
+                          _vp, _i, _vp, _vp, _vp, _vp]),
+    "alv_attention": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, ctypes.c_float, _vp, _vp]),
+    "alv_add_norm": (_i, [_vp, _i, _vp, _i, _vp, _i, ctypes.c_float, _i, _vp, _i, _vp, _vp, _i, _i, _i, _i,
+                          ctypes.c_float, _vp]),
     "alv_weight_quantize": (_i, [_vp, _i, _i, _i, _i, _i, ctypes.POINTER(_vp), _vp]),
     "alv_q4_tiled_bytes": (ctypes.c_uint64, [_i, _i]),
     "alv_q4_tile": (_i, [_vp, _vp, _i, _i, _vp]),

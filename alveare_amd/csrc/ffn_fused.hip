@@ -155,6 +155,50 @@ extern "C" int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int l
     return ALV_OK;
 }
 
+extern "C" int alv_ffn_fused_bf16(alv_ffn_t w, const uint16_t* X, uint16_t* Y, int M, int ldx, int ldy, void* stream) {
+    if (int rc = check_handle(w)) return rc;
+    if (!X || !Y) return fail(ALV_ERR_ARG, "null activation pointer");
+    if (M < 1 || ldx < w->H || ldy < w->H) return fail(ALV_ERR_ARG, "bad M=%d ldx=%d ldy=%d for H=%d", M, ldx, ldy, w->H);
+    if (reinterpret_cast<uintptr_t>(X) % 16 || ldx % 8 || reinterpret_cast<uintptr_t>(Y) % 2)
+        return fail(ALV_ERR_ALIGN, "X needs 16-byte aligned rows (ldx a multiple of 8), Y 2-byte alignment");
+    int dev = -1;
+    if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    if (dev != w->device) return fail(ALV_ERR_HANDLE, "FFN handle belongs to device %d, current device is %d", w->device, dev);
+    hipStream_t s = (hipStream_t)stream;
+    // The fp32 plan with bf16 ends: gate/up reads X as one bf16 term, down
+    // writes bf16 (the reference's y_bf16, runtime/cpp/src/npu.cpp:340-378).
+    auto bf16_ends = [&](GemvLaunch (&op)[2], const uint16_t* x, uint16_t* y) {
+        op[0].X = nullptr;
+        op[0].Xb = x;
+        op[0].parts = 1;
+        op[1].Y = nullptr;
+        op[1].Yb = y;
+    };
+    if (M >= tiled_min_m()) {
+        void* act = nullptr;
+        if (int rc = get_scratch(s, kScratchAct, (size_t)M * w->I * sizeof(uint16_t), &act)) return rc;
+        GemvLaunch op[2];
+        ffn_ops(w, static_cast<uint16_t*>(act), nullptr, ldx, nullptr, ldy, M, op);
+        bf16_ends(op, X, Y);
+        if (int rc = launch_gemm_tiled(op[0], s)) return rc;
+        if (int rc = launch_gemm_tiled(op[1], s)) return rc;
+        w->last_a = static_cast<uint16_t*>(act);
+        w->a_rows = M;
+        return ALV_OK;
+    }
+    for (int m0 = 0; m0 < M; m0 += kGemvMaxM) {
+        const int mc = std::min(kGemvMaxM, M - m0);
+        GemvLaunch op[2];
+        ffn_ops(w, w->a, nullptr, ldx, nullptr, ldy, mc, op);
+        bf16_ends(op, X + (size_t)m0 * ldx, Y + (size_t)m0 * ldy);
+        if (int rc = launch_gemv(op[0], s)) return rc;
+        if (int rc = launch_gemv(op[1], s)) return rc;
+        w->last_a = w->a;
+        w->a_rows = mc;
+    }
+    return ALV_OK;
+}
+
 // ---- alv_ffn_fused_noalloc ------------------------------------------------------
 // The decode FFN with its split-K temporaries (arrival counters, partial sums)
 // in `scratch`, a fixed array in device memory that every GPU the library runs

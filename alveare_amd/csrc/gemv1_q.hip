@@ -621,6 +621,15 @@ Shape shape_for(const GemvLaunch& L, int m) {
 }
 
 hipError_t launch_shape(const Gemv1Args& a, const GemvLaunch& L, Shape sh, int groups, size_t lds, hipStream_t s) {
+    if (L.Xb && L.glu) {
+        switch (sh.mt) {
+            case 1: return launch_k<kP, 1, true, true, 1>(a, groups, lds, s);
+            case 2: return launch_k<kP, 1, true, true, 2>(a, groups, lds, s);
+            case 4: return launch_k<kP, 1, true, true, 4>(a, groups, lds, s);
+            case 8: return launch_k<kP, 1, true, true, 8>(a, groups, lds, s);
+            default: return launch_k<kP, 1, true, true, 16>(a, groups, lds, s);
+        }
+    }
     if (L.Xb) {
         switch (sh.mt) {
             case 1: return launch_k<kP, 1, true, false, 1>(a, groups, lds, s);
@@ -796,7 +805,6 @@ int64_t gemv_split_bytes(const GemvLaunch& L) {
 int launch_gemv(const GemvLaunch& L, hipStream_t s) {
     if (L.M < 1 || L.M > kGemvMaxM) return fail(ALV_ERR_ARG, "streaming GEMV takes 1 <= M <= %d (got %d)", kGemvMaxM, L.M);
     if (L.parts != (L.Xb ? 1 : 3)) return fail(ALV_ERR_ARG, "fp32 activations take 3 terms, bf16 activations 1");
-    if (L.Xb && L.glu) return fail(ALV_ERR_ARG, "bf16 activations take no GLU");
     const int mmax = max_tokens(L);
     if (!mmax) return fail(ALV_ERR_RANGE, "streaming GEMV: no launch plan for M=%d N=%d K=%d", L.M, L.N, L.K);
     // Groups of as equal a size as the capacity allows (16 tokens at a

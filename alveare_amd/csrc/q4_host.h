@@ -41,6 +41,7 @@ constexpr int kScratchGemm = 0;
 constexpr int kScratchSplit = 1;
 constexpr int kScratchAct = 2;
 constexpr int kScratchHead = 3;  // the LM head's per-workgroup argmax pairs
+constexpr int kScratchAttn = 4;  // attention's arrival counters and chunk partials
 int get_scratch(hipStream_t s, int slot, size_t bytes, void** out);
 // Largest split-K partial-sum block of one streaming GEMV launch.
 constexpr size_t kPartMax = 256u << 20;

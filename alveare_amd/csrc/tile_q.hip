@@ -156,6 +156,40 @@ extern "C" int alv_gemv(alv_weight_t w, const float* X, float* Y, int M, int ldx
     return ALV_OK;
 }
 
+extern "C" int alv_gemv_bf16(alv_weight_t w, const uint16_t* X, uint16_t* Y, int M, int ldx, int ldy, void* stream) {
+    if (int rc = check_weight(w)) return rc;
+    if (!X || !Y) return fail(ALV_ERR_ARG, "null activation pointer");
+    if (M < 1 || ldx < w->K || ldy < w->N)
+        return fail(ALV_ERR_ARG, "bad M=%d ldx=%d ldy=%d for N=%d K=%d", M, ldx, ldy, w->N, w->K);
+    if (reinterpret_cast<uintptr_t>(X) % 16 || ldx % 8 || reinterpret_cast<uintptr_t>(Y) % 2)
+        return fail(ALV_ERR_ALIGN, "X needs 16-byte aligned rows (ldx a multiple of 8), Y 2-byte alignment");
+    int dev = -1;
+    if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    if (dev != w->device) return fail(ALV_ERR_HANDLE, "weight handle belongs to device %d, current device is %d", w->device, dev);
+    GemvLaunch L;
+    L.W0 = w->w;
+    L.ldx = ldx;
+    L.ldy = ldy;
+    L.N = w->N;
+    L.K = w->K;
+    L.parts = 1;
+    L.tiled = true;
+    hipStream_t s = (hipStream_t)stream;
+    if (M >= tiled_min_m()) {
+        L.Xb = X;
+        L.Yb = Y;
+        L.M = M;
+        return launch_gemm_tiled(L, s);
+    }
+    for (int m0 = 0; m0 < M; m0 += kGemvMaxM) {
+        L.Xb = X + (size_t)m0 * ldx;
+        L.Yb = Y + (size_t)m0 * ldy;
+        L.M = std::min(kGemvMaxM, M - m0);
+        if (int rc = launch_gemv(L, s)) return rc;
+    }
+    return ALV_OK;
+}
+
 extern "C" void alv_weight_release(alv_weight_t w) {
     if (!w || w->magic != kWeightMagic) return;
     int cur = -1;

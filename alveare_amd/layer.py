@@ -1,0 +1,276 @@
+"""Device-resident decode layer: the reference's per-layer host work on the GPU.
+
+The reference runs a decode layer as NPU matmuls with numpy (Python runtime,
+``runtime/py/model.py:705-790``) or C++ (``runtime/cpp/src/model.cpp:314-420``)
+host code between them: RMSNorms, per-head q/k/v norms, RoPE, the KV-cache
+insert, attention, residual adds and the layer output scale, with a host round
+trip for every matmul. Here the whole layer is a sequence of launches on one
+stream over device tensors (bf16 activations, bf16 KV caches), so the layer
+never leaves the GPU and a token step can be captured in one HIP graph.
+
+Op wrappers (bf16 tensors are ``torch.bfloat16``; float32 norm weights):
+
+=====================  ======================================================
+``rmsnorm``            run_rmsnorm_cpu (model.py:522-531), bit-exact
+``qkv_post``           q/k/v norms + RoPE + cache insert (model.py:742-770)
+``attention``          run_attention_host (model.py:577-628), float32
+``add_norm``           residual (+ scale) (+ next norm) (model.py:775-788)
+``gemv_bf16``          run_gemv_npu: bf16 in, bf16 out (model.py:283-362)
+``ffn_fused_bf16``     run_ffn_fused_npu: bf16 in, bf16 out (model.py:363-397)
+=====================  ======================================================
+
+``Gemma4DecodeLayer`` composes them into the Gemma-4 layer of model.py:705-790
+(sliding layers: 16 q heads of 256, 8 kv heads, window 1024, RoPE base 1e4;
+global layers: 16 q heads of 512, one kv head whose v is its un-normalised k,
+proportional RoPE base 1e6 on a quarter of the angles; attention scale 1).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from ._lib import check, lib
+from .ops import FfnWeights, Q4Weight, _need_gpu, _stream
+
+_GEMMA_EPS = 1e-6
+
+
+def _bf16(t: torch.Tensor, name: str, n: int) -> torch.Tensor:
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bfloat16 (got {t.dtype})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.numel() < n:
+        raise ValueError(f"{name} has {t.numel()} elements, needs {n}")
+    return t
+
+
+def _f32(t, name: str, n: int, dev) -> torch.Tensor | None:
+    if t is None:
+        return None
+    t = torch.as_tensor(t, dtype=torch.float32, device=dev).contiguous()
+    if t.numel() < n:
+        raise ValueError(f"{name} has {t.numel()} elements, needs {n}")
+    return t
+
+
+def _ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+def rmsnorm(x: torch.Tensor, w=None, *, K: int | None = None, rows: int = 1, pad: int | None = None,
+            eps: float = _GEMMA_EPS, out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16(x / sqrt(mean(x^2) + eps) * w) per row of K values, zero-padded to
+    `pad` columns (run_rmsnorm_cpu, runtime/py/model.py:522-531)."""
+    dev = _need_gpu(x)
+    K = x.numel() // rows if K is None else K
+    pad = K if pad is None else pad
+    _bf16(x, "x", rows * K)
+    w = _f32(w, "w", K, dev)
+    if out is None:
+        out = torch.empty(rows * pad, dtype=torch.bfloat16, device=dev)
+    _bf16(out, "out", rows * pad)
+    with torch.cuda.device(dev):
+        check(lib().alv_rmsnorm(x.data_ptr(), _ptr(w), out.data_ptr(), rows, K, K, pad, pad, ctypes.c_float(eps),
+                                _stream(x)), "alv_rmsnorm")
+    return out
+
+
+def qkv_post(qkv: torch.Tensor, pos_dev: torch.Tensor, kcache: torch.Tensor, vcache: torch.Tensor, *,
+             heads: int, kv_heads: int, D: int, k_off: int, v_off: int, q_w=None, k_w=None, norm_q: bool = True,
+             norm_k: bool = True, norm_v: bool = True, eps: float = _GEMMA_EPS, rope: torch.Tensor | None = None,
+             rope_stride: int | None = None, cos_off: int = 0, sin_off: int | None = None, half: int | None = None,
+             q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-head norms, RoPE of q and k at the device position `pos_dev`, K/V
+    cache insert (runtime/py/model.py:742-770). Caches are (kv_heads, max_seq, D)."""
+    dev = _need_gpu(qkv)
+    n_v = 0 if v_off < 0 else v_off + kv_heads * D
+    _bf16(qkv, "qkv", max(k_off + kv_heads * D, n_v))
+    if kcache.shape != vcache.shape or kcache.dim() != 3 or kcache.shape[0] != kv_heads or kcache.shape[2] != D:
+        raise ValueError(f"caches must be ({kv_heads}, max_seq, {D}), got {tuple(kcache.shape)} / {tuple(vcache.shape)}")
+    _bf16(kcache, "kcache", kcache.numel())
+    _bf16(vcache, "vcache", vcache.numel())
+    if pos_dev.dtype != torch.int32 or pos_dev.device != dev:
+        raise ValueError("pos_dev must be an int32 tensor on the activations' device")
+    q_w = _f32(q_w, "q_w", D, dev)
+    k_w = _f32(k_w, "k_w", D, dev)
+    if rope is not None:
+        _bf16(rope, "rope", rope.numel())
+        rope_stride = D if rope_stride is None else rope_stride
+        half = D // 2 if half is None else half
+        sin_off = half if sin_off is None else sin_off
+        if rope.numel() < kcache.shape[1] * rope_stride:
+            raise ValueError(f"rope table of {rope.numel()} values has fewer than the cache's {kcache.shape[1]} rows "
+                             f"of {rope_stride}")
+    if q_out is None:
+        q_out = torch.empty(heads * D, dtype=torch.bfloat16, device=dev)
+    _bf16(q_out, "q_out", heads * D)
+    with torch.cuda.device(dev):
+        check(lib().alv_qkv_post(qkv.data_ptr(), k_off, v_off, heads, kv_heads, D, _ptr(q_w), _ptr(k_w), int(norm_q),
+                                 int(norm_k), int(norm_v), ctypes.c_float(eps), _ptr(rope), rope_stride or 0, cos_off,
+                                 sin_off or 0, half or 0, pos_dev.data_ptr(), kcache.shape[1], q_out.data_ptr(),
+                                 kcache.data_ptr(), vcache.data_ptr(), _stream(qkv)), "alv_qkv_post")
+    return q_out
+
+
+def attention(q: torch.Tensor, kcache: torch.Tensor, vcache: torch.Tensor, pos_dev: torch.Tensor, *, heads: int,
+              window: int = 0, scale: float = 1.0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """One token's attention over the cache positions up to `pos_dev`
+    (run_attention_host, runtime/py/model.py:577-628)."""
+    dev = _need_gpu(q)
+    kv_heads, max_seq, D = kcache.shape
+    _bf16(q, "q", heads * D)
+    _bf16(kcache, "kcache", kcache.numel())
+    _bf16(vcache, "vcache", vcache.numel())
+    if out is None:
+        out = torch.empty(heads * D, dtype=torch.bfloat16, device=dev)
+    _bf16(out, "out", heads * D)
+    with torch.cuda.device(dev):
+        check(lib().alv_attention(q.data_ptr(), kcache.data_ptr(), vcache.data_ptr(), out.data_ptr(), heads, kv_heads,
+                                  D, max_seq, window, ctypes.c_float(scale), pos_dev.data_ptr(), _stream(q)),
+              "alv_attention")
+    return out
+
+
+def add_norm(resid: torch.Tensor, y: torch.Tensor, *, K: int, w_y=None, norm_y: bool = True, scale: float = 1.0,
+             scale_mode: int = 0, w_out=None, norm_out: bool = False, pad: int | None = None, rows: int = 1,
+             eps: float = _GEMMA_EPS, sum_out: torch.Tensor | None = None, norm_buf: torch.Tensor | None = None):
+    """Residual step: s = bf16(resid + (norm_y ? bf16(rmsnorm(y) * w_y) : y)),
+    scaled per scale_mode (1: Python runtime, two roundings; 2: C++ runtime, one),
+    and optionally the next norm of s zero-padded to `pad`. Returns (s, norm)."""
+    dev = _need_gpu(resid)
+    pad = K if pad is None else pad
+    _bf16(resid, "resid", rows * K)
+    _bf16(y, "y", rows * K)
+    w_y = _f32(w_y, "w_y", K, dev)
+    w_out = _f32(w_out, "w_out", K, dev)
+    if sum_out is None:
+        sum_out = torch.empty(rows * K, dtype=torch.bfloat16, device=dev)
+    _bf16(sum_out, "sum_out", rows * K)
+    if norm_out and norm_buf is None:
+        norm_buf = torch.empty(rows * pad, dtype=torch.bfloat16, device=dev)
+    if norm_out:
+        _bf16(norm_buf, "norm_out", rows * pad)
+    with torch.cuda.device(dev):
+        check(lib().alv_add_norm(resid.data_ptr(), K, y.data_ptr(), K, _ptr(w_y), int(norm_y), ctypes.c_float(scale),
+                                 scale_mode, sum_out.data_ptr(), K, _ptr(w_out), _ptr(norm_buf) if norm_out else 0,
+                                 pad, rows, K, pad, ctypes.c_float(eps), _stream(resid)), "alv_add_norm")
+    return sum_out, (norm_buf if norm_out else None)
+
+
+def gemv_bf16(W: Q4Weight, X: torch.Tensor, Y: torch.Tensor | None = None, M: int = 1) -> torch.Tensor:
+    """Y = bf16(X W^T), bf16 in and out (the reference's run_gemv contract)."""
+    _bf16(X, "X", M * W.K)
+    if Y is None:
+        Y = torch.empty(M * W.N, dtype=torch.bfloat16, device=W.device)
+    _bf16(Y, "Y", M * W.N)
+    with torch.cuda.device(W.device):
+        check(lib().alv_gemv_bf16(W.handle, X.data_ptr(), Y.data_ptr(), M, W.K, W.N, _stream(X)), "alv_gemv_bf16")
+    return Y
+
+
+def ffn_fused_bf16(F: FfnWeights, X: torch.Tensor, Y: torch.Tensor | None = None, M: int = 1) -> torch.Tensor:
+    """Y = bf16(down(GLU(gate X, up X))), bf16 in and out (run_ffn_fused)."""
+    _bf16(X, "X", M * F.H)
+    if Y is None:
+        Y = torch.empty(M * F.H, dtype=torch.bfloat16, device=F.device)
+    _bf16(Y, "Y", M * F.H)
+    with torch.cuda.device(F.device):
+        check(lib().alv_ffn_fused_bf16(F.handle, X.data_ptr(), Y.data_ptr(), M, F.H, F.H, _stream(X)),
+              "alv_ffn_fused_bf16")
+    return Y
+
+
+def cos_sin_table_gemma(base: float, dim: int, max_seq_len: int, gemma4: bool = True) -> np.ndarray:
+    """The reference's RoPE table (precompute_cos_sin_table_gemma,
+    runtime/py/model.py:263-280): float32 rows [cos(pos f) | sin(pos f)] in
+    numpy, then bf16 (round to nearest even; returned as uint16 bit patterns).
+    Gemma-4's 512-wide heads rotate a quarter of the angles."""
+    if gemma4 and dim == 512:
+        angles = int(0.25 * dim // 2)
+        inv_freq = np.zeros(dim // 2, dtype=np.float32)
+        inv_freq[:angles] = 1.0 / (base ** (np.arange(0, 2 * angles, 2, dtype=np.float32) / dim))
+    else:
+        inv_freq = 1.0 / (base ** (np.arange(0, dim, 2, dtype=np.float32) / dim))
+    table = np.zeros((max_seq_len, dim), dtype=np.float32)
+    for pos in range(max_seq_len):
+        freqs = pos * inv_freq
+        table[pos] = np.concatenate([np.cos(freqs), np.sin(freqs)])
+    u = table.view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+class Gemma4DecodeLayer:
+    """One Gemma-4 decoder layer with every step on the device
+    (runtime/py/model.py:705-790 with the NPU matmuls). Weights are combined
+    Q4 arrays: ``qkv`` the rows [q | k | v] (sliding) or [q | k] (global) of
+    H columns, ``o`` (H, q_size) and the FFN; norms float32. ``forward(x, pos)``
+    takes and returns bf16 [H] device tensors and updates the KV caches."""
+
+    def __init__(self, *, qkv, o, gate, up, down, norms: dict, scale: float, sliding: bool, H: int, I: int,
+                 max_seq: int, device, rope_table=None):
+        dev = torch.device(device)
+        self.sliding, self.H, self.I, self.max_seq, self.device = sliding, H, I, max_seq, dev
+        self.heads = 16
+        self.kv_heads = 8 if sliding else 1
+        self.D = 256 if sliding else 512
+        self.q_size = self.heads * self.D
+        self.k_size = self.kv_heads * self.D
+        self.n_qkv = self.q_size + (2 if sliding else 1) * self.k_size
+        self.window = 1024 if sliding else 0
+        self.scale = float(np.float32(scale))
+
+        def dev_u8(a):
+            return torch.as_tensor(np.ascontiguousarray(a)).to(dev) if isinstance(a, np.ndarray) else a
+
+        self.w_qkv = Q4Weight(dev_u8(qkv), self.n_qkv, H)
+        self.w_o = Q4Weight(dev_u8(o), H, self.q_size)
+        self.ffn = FfnWeights(dev_u8(gate), dev_u8(up), dev_u8(down), H, I, "gelu")
+        self.norms = {k: _f32(v, k, self.D if k in ("q", "k") else H, dev) for k, v in norms.items()}
+        if rope_table is None:
+            rope_table = cos_sin_table_gemma(10000.0 if sliding else 1000000.0, self.D, max_seq)
+        self.rope = torch.as_tensor(np.ascontiguousarray(rope_table)).view(torch.bfloat16).to(dev)
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        self.kcache = torch.zeros((self.kv_heads, max_seq, self.D), **bf)
+        self.vcache = torch.zeros((self.kv_heads, max_seq, self.D), **bf)
+        self.pos_dev = torch.zeros(1, dtype=torch.int32, device=dev)
+        # Intermediates (kept for inspection and for graph capture: fixed addresses).
+        self.x_norm = torch.empty(H, **bf)
+        self.qkv_out = torch.empty(self.n_qkv, **bf)
+        self.q_rope = torch.empty(self.q_size, **bf)
+        self.attn_out = torch.empty(self.q_size, **bf)
+        self.attn_proj = torch.empty(H, **bf)
+        self.x_post = torch.empty(H, **bf)
+        self.x_norm2 = torch.empty(H, **bf)
+        self.down = torch.empty(H, **bf)
+        self.y = torch.empty(H, **bf)
+
+    def enqueue(self, x: torch.Tensor) -> torch.Tensor:
+        """The layer's launches for the position already in ``pos_dev``."""
+        H, n = self.H, self.norms
+        rmsnorm(x, n["attn"], K=H, out=self.x_norm)
+        gemv_bf16(self.w_qkv, self.x_norm, self.qkv_out)
+        qkv_post(self.qkv_out, self.pos_dev, self.kcache, self.vcache, heads=self.heads, kv_heads=self.kv_heads,
+                 D=self.D, k_off=self.q_size, v_off=self.q_size + self.k_size if self.sliding else -1,
+                 q_w=n["q"], k_w=n["k"], norm_v=True, rope=self.rope, q_out=self.q_rope)
+        attention(self.q_rope, self.kcache, self.vcache, self.pos_dev, heads=self.heads, window=self.window,
+                  out=self.attn_out)
+        gemv_bf16(self.w_o, self.attn_out, self.attn_proj)
+        add_norm(x, self.attn_proj, K=H, w_y=n["post_attn"], w_out=n["ffn"], norm_out=True, sum_out=self.x_post,
+                 norm_buf=self.x_norm2)
+        ffn_fused_bf16(self.ffn, self.x_norm2, self.down)
+        add_norm(self.x_post, self.down, K=H, w_y=n["post_ffw"], scale=self.scale, scale_mode=1, sum_out=self.y)
+        return self.y
+
+    def forward(self, x: torch.Tensor, pos: int) -> torch.Tensor:
+        if not 0 <= pos < self.max_seq:
+            raise ValueError(f"position {pos} outside the cache of {self.max_seq}")
+        self.pos_dev.fill_(pos)
+        return self.enqueue(x)
+
+    def close(self) -> None:
+        self.w_qkv.close()
+        self.w_o.close()
+        self.ffn.close()

@@ -107,6 +107,14 @@ int alv_weight_shape(alv_weight_t w, int* N, int* K);
  */
 int alv_gemv(alv_weight_t w, const float* X, float* Y, int M, int ldx, int ldy, void* stream);
 
+/*
+ * alv_gemv with bf16 activations and outputs (bit patterns): Y = bf16(X W^T),
+ * the reference's run_gemv(N, K, w, x_bf16, y_bf16) contract
+ * (runtime/cpp/include/alveare/npu.h:78-87; runtime/py/model.py:283-362
+ * run_gemv_npu returns bf16). X rows 16-byte aligned (ldx a multiple of 8).
+ */
+int alv_gemv_bf16(alv_weight_t w, const uint16_t* X, uint16_t* Y, int M, int ldx, int ldy, void* stream);
+
 /* Free a handle from alv_weight_register (NULL is a no-op). Synchronises the
  * device before freeing. */
 void alv_weight_release(alv_weight_t w);
@@ -185,6 +193,15 @@ int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int ldx, int ldy
                   void* stream);
 
 /*
+ * alv_ffn_fused with bf16 activations and outputs (bit patterns): the
+ * reference's run_ffn_fused(H, I, act, w, x_bf16, y_bf16)
+ * (runtime/cpp/include/alveare/npu.h:90-97, runtime/cpp/src/npu.cpp:340-378:
+ * partials summed in float32, then bf16). Same rounding points as
+ * alv_ffn_fused; Y = bf16(down). X rows 16-byte aligned (ldx a multiple of 8).
+ */
+int alv_ffn_fused_bf16(alv_ffn_t w, const uint16_t* X, uint16_t* Y, int M, int ldx, int ldy, void* stream);
+
+/*
  * alv_ffn_fused for M <= 16 tokens (decode and small-M verification) that
  * allocates nothing: the split-K partial sums and arrival counters of its two
  * launches live in a fixed 16 MiB + 4 KiB array in device memory, one per GPU
@@ -224,6 +241,64 @@ int alv_ffn_shape(alv_ffn_t w, int* H, int* I, int* act);
 /* Free a handle from alv_ffn_register (NULL is a no-op). Synchronises the
  * device before freeing. */
 void alv_ffn_release(alv_ffn_t w);
+
+/*
+ * ---- host ops of a decode layer (bf16 tensors as uint16 bit patterns) ----------
+ * The work the reference does on the CPU between its matmuls
+ * (runtime/py/model.py:522-628, :705-790; runtime/cpp/src/model.cpp:127-262,
+ * :314-420). Elementwise steps and RMSNorm are bit-exact with the reference's
+ * numpy float32 arithmetic (numpy >= 2; RMSNorm's mean uses numpy's pairwise
+ * summation order); attention is float32 with its own summation order.
+ * `pos_dev` is a device int holding the decode position, so captured graphs
+ * replay for every token. All asynchronous on `stream`.
+ */
+
+/*
+ * out[r, :K] = bf16(x * (1 / sqrt(mean(x^2) + eps)) * w) for rows r < rows
+ * (w NULL: no weight), out[r, K:pad] = 0 (the reference pads 3840 -> 4096,
+ * runtime/cpp/src/model.cpp:334-336). run_rmsnorm_cpu (runtime/py/model.py:522-531;
+ * model.cpp:127-141). K <= 20480.
+ */
+int alv_rmsnorm(const uint16_t* x, const float* w, uint16_t* out, int rows, int K, int ldx, int ldo, int pad,
+                float eps, void* stream);
+
+/*
+ * After the QKV projection: per-head RMSNorm of q (weights q_w), k (k_w) and,
+ * when norm_v, of v without weights (Gemma-4); RoPE of q and k with the bf16
+ * table row `rope + pos * rope_stride` (cos at cos_off, sin at sin_off, pairs
+ * (i, i + half)); q to q_out [heads][D]; k and v into the caches at pos
+ * ([kv_heads][max_seq][D]). qkv holds q at 0, k at k_off and v at v_off
+ * (v_off < 0: v is the un-normalised k, Gemma-4 global layers). rope NULL: no
+ * rotation; otherwise the table holds max_seq rows of rope_stride values.
+ * model.py:742-770; model.cpp:357-404.
+ */
+int alv_qkv_post(const uint16_t* qkv, int k_off, int v_off, int heads, int kv_heads, int D, const float* q_w,
+                 const float* k_w, int norm_q, int norm_k, int norm_v, float eps, const uint16_t* rope,
+                 int rope_stride, int cos_off, int sin_off, int half, const int* pos_dev, int max_seq,
+                 uint16_t* q_out, uint16_t* kcache, uint16_t* vcache, void* stream);
+
+/*
+ * out[h] = softmax(scale * K q[h]) V over cache positions [start, pos] of kv
+ * head h / (heads / kv_heads), start = pos + 1 - window for a sliding layer
+ * (window > 0), else 0; float32 scores and softmax, bf16 out [heads][D].
+ * run_attention_host (runtime/py/model.py:577-628; model.cpp:185-262). D a
+ * multiple of 32 up to 512, at most 16 q heads per kv head; kcache 16-byte
+ * aligned. Uses per-stream scratch (grown outside graph capture).
+ */
+int alv_attention(const uint16_t* q, const uint16_t* kcache, const uint16_t* vcache, uint16_t* out, int heads,
+                  int kv_heads, int D, int max_seq, int window, float scale, const int* pos_dev, void* stream);
+
+/*
+ * Residual step of a layer, per row: t = norm_y ? bf16(rmsnorm(y) * w_y) : y;
+ * s = bf16(resid + t), then scale_mode 1: s = bf16(s * scale) (the Python
+ * runtime's two roundings, model.py:783-788), 2: s = bf16((resid + t) * scale)
+ * (the C++ runtime's one rounding, model.cpp:410-416), 0: no scale; sum_out = s;
+ * norm_out (optional) = bf16(rmsnorm(s) * w_out) zero-padded to pad.
+ * model.py:775-788; model.cpp:409-420.
+ */
+int alv_add_norm(const uint16_t* resid, int ldr, const uint16_t* y, int ldy, const float* w_y, int norm_y,
+                 float scale, int scale_mode, uint16_t* sum_out, int ld_sum, const float* w_out, uint16_t* norm_out,
+                 int ld_norm, int rows, int K, int pad, float eps, void* stream);
 
 /*
  * One op of a chain: a registered projection (y = W x) or a registered FFN

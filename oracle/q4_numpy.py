@@ -15,6 +15,16 @@ numpy expressions, so numpy decides dtype promotion and the matmul order:
 * ``lm_head_cpu``           -- ``runtime/py/model.py:904-916`` (bf16 logits,
                               vocabulary slice, float32 softcap) and
                               ``runtime/py/sampler.py:9`` (greedy np.argmax)
+* ``rmsnorm_cpu``           -- ``runtime/py/model.py:522-531``
+* ``rope_cpu_gemma``        -- ``runtime/py/model.py:549-575``
+* ``cos_sin_table_gemma``   -- ``runtime/py/model.py:263-280``
+* ``attention_host``        -- ``runtime/py/model.py:577-628``
+* ``gemma4_decode_layer``   -- ``runtime/py/model.py:705-790`` (the NPU path:
+                              the projections and the FFN are callables)
+
+bf16 arrays of the reference are float32 arrays of bf16-exact values here, so
+``x.astype(np.float32)`` of a bf16 array is the identity and
+``.astype(bfloat16)`` is ``bf16_rne``.
 """
 from __future__ import annotations
 
@@ -108,3 +118,121 @@ def quantize_to_q4_0(W: np.ndarray) -> np.ndarray:
     out[:, :, 16] = sb & 0xFF
     out[:, :, 17] = sb >> 8
     return out.reshape(N, K // 32 * 20)
+
+
+# ---- host ops of a decode layer (runtime/py/model.py) ------------------------------
+
+def rmsnorm_cpu(x: np.ndarray, w, eps: float = 1e-6) -> np.ndarray:
+    """run_rmsnorm_cpu (model.py:522-531): Gemma eps 1e-6 (weights optional),
+    Llama eps 1e-5. numpy >= 2 evaluates the scalar arithmetic in float32."""
+    x32 = np.asarray(x, np.float32)
+    variance = np.mean(x32 ** 2)
+    normed = x32 * (1.0 / np.sqrt(variance + eps))
+    if w is not None:
+        normed = normed * np.asarray(w, np.float32)
+    return bf16_rne(normed)
+
+
+def cos_sin_table_gemma(base: float, dim: int, max_seq_len: int, gemma4: bool = True) -> np.ndarray:
+    """precompute_cos_sin_table_gemma (model.py:263-280): (max_seq_len, dim)
+    bf16 rows [cos | sin]; Gemma-4's 512-wide global heads rotate only the
+    first quarter of the angles (the rest have inv_freq 0: cos 1, sin 0)."""
+    if gemma4 and dim == 512:
+        rope_angles = int(0.25 * dim // 2)
+        inv_freq_rotated = 1.0 / (base ** (np.arange(0, 2 * rope_angles, 2, dtype=np.float32) / dim))
+        inv_freq = np.zeros(dim // 2, dtype=np.float32)
+        inv_freq[:rope_angles] = inv_freq_rotated
+    else:
+        inv_freq = 1.0 / (base ** (np.arange(0, dim, 2, dtype=np.float32) / dim))
+    table = np.zeros((max_seq_len, dim), dtype=np.float32)
+    for pos in range(max_seq_len):
+        freqs = pos * inv_freq
+        table[pos] = np.concatenate([np.cos(freqs), np.sin(freqs)])
+    return bf16_rne(table)
+
+
+def rope_cpu_gemma(x: np.ndarray, cos_sin_row: np.ndarray, dim: int) -> np.ndarray:
+    """run_rope_cpu_gemma (model.py:549-575) on one table row: rotate-half
+    pairs (i, i + dim/2) of every dim-wide head, float32, then bf16."""
+    x_flat = np.asarray(x, np.float32).reshape(-1)
+    num_heads = x_flat.shape[0] // dim
+    cos = np.asarray(cos_sin_row[:dim // 2], np.float32)
+    sin = np.asarray(cos_sin_row[dim // 2:dim], np.float32)
+    x_fp32 = x_flat.reshape(num_heads, dim)
+    y_fp32 = np.zeros_like(x_fp32)
+    for h in range(num_heads):
+        x1 = x_fp32[h, :dim // 2]
+        x2 = x_fp32[h, dim // 2:]
+        y_fp32[h, :dim // 2] = x1 * cos - x2 * sin
+        y_fp32[h, dim // 2:] = x2 * cos + x1 * sin
+    return bf16_rne(y_fp32.reshape(-1))
+
+
+def attention_host(q_rope: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, pos: int, num_heads: int,
+                   num_kv_heads: int, dim: int, scale: float, window: int = 0) -> np.ndarray:
+    """run_attention_host (model.py:577-628) for one token at `pos`: caches are
+    (kv_heads, max_seq, dim); window > 0 is a sliding layer's window. float32
+    scores, softmax and weighted sum; bf16 out."""
+    q = np.asarray(q_rope, np.float32).reshape(num_heads, dim)
+    seq_len = pos + 1
+    if window > 0:
+        W = min(seq_len, window)
+        k = np.asarray(k_cache[:, pos + 1 - W:pos + 1, :], np.float32)
+        v = np.asarray(v_cache[:, pos + 1 - W:pos + 1, :], np.float32)
+    else:
+        k = np.asarray(k_cache[:, :seq_len, :], np.float32)
+        v = np.asarray(v_cache[:, :seq_len, :], np.float32)
+        W = seq_len
+    group_ratio = num_heads // num_kv_heads
+    if group_ratio > 1:
+        k = np.repeat(k, group_ratio, axis=0)
+        v = np.repeat(v, group_ratio, axis=0)
+    scores = np.zeros((num_heads, W), dtype=np.float32)
+    for h in range(num_heads):
+        scores[h] = np.dot(k[h], q[h]) * scale
+    max_scores = np.max(scores, axis=-1, keepdims=True)
+    exp_scores = np.exp(scores - max_scores)
+    probs = exp_scores / np.sum(exp_scores, axis=-1, keepdims=True)
+    output = np.zeros((num_heads, dim), dtype=np.float32)
+    for h in range(num_heads):
+        output[h] = np.dot(probs[h], v[h])
+    return bf16_rne(output.reshape(-1))
+
+
+def gemma4_decode_layer(x: np.ndarray, pos: int, sliding: bool, w: dict, qkv_proj, o_proj, ffn,
+                        k_cache: np.ndarray, v_cache: np.ndarray, cos_sin_row: np.ndarray, stages: dict | None = None):
+    """run_layer for gemma4 (model.py:705-790), NPU path. qkv_proj(x_norm)
+    returns the bf16 [q | k | v] rows (v absent on global layers, where v is
+    the raw k), o_proj(attn_out) and ffn(x_norm2) the bf16 outputs (first 3840
+    used). w holds the float32 norm weights (attn, q, k, post_attn, ffn,
+    post_ffw) and the layer output scale. The caches are updated at `pos`.
+    `stages` (optional) receives every intermediate."""
+    H = x.shape[0]
+    q_size = 4096 if sliding else 8192
+    k_size = 2048 if sliding else 512
+    h_dim = 256 if sliding else 512
+    n_heads, n_kv = 16, (8 if sliding else 1)
+    st = {} if stages is None else stages
+    st["x_norm"] = x_norm = rmsnorm_cpu(x, w["attn"])
+    qkv = qkv_proj(x_norm)
+    q = qkv[:q_size]
+    k = qkv[q_size:q_size + k_size]
+    v = qkv[q_size + k_size:q_size + 2 * k_size] if sliding else k
+    q_n = np.concatenate([rmsnorm_cpu(q[h * h_dim:(h + 1) * h_dim], w["q"]) for h in range(n_heads)])
+    k_n = np.concatenate([rmsnorm_cpu(k[h * h_dim:(h + 1) * h_dim], w["k"]) for h in range(n_kv)])
+    v_n = np.concatenate([rmsnorm_cpu(v[h * h_dim:(h + 1) * h_dim], None) for h in range(n_kv)])
+    st["q_rope"] = q_rope = rope_cpu_gemma(q_n, cos_sin_row, h_dim)
+    k_rope = rope_cpu_gemma(k_n, cos_sin_row, h_dim)
+    k_cache[:, pos, :] = k_rope.reshape(n_kv, h_dim)
+    v_cache[:, pos, :] = v_n.reshape(n_kv, h_dim)
+    st["attn_out"] = attn_out = attention_host(q_rope, k_cache, v_cache, pos, n_heads, n_kv, h_dim, 1.0,
+                                               1024 if sliding else 0)
+    st["attn_proj"] = attn_proj = o_proj(attn_out)[:H]
+    normed = rmsnorm_cpu(attn_proj, w["post_attn"])
+    st["x_post"] = x_post = bf16_rne(x + normed)
+    st["x_norm2"] = x_norm2 = rmsnorm_cpu(x_post, w["ffn"])
+    st["down"] = down = ffn(x_norm2)[:H]
+    down_normed = rmsnorm_cpu(down, w["post_ffw"])
+    y = bf16_rne(x_post + down_normed)
+    st["y"] = y = bf16_rne(y * np.float32(w["scale"]))
+    return y

@@ -171,3 +171,103 @@ def quant_cases():
     w[9, :32] = -0.0
     w[10, :32] = np.float32(1e-45) * np.array([0, 1, 2, 3] * 8, np.float32)  # max / 7 underflows to 0
     return w
+
+
+# ---- host ops of a decode layer ---------------------------------------------------
+
+def pw_sum_gpu_order(a: np.ndarray) -> np.float32:
+    """The GPU's float32 sum of a (layer_ops.hip pw_sum_wave): per buffer of
+    8192 values (buffer sums added in order), leaves of a halving tree summed
+    by the 8-accumulator rule and combined pairwise up the tree, or the full
+    recursion on one lane for other widths. Meant to equal np.add.reduce(a)
+    bit for bit."""
+    a = np.asarray(a, np.float32)
+    if len(a) > 8192:
+        r = _pw_chunk(a[:8192])
+        for off in range(8192, len(a), 8192):
+            r = np.float32(r + _pw_chunk(a[off:off + 8192]))
+        return r
+    return _pw_chunk(a)
+
+
+def _pw_chunk(a: np.ndarray) -> np.float32:
+    n = len(a)
+
+    def leaf(x):
+        if len(x) < 8:
+            r = np.float32(0)
+            for v in x:
+                r = np.float32(r + v)
+            return r
+        r = [np.float32(v) for v in x[:8]]
+        i = 8
+        while i < len(x) - len(x) % 8:
+            for j in range(8):
+                r[j] = np.float32(r[j] + x[i + j])
+            i += 8
+        res = np.float32(np.float32(np.float32(r[0] + r[1]) + np.float32(r[2] + r[3])) +
+                         np.float32(np.float32(r[4] + r[5]) + np.float32(r[6] + r[7])))
+        for v in x[i:]:
+            res = np.float32(res + v)
+        return res
+
+    def rec(x):
+        if len(x) <= 128:
+            return leaf(x)
+        n2 = len(x) // 2
+        n2 -= n2 % 8
+        return np.float32(rec(x[:n2]) + rec(x[n2:]))
+
+    lf, leaves = n, 1
+    halving = True
+    while lf > 128:
+        if lf % 2 or (lf // 2) % 8:
+            halving = False
+            break
+        lf //= 2
+        leaves *= 2
+    if not (halving and leaves <= 64):
+        return rec(a)
+    v = [leaf(a[i * lf:(i + 1) * lf]) for i in range(leaves)]
+    s = 1
+    while s < leaves:
+        v = [np.float32(v[i] + v[i + 1]) for i in range(0, len(v), 2)]
+        s *= 2
+    return v[0]
+
+
+def bf16_bits(t) -> np.ndarray:
+    """uint16 bit patterns of a torch bfloat16 tensor (on any device)."""
+    return t.detach().cpu().view(__import__("torch").int16).numpy().view(np.uint16)
+
+
+def bits_bf16_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_bits_bf16(x: np.ndarray) -> np.ndarray:
+    from oracle import q4_numpy
+    return (q4_numpy.bf16_rne(x).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def bf16_interval_check(out_bits: np.ndarray, ref64: np.ndarray, bound: np.ndarray, what: str) -> int:
+    """Every bf16 output lies between the bf16 roundings of ref64 - bound and
+    ref64 + bound (a float32 value within `bound` of the exact one, rounded to
+    bf16); returns how many differ from the rounding of ref64 itself."""
+    from oracle import q4_numpy
+    out = bits_bf16_f32(out_bits).astype(np.float64)
+    lo = q4_numpy.bf16_rne(np.nextafter((ref64 - bound).astype(np.float32), np.float32(-np.inf))).astype(np.float64)
+    hi = q4_numpy.bf16_rne(np.nextafter((ref64 + bound).astype(np.float32), np.float32(np.inf))).astype(np.float64)
+    bad = (out < lo) | (out > hi)
+    assert not bad.any(), f"{what}: {bad.sum()} bf16 outputs outside the bound, first at {np.argmax(bad)}"
+    mid = q4_numpy.bf16_rne(ref64.astype(np.float32)).astype(np.float64)
+    return int((out != mid).sum())
+
+
+def gemv_bf16_check(orc, W, x, y_bits, N, K) -> int:
+    """bf16 GEMV output against the fp64 value with the fp32 bound (rows can
+    round either way only when the bound straddles a bf16 rounding point)."""
+    y64 = orc.gemv_q_f64(W, x, N, K)
+    absdot = np.abs(deq_f64(orc, W, N, K)) @ np.abs(np.asarray(x, np.float64))
+    gamma = K * U32 / (1 - K * U32)
+    return bf16_interval_check(y_bits, y64, 2 * gamma * absdot + 1e-30, "bf16 GEMV")

@@ -1,0 +1,281 @@
+"""GPU parity of the device-resident decode layer (host ops on the GPU).
+
+Bars: RMSNorm, the q/k/v post-processing (norms, RoPE, cache insert) and the
+residual steps bit-exact against the reference's numpy expressions
+(oracle/q4_numpy.py); attention within the float32 bound of an fp64
+evaluation (the reference's own np.dot order is its BLAS's); bf16 GEMV / FFN
+outputs between the bf16 roundings of the fp64 value +- its float32 bound; the
+whole layer checked stage by stage, each stage's oracle fed the GPU's own
+inputs to that stage, so every stage meets its own bar.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import parity
+from oracle import q4_numpy as qn
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def bf_dev(a, dev):
+    """float32 array of bf16-exact values -> torch bfloat16 on dev."""
+    bits = parity.f32_bits_bf16(np.asarray(a, np.float32)).view(np.int16)
+    return torch.from_numpy(np.ascontiguousarray(bits)).view(torch.bfloat16).to(dev)
+
+
+def bf_np(t):
+    return parity.bits_bf16_f32(parity.bf16_bits(t))
+
+
+def rnd_bf16(rng, shape, sd=1.0):
+    return qn.bf16_rne(rng.normal(0, sd, shape).astype(np.float32))
+
+
+# ---- RMSNorm (runtime/py/model.py:522-531) ----------------------------------------
+
+@pytest.mark.parametrize("rows,K,weighted", [(1, 3840, True), (16, 256, True), (1, 512, True), (3, 1152, True),
+                                              (2, 1000, True), (1, 20480, True), (4, 100, False), (8, 256, False)])
+def test_rmsnorm_bit_exact(dev, rows, K, weighted):
+    from alveare_amd import layer
+
+    _say(f"rmsnorm rows={rows} K={K} weighted={weighted}")
+    rng = np.random.default_rng(K + rows)
+    x = rnd_bf16(rng, (rows, K), rng.uniform(0.05, 20))
+    w = rng.uniform(0.3, 2.0, K).astype(np.float32) if weighted else None
+    pad = K + 64
+    out = layer.rmsnorm(bf_dev(x, dev), w, K=K, rows=rows, pad=pad)
+    got = bf_np(out).reshape(rows, pad)
+    for r in range(rows):
+        assert np.array_equal(got[r, :K], qn.rmsnorm_cpu(x[r], w)), f"row {r}"
+    assert not got[:, K:].any()
+
+
+# ---- q/k/v post-processing (model.py:742-770) ---------------------------------------
+
+@pytest.mark.parametrize("sliding,pos", [(True, 0), (True, 7), (True, 1500), (False, 0), (False, 2047)])
+def test_qkv_post_bit_exact(dev, sliding, pos):
+    from alveare_amd import layer
+
+    _say(f"qkv_post sliding={sliding} pos={pos}")
+    rng = np.random.default_rng(pos + (1 if sliding else 2))
+    D, kv = (256, 8) if sliding else (512, 1)
+    q_size, k_size, S = 16 * D, kv * D, 2048
+    qkv = rnd_bf16(rng, q_size + (2 if sliding else 1) * k_size, 2.0)
+    qw, kw = rng.uniform(0.5, 1.5, D).astype(np.float32), rng.uniform(0.5, 1.5, D).astype(np.float32)
+    table = qn.cos_sin_table_gemma(10000.0 if sliding else 1e6, D, S)
+    assert np.array_equal(layer.cos_sin_table_gemma(10000.0 if sliding else 1e6, D, S), parity.f32_bits_bf16(table))
+    kc = torch.zeros((kv, S, D), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    pos_dev = torch.tensor([pos], dtype=torch.int32, device=dev)
+    q_out = layer.qkv_post(bf_dev(qkv, dev), pos_dev, kc, vc, heads=16, kv_heads=kv, D=D, k_off=q_size,
+                           v_off=q_size + k_size if sliding else -1, q_w=qw, k_w=kw, norm_v=True,
+                           rope=bf_dev(table, dev))
+    q = qkv[:q_size]
+    k = qkv[q_size:q_size + k_size]
+    v = qkv[q_size + k_size:] if sliding else k
+    q_n = np.concatenate([qn.rmsnorm_cpu(q[h * D:(h + 1) * D], qw) for h in range(16)])
+    k_n = np.concatenate([qn.rmsnorm_cpu(k[h * D:(h + 1) * D], kw) for h in range(kv)])
+    v_n = np.concatenate([qn.rmsnorm_cpu(v[h * D:(h + 1) * D], None) for h in range(kv)])
+    assert np.array_equal(bf_np(q_out), qn.rope_cpu_gemma(q_n, table[pos], D))
+    kcn, vcn = bf_np(kc).reshape(kv, S, D), bf_np(vc).reshape(kv, S, D)
+    assert np.array_equal(kcn[:, pos].reshape(-1), qn.rope_cpu_gemma(k_n, table[pos], D))
+    assert np.array_equal(vcn[:, pos].reshape(-1), v_n)
+    kcn[:, pos] = 0
+    vcn[:, pos] = 0
+    assert not kcn.any() and not vcn.any()
+
+
+# ---- attention (model.py:577-628) ---------------------------------------------------
+
+def _attn_check(q, kc, vc, pos, heads, kv, D, window, got_bits):
+    """fp64 softmax(K q) V with the float32 bound; returns the bf16 mismatch
+    count against numpy's own float32 evaluation."""
+    g = heads // kv
+    seq = pos + 1
+    st = max(0, seq - window) if window else 0
+    ref = np.empty(heads * D)
+    bound = np.empty(heads * D)
+    for h in range(heads):
+        k64 = kc[h // g, st:seq].astype(np.float64)
+        v64 = vc[h // g, st:seq].astype(np.float64)
+        qh = q[h * D:(h + 1) * D].astype(np.float64)
+        s = k64 @ qh
+        ds = (D + 2) * 2.0 ** -24 * (np.abs(k64) @ np.abs(qh))  # float32 score error
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        ref[h * D:(h + 1) * D] = p @ v64
+        # score errors move the weights by exp(+-2 ds); plus float32 sums over W and D
+        bound[h * D:(h + 1) * D] = (np.expm1(2 * ds.max()) + (seq - st + 16) * 2.0 ** -23) * (p @ np.abs(v64)) + 1e-30
+    parity.bf16_interval_check(got_bits, ref, bound, "attention")
+    npy = qn.attention_host(q, kc, vc, pos, heads, kv, D, 1.0, window)
+    return int((parity.bits_bf16_f32(got_bits) != npy).sum())
+
+
+@pytest.mark.parametrize("sliding,pos", [(True, 0), (True, 100), (True, 1023), (True, 1500), (True, 2047),
+                                          (False, 0), (False, 700), (False, 2047)])
+def test_attention_bound(dev, sliding, pos):
+    from alveare_amd import layer
+
+    _say(f"attention sliding={sliding} pos={pos}")
+    rng = np.random.default_rng(10 * pos + sliding)
+    D, kv, S = (256, 8, 2048) if sliding else (512, 1, 2048)
+    kc = rnd_bf16(rng, (kv, S, D), 1.0)
+    vc = rnd_bf16(rng, (kv, S, D), 1.0)
+    q = rnd_bf16(rng, 16 * D, 0.15)  # scores of a few units: a peaked, not one-hot, softmax
+    pos_dev = torch.tensor([pos], dtype=torch.int32, device=dev)
+    out = layer.attention(bf_dev(q, dev), bf_dev(kc, dev), bf_dev(vc, dev), pos_dev, heads=16,
+                          window=1024 if sliding else 0)
+    mism = _attn_check(q, kc, vc, pos, 16, kv, D, 1024 if sliding else 0, parity.bf16_bits(out))
+    _say(f"  bf16 outputs differing from numpy's float32 evaluation: {mism} of {16 * D}")
+    assert mism <= 16 * D // 50
+
+
+# ---- residual steps (model.py:775-788; model.cpp:409-420) ---------------------------
+
+@pytest.mark.parametrize("mode,norm_y,norm_out", [(0, True, True), (1, True, False), (2, True, False),
+                                                   (0, False, True)])
+def test_add_norm_bit_exact(dev, mode, norm_y, norm_out):
+    from alveare_amd import layer
+
+    _say(f"add_norm mode={mode} norm_y={norm_y} norm_out={norm_out}")
+    rng = np.random.default_rng(mode * 4 + norm_y * 2 + norm_out)
+    K, rows = 3840, 2
+    r = rnd_bf16(rng, (rows, K), 4.0)
+    y = rnd_bf16(rng, (rows, K), 0.7)
+    wy = rng.uniform(0.3, 2.0, K).astype(np.float32)
+    wo = rng.uniform(0.3, 2.0, K).astype(np.float32)
+    scale = np.float32(0.8125 if mode else 1.0) * np.float32(1.0001)
+    s_out, n_out = layer.add_norm(bf_dev(r, dev), bf_dev(y, dev), K=K, rows=rows, w_y=wy, norm_y=norm_y,
+                                  scale=float(scale), scale_mode=mode, w_out=wo, norm_out=norm_out, pad=4096)
+    got_s = bf_np(s_out).reshape(rows, K)
+    for i in range(rows):
+        t = qn.rmsnorm_cpu(y[i], wy) if norm_y else y[i]
+        s = qn.bf16_rne(r[i] + t)
+        if mode == 1:
+            s = qn.bf16_rne(s * scale)
+        elif mode == 2:
+            s = qn.bf16_rne((r[i] + t) * scale)
+        assert np.array_equal(got_s[i], s), f"row {i}"
+        if norm_out:
+            got_n = bf_np(n_out).reshape(rows, 4096)
+            assert np.array_equal(got_n[i, :K], qn.rmsnorm_cpu(s, wo))
+            assert not got_n[i, K:].any()
+
+
+# ---- bf16 GEMV and FFN (the reference's run_gemv / run_ffn_fused contract) ----------
+
+@pytest.mark.parametrize("M,N,K", [(1, 8192, 3840), (1, 3840, 4096), (4, 2048, 2048), (16, 1024, 3840),
+                                   (64, 1024, 3840)])
+def test_gemv_bf16(orc, dev, M, N, K):
+    import alveare_amd as aa
+    from alveare_amd import layer
+
+    _say(f"gemv_bf16 M={M} N={N} K={K}")
+    W = orc.synth_q4(N, K, 100 + M)
+    X = qn.bf16_rne(orc.synth_normal(M * K, 101 + M)).reshape(M, K)
+    w = aa.Q4Weight(torch.from_numpy(W).to(dev), N, K)
+    Y = layer.gemv_bf16(w, bf_dev(X, dev), M=M)
+    torch.cuda.synchronize()
+    yb = parity.bf16_bits(Y).reshape(M, N)
+    flips = sum(parity.gemv_bf16_check(orc, W, X[m], yb[m], N, K) for m in range(M))
+    _say(f"  rows rounding away from the fp64 value's bf16: {flips} of {M * N}")
+    w.close()
+
+
+@pytest.mark.parametrize("H,I,M", [(1152, 6912, 1), (3840, 15360, 1), (1152, 6912, 4), (1024, 2048, 64)])
+def test_ffn_fused_bf16(orc, dev, H, I, M):
+    """bf16 ends on the same device FFN: gate/up reads the bf16 activation as
+    its one term and gives the activation alv_ffn_fused gives for the same
+    (bf16-valued) input, bit for bit; the bf16 output is the rounding of
+    alv_ffn_fused's float32 output (which meets the FFN bar against the oracle)."""
+    import alveare_amd as aa
+    from alveare_amd import layer
+
+    _say(f"ffn_fused_bf16 H={H} I={I} M={M}")
+    Wg, Wu, Wd = orc.synth_q4(I, H, 200), orc.synth_q4(I, H, 201), orc.synth_q4(H, I, 202)
+    X = qn.bf16_rne(orc.synth_normal(M * H, 203)).reshape(M, H)
+    F = aa.FfnWeights(*(torch.from_numpy(w).to(dev) for w in (Wg, Wu, Wd)), H, I, "gelu")
+    Yb = layer.ffn_fused_bf16(F, bf_dev(X, dev), M=M)
+    a_bf = F.last_activation(M).cpu().numpy()
+    Y32 = F(torch.from_numpy(X.reshape(-1)).to(dev), M=M)
+    a_32 = F.last_activation(M).cpu().numpy()
+    torch.cuda.synchronize()
+    assert np.array_equal(a_bf, a_32)
+    y32 = Y32.cpu().numpy().reshape(M, H)
+    got = parity.bits_bf16_f32(parity.bf16_bits(Yb)).reshape(M, H)
+    same = got == qn.bf16_rne(y32)
+    # where they differ, y32 sits within float32 noise of a bf16 rounding point
+    if not same.all():
+        off = np.abs(y32[~same].astype(np.float64) - got[~same].astype(np.float64))
+        half_ulp = np.abs(got[~same].astype(np.float64)) * 2.0 ** -9
+        assert np.all(np.abs(off - half_ulp) <= np.abs(y32[~same]) * 2.0 ** -20 + 1e-30)
+    F.close()
+
+
+# ---- the whole layer, stage by stage (model.py:705-790) -----------------------------
+
+@pytest.mark.parametrize("sliding", [True, False])
+def test_gemma4_layer_stagewise(orc, dev, sliding):
+    from alveare_amd import layer
+
+    H, I, S = 512, 1024, 64
+    D, kv = (256, 8) if sliding else (512, 1)
+    q_size, k_size = 16 * D, kv * D
+    n_qkv = q_size + (2 if sliding else 1) * k_size
+    _say(f"gemma4 layer sliding={sliding} H={H} I={I}")
+    rng = np.random.default_rng(300 + sliding)
+    Wqkv = orc.synth_q4(n_qkv, H, 301)
+    Wo = orc.synth_q4(H, q_size, 302)
+    Wg, Wu, Wd = orc.synth_q4(I, H, 303), orc.synth_q4(I, H, 304), orc.synth_q4(H, I, 305)
+    norms = {k: rng.uniform(0.5, 1.5, D if k in ("q", "k") else H).astype(np.float32)
+             for k in ("attn", "q", "k", "post_attn", "ffn", "post_ffw")}
+    scale = np.float32(0.6)
+    L = layer.Gemma4DecodeLayer(qkv=Wqkv, o=Wo, gate=Wg, up=Wu, down=Wd, norms=norms, scale=float(scale),
+                                sliding=sliding, H=H, I=I, max_seq=S, device=dev)
+    table = qn.cos_sin_table_gemma(10000.0 if sliding else 1e6, D, S)
+    kc = np.zeros((kv, S, D), np.float32)
+    vc = np.zeros((kv, S, D), np.float32)
+    for pos in range(6):
+        x = rnd_bf16(rng, H, 1.0)
+        y = L.forward(bf_dev(x, dev), pos)
+        torch.cuda.synchronize()
+        g = {k: bf_np(getattr(L, k)) for k in ("x_norm", "qkv_out", "q_rope", "attn_out", "attn_proj", "x_post",
+                                                "x_norm2", "down")}
+        assert np.array_equal(g["x_norm"], qn.rmsnorm_cpu(x, norms["attn"]))
+        parity.gemv_bf16_check(orc, Wqkv, g["x_norm"], parity.bf16_bits(L.qkv_out), n_qkv, H)
+        # norms + rope + cache insert from the GPU's qkv
+        qkv = g["qkv_out"]
+        q, k = qkv[:q_size], qkv[q_size:q_size + k_size]
+        v = qkv[q_size + k_size:] if sliding else k
+        q_n = np.concatenate([qn.rmsnorm_cpu(q[h * D:(h + 1) * D], norms["q"]) for h in range(16)])
+        k_n = np.concatenate([qn.rmsnorm_cpu(k[h * D:(h + 1) * D], norms["k"]) for h in range(kv)])
+        v_n = np.concatenate([qn.rmsnorm_cpu(v[h * D:(h + 1) * D], None) for h in range(kv)])
+        assert np.array_equal(g["q_rope"], qn.rope_cpu_gemma(q_n, table[pos], D))
+        kc[:, pos] = qn.rope_cpu_gemma(k_n, table[pos], D).reshape(kv, D)
+        vc[:, pos] = v_n.reshape(kv, D)
+        assert np.array_equal(bf_np(L.kcache).reshape(kv, S, D), kc)
+        assert np.array_equal(bf_np(L.vcache).reshape(kv, S, D), vc)
+        _attn_check(g["q_rope"], kc, vc, pos, 16, kv, D, 1024 if sliding else 0, parity.bf16_bits(L.attn_out))
+        parity.gemv_bf16_check(orc, Wo, g["attn_out"], parity.bf16_bits(L.attn_proj), H, q_size)
+        x_post = qn.bf16_rne(x + qn.rmsnorm_cpu(g["attn_proj"], norms["post_attn"]))
+        assert np.array_equal(g["x_post"], x_post)
+        assert np.array_equal(g["x_norm2"], qn.rmsnorm_cpu(x_post, norms["ffn"]))
+        # FFN from the GPU's x_norm2: the layer's bf16 FFN is the rounding of the
+        # float32 FFN on the same input, which meets the flip-aware FFN bar.
+        a_layer = L.ffn.last_activation().cpu().numpy().reshape(-1)
+        y32 = L.ffn(torch.from_numpy(g["x_norm2"]).to(dev)).cpu().numpy().reshape(-1)
+        a32 = L.ffn.last_activation().cpu().numpy().reshape(-1)
+        assert np.array_equal(a_layer, a32)
+        parity.ffn_check(orc, Wg, Wu, Wd, g["x_norm2"], H, I, 0, y32, a_test=a32)
+        assert np.array_equal(g["down"], qn.bf16_rne(y32))
+        y_ref = qn.bf16_rne(qn.bf16_rne(x_post + qn.rmsnorm_cpu(g["down"], norms["post_ffw"])) * scale)
+        assert np.array_equal(bf_np(y), y_ref)
+    L.close()

@@ -381,3 +381,105 @@ def test_quantize_matches_numpy_restatement(orc):
     assert q[7, 96] == -8 and np.all(q[7, 97:128] == 0) and s[7, 3] == 0x7F80
     assert np.all(q[10, :32] == 0) and s[10, 0] == 0x3F80
     assert q[3, 31] == 7 and s[3, 0] == 0  # subnormal scale 3 * 2^-149 rounds to bf16 +0
+
+
+# ---- host ops of a decode layer (runtime/py/model.py:522-628, :705-790) ------------
+
+@pytest.mark.parametrize("n", [1, 7, 8, 100, 128, 129, 256, 512, 1000, 1152, 2048, 2560, 3840, 4096, 5376,
+                               8192, 12288, 15360, 16384, 20480])
+def test_gpu_summation_order_is_numpys(n):
+    """The GPU RMSNorm sums squares in numpy's pairwise order: its algorithm,
+    restated in parity.pw_sum_gpu_order, equals np.add.reduce (and np.mean is
+    that sum / n in float32) bit for bit, for halving widths and others."""
+    rng = np.random.default_rng(n)
+    for _ in range(3):
+        x = q4_numpy.bf16_rne(rng.normal(0, rng.uniform(0.01, 30), n).astype(np.float32))
+        sq = x ** 2
+        s = np.add.reduce(sq)
+        assert parity.pw_sum_gpu_order(sq) == s
+        assert np.mean(sq) == np.float32(s / np.float32(n))
+
+
+def test_rmsnorm_restatement_pins():
+    rng = np.random.default_rng(3)
+    w = rng.uniform(0.5, 1.5, 3840).astype(np.float32)
+    # Constant +-2^k rows: mean(x^2) = 4^k exactly, sqrt(4^k + eps) rounds to
+    # 2^k (k >= 3), so the output is bf16(+-w).
+    for k in (3, 5, -1 + 10):
+        c = np.float32(2.0 ** k)
+        x = np.full(3840, c, np.float32)
+        x[::3] = -c
+        assert np.array_equal(q4_numpy.rmsnorm_cpu(x, w), q4_numpy.bf16_rne(np.sign(x) * w))
+    # fp64 brute force: within one bf16 ulp.
+    x = q4_numpy.bf16_rne(rng.normal(0, 3, 3840).astype(np.float32))
+    y = q4_numpy.rmsnorm_cpu(x, w).astype(np.float64)
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt(np.mean(x64 ** 2) + 1e-6) * w
+    assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-30)
+    # No weights (Gemma-4's v norm): unit RMS.
+    z = q4_numpy.rmsnorm_cpu(x, None).astype(np.float64)
+    assert abs(np.sqrt(np.mean(z ** 2)) - 1.0) < 5e-3
+
+
+def test_rope_restatement_pins():
+    t = q4_numpy.cos_sin_table_gemma(10000.0, 256, 64)
+    assert np.all(t[0, :128] == 1.0) and np.all(t[0, 128:] == 0.0)
+    g = q4_numpy.cos_sin_table_gemma(1e6, 512, 8)
+    assert np.all(g[5, 64:256] == 1.0) and np.all(g[5, 256 + 64:] == 0.0)  # unrotated three quarters
+    rng = np.random.default_rng(4)
+    x = q4_numpy.bf16_rne(rng.normal(0, 1, 16 * 256).astype(np.float32))
+    assert np.array_equal(q4_numpy.rope_cpu_gemma(x, t[0], 256), x)  # position 0: identity
+    # A rotation: per pair, within one bf16 ulp of the fp64 rotation by the table's angles.
+    pos = 37
+    y = q4_numpy.rope_cpu_gemma(x, t[pos], 256).astype(np.float64).reshape(16, 256)
+    c, s = t[pos, :128].astype(np.float64), t[pos, 128:].astype(np.float64)
+    xr = x.astype(np.float64).reshape(16, 256)
+    ref = np.concatenate([xr[:, :128] * c - xr[:, 128:] * s, xr[:, 128:] * c + xr[:, :128] * s], axis=1)
+    assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -8 + 2.0 ** -24 * (np.abs(xr) @ np.ones((256, 256))))
+    # the table holds cos/sin of pos * base^(-2i/dim) to bf16 precision
+    f = pos * 10000.0 ** (-np.arange(0, 256, 2) / 256)
+    assert np.all(np.abs(t[pos, :128] - np.cos(f)) <= 2.0 ** -8 + 1e-6)
+
+
+def test_attention_restatement_pins():
+    rng = np.random.default_rng(5)
+    kv, D, S, heads = 2, 64, 40, 4
+    kc = q4_numpy.bf16_rne(rng.normal(0, 1, (kv, S, D)).astype(np.float32))
+    vc = q4_numpy.bf16_rne(rng.normal(0, 1, (kv, S, D)).astype(np.float32))
+    q = q4_numpy.bf16_rne(rng.normal(0, 1, heads * D).astype(np.float32))
+    # One position: softmax 1, the output is v itself (bf16 exact).
+    out = q4_numpy.attention_host(q, kc, vc, 0, heads, kv, D, 1.0)
+    assert np.array_equal(out.reshape(heads, D), np.repeat(vc[:, 0], 2, axis=0))
+    # q = 0: uniform weights, the mean of v over the window (GQA: heads 2k, 2k+1 share kv head k).
+    out = q4_numpy.attention_host(np.zeros(heads * D, np.float32), kc, vc, 29, heads, kv, D, 1.0, window=10)
+    mean = vc[:, 20:30].astype(np.float64).mean(1)
+    assert np.all(np.abs(out.reshape(heads, D) - np.repeat(mean, 2, axis=0)) <= np.abs(np.repeat(mean, 2, 0)) * 2.0 ** -8 + 1e-6)
+    # fp64 brute force, global attention.
+    out = q4_numpy.attention_host(q, kc, vc, 33, heads, kv, D, 0.125).astype(np.float64).reshape(heads, D)
+    for h in range(heads):
+        k64, v64 = kc[h // 2, :34].astype(np.float64), vc[h // 2, :34].astype(np.float64)
+        sc = k64 @ q[h * D:(h + 1) * D].astype(np.float64) * 0.125
+        p = np.exp(sc - sc.max())
+        ref = (p / p.sum()) @ v64
+        assert np.all(np.abs(out[h] - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-5 * (p / p.sum()) @ np.abs(v64) + 1e-6)
+
+
+def test_gemma4_layer_restatement_closed_form():
+    """With zero O and down projections both branches vanish (rmsnorm(0) = 0),
+    so the layer is y = bf16(bf16(x) * scale) and the caches still receive k
+    and v at pos."""
+    rng = np.random.default_rng(6)
+    H = 256
+    x = q4_numpy.bf16_rne(rng.normal(0, 1, H).astype(np.float32))
+    w = {k: rng.uniform(0.5, 1.5, 256).astype(np.float32) for k in ("attn", "q", "k", "post_attn", "ffn", "post_ffw")}
+    w["scale"] = np.float32(0.75)
+    qkv_val = q4_numpy.bf16_rne(rng.normal(0, 1, 8192).astype(np.float32))
+    kc = np.zeros((8, 16, 256), np.float32)
+    vc = np.zeros((8, 16, 256), np.float32)
+    t = q4_numpy.cos_sin_table_gemma(10000.0, 256, 16)
+    y = q4_numpy.gemma4_decode_layer(x, 3, True, w, lambda xn: qkv_val, lambda a: np.zeros(H, np.float32),
+                                     lambda xn: np.zeros(H, np.float32), kc, vc, t[3])
+    assert np.array_equal(y, q4_numpy.bf16_rne(x * np.float32(0.75)))
+    v_n = np.concatenate([q4_numpy.rmsnorm_cpu(qkv_val[6144 + 256 * h:6144 + 256 * (h + 1)], None) for h in range(8)])
+    assert np.array_equal(vc[:, 3].reshape(-1), v_n)
+    assert np.any(kc[:, 3] != 0) and not np.any(kc[:, 4])
