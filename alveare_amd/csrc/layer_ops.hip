@@ -8,6 +8,8 @@
 //                    sliding window), float32 softmax, bf16 out
 //   alv_add_norm     residual add of a (normalised) branch, output scale, and
 //                    the next norm, in one pass
+//   alv_embed        token embedding row (fp16 table) scaled to bf16, the token
+//                    read from device memory
 //
 // Bit-exact parts. The reference computes with numpy in float32 on bf16
 // arrays. Every elementwise step here is the same float32 operation with the
@@ -29,9 +31,14 @@
 //
 // Attention is not bit-exact: the reference's scores and weighted sums are
 // BLAS dot products (np.dot) whose order is the library's. Here the positions
-// are split into chunks of 64 (workgroup per (kv head, chunk)); each chunk's
-// max, exp-sum and weighted V sum go to the stream's scratch and the last
-// workgroup of a kv head merges them in chunk order (deterministic).
+// are split into chunks of 64: a workgroup per (chunk, kv head, group of up
+// to 4 q heads) writes the chunk's max, exp-sum and weighted V sum to the
+// stream's scratch, and a second launch merges the chunks of every (head,
+// column) in chunk order (deterministic).
+//
+// Row kernels run 256 threads per row: 16-byte loads and stores, and the
+// pairwise sum with 8 lanes per leaf (lane j holds the leaf's accumulator
+// r[j]; three xor shuffles combine them in numpy's order).
 //
 // Decode position `pos` is read from device memory (pos_dev), so a captured
 // graph replays for every token; positions at or past the cache length write
@@ -45,6 +52,9 @@ namespace alv {
 
 namespace {
 
+constexpr int kRowThreads = 256;
+constexpr int kMaxRowK = 32768;  // 128 KiB of float32 row in LDS
+
 __device__ __forceinline__ uint16_t bf16_rne_bits(float v) {
     if (v != v) return 0x7FC0u;
     const uint32_t u = __builtin_bit_cast(uint32_t, v);
@@ -53,31 +63,33 @@ __device__ __forceinline__ uint16_t bf16_rne_bits(float v) {
 
 __device__ __forceinline__ float bf16r(float v) { return bf16_bits_to_f32(bf16_rne_bits(v)); }
 
-// ---- numpy's pairwise float32 sum ------------------------------------------------
+__device__ __forceinline__ float sqv(const float* a, int i) { return __fmul_rn(a[i], a[i]); }
 
-// The leaf rule over a[0, n), n <= 128 (a 16-byte aligned when n >= 8).
-__device__ float pw_leaf(const float* a, int n) {
+// ---- numpy's pairwise float32 sum of squares ---------------------------------------
+
+// The leaf rule over the squares of a[0, n), n <= 128, on one lane.
+__device__ float pw_leaf_sq(const float* a, int n) {
     if (n < 8) {
         float r = 0.0f;
-        for (int i = 0; i < n; ++i) r = __fadd_rn(r, a[i]);
+        for (int i = 0; i < n; ++i) r = __fadd_rn(r, sqv(a, i));
         return r;
     }
     float r[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] = a[j];
+    for (int j = 0; j < 8; ++j) r[j] = sqv(a, j);
     int i = 8;
     for (; i < n - (n % 8); i += 8) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) r[j] = __fadd_rn(r[j], a[i + j]);
+        for (int j = 0; j < 8; ++j) r[j] = __fadd_rn(r[j], sqv(a, i + j));
     }
     float res = __fadd_rn(__fadd_rn(__fadd_rn(r[0], r[1]), __fadd_rn(r[2], r[3])),
                           __fadd_rn(__fadd_rn(r[4], r[5]), __fadd_rn(r[6], r[7])));
-    for (; i < n; ++i) res = __fadd_rn(res, a[i]);
+    for (; i < n; ++i) res = __fadd_rn(res, sqv(a, i));
     return res;
 }
 
-// The full recursion on one lane (row widths whose splits are not halvings).
-__device__ float pw_serial(const float* a, int n) {
+// The full recursion on one lane (widths whose splits are not halvings).
+__device__ float pw_serial_sq(const float* a, int n) {
     struct Frame {
         int off, n, stage;
         float left;
@@ -89,7 +101,7 @@ __device__ float pw_serial(const float* a, int n) {
     while (sp >= 0) {
         Frame& f = st[sp];
         if (f.n <= 128) {
-            ret = pw_leaf(a + f.off, f.n);
+            ret = pw_leaf_sq(a + f.off, f.n);
             --sp;
             continue;
         }
@@ -112,9 +124,9 @@ __device__ float pw_serial(const float* a, int n) {
     return ret;
 }
 
-// The pairwise sum of a[0, n), n <= 8192, for the calling wave (all 64
-// lanes; a in LDS, 16-byte aligned). Returned in every lane.
-__device__ float pw_chunk_wave(const float* a, int n, int lane) {
+// Pairwise sum of the squares of a[0, n), n <= 8192, by the workgroup
+// (kRowThreads threads; a and red in LDS, red >= 65 floats). Returned to all.
+__device__ float pw_chunk_sq(const float* a, int n, float* red, int tid) {
     int leaf = n, leaves = 1;
     bool halving = true;
     while (leaf > 128) {
@@ -125,76 +137,136 @@ __device__ float pw_chunk_wave(const float* a, int n, int lane) {
         leaf /= 2;
         leaves *= 2;
     }
-    if (halving && leaves <= 64) {
-        float v = lane < leaves ? pw_leaf(a + (size_t)lane * leaf, leaf) : 0.0f;
-        for (int s = 1; s < leaves; s *= 2) {
-            const float o = __shfl_down(v, s);
-            if ((lane & (2 * s - 1)) == 0) v = __fadd_rn(v, o);
+    if (!halving || leaves > 64) {
+        if (tid == 0) red[64] = pw_serial_sq(a, n);
+    } else {
+        // 8 lanes per leaf: lane j sums r[j] = a[j] + a[8 + j] + ... in order.
+        const int j = tid & 7;
+        const int m8 = leaf - leaf % 8;
+        for (int base = 0; base < leaves; base += kRowThreads / 8) {
+            const int lf = base + (tid >> 3);
+            const bool act = lf < leaves;
+            const float* p = a + (size_t)(act ? lf : 0) * leaf;
+            float r = 0.0f;
+            if (act && leaf >= 8) {
+                r = sqv(p, j);
+                for (int i = 8 + j; i < m8; i += 8) r = __fadd_rn(r, sqv(p, i));
+            }
+            r = __fadd_rn(r, __shfl_xor(r, 1));
+            r = __fadd_rn(r, __shfl_xor(r, 2));
+            r = __fadd_rn(r, __shfl_xor(r, 4));
+            if (act && j == 0) {
+                if (leaf < 8) {
+                    r = 0.0f;
+                    for (int i = 0; i < leaf; ++i) r = __fadd_rn(r, sqv(p, i));
+                } else {
+                    for (int i = m8; i < leaf; ++i) r = __fadd_rn(r, sqv(p, i));
+                }
+                red[lf] = r;
+            }
         }
-        return __shfl(v, 0);
+        __syncthreads();
+        if (tid < 64) {
+            float v = tid < leaves ? red[tid] : 0.0f;
+            for (int s = 1; s < leaves; s *= 2) {
+                const float o = __shfl_down(v, s);
+                if ((tid & (2 * s - 1)) == 0) v = __fadd_rn(v, o);
+            }
+            if (tid == 0) red[64] = v;
+        }
     }
-    float r = 0.0f;
-    if (lane == 0) r = pw_serial(a, n);
-    return __shfl(r, 0);
-}
-
-// np.add.reduce(a[0, n)): numpy's reduction loop takes the array in buffers
-// of 8192 elements (np.getbufsize()), sums each pairwise and adds the buffer
-// sums in order.
-__device__ float pw_sum_wave(const float* a, int n, int lane) {
-    constexpr int kBuf = 8192;
-    float r = pw_chunk_wave(a, min(n, kBuf), lane);
-    for (int off = kBuf; off < n; off += kBuf) r = __fadd_rn(r, pw_chunk_wave(a + off, min(n - off, kBuf), lane));
+    __syncthreads();
+    const float r = red[64];
+    __syncthreads();  // red is reused by the next call
     return r;
 }
 
-// 1 / sqrt(mean(x^2) + eps) of the K float32 values xs (LDS) in numpy's
-// float32 arithmetic; sq is K floats of LDS scratch. One wave (the workgroup).
-__device__ float rms_inv(const float* xs, float* sq, int K, float eps, int lane) {
-    for (int i = lane; i < K; i += 64) sq[i] = __fmul_rn(xs[i], xs[i]);
-    __syncthreads();
-    const float s = pw_sum_wave(sq, K, lane);
-    __syncthreads();
+// 1 / sqrt(mean(x^2) + eps) of the K values xs (LDS) in numpy's float32
+// arithmetic: np.add.reduce takes the array in buffers of 8192 elements
+// (np.getbufsize()), sums each pairwise and adds the buffer sums in order.
+__device__ float rms_inv(const float* xs, int K, float eps, float* red, int tid) {
+    constexpr int kBuf = 8192;
+    float s = pw_chunk_sq(xs, min(K, kBuf), red, tid);
+    for (int off = kBuf; off < K; off += kBuf) s = __fadd_rn(s, pw_chunk_sq(xs + off, min(K - off, kBuf), red, tid));
     const float var = __fdiv_rn(s, (float)K);
     // sqrtf is the correctly rounded square root here (v_sqrt_f32 plus a
     // neighbour test); __fsqrt_rn compiles to the bare 1-ulp v_sqrt_f32.
     return __fdiv_rn(1.0f, sqrtf(__fadd_rn(var, eps)));
 }
 
-__device__ __forceinline__ void stage_bf16(const uint16_t* x, float* xs, int K, int lane) {
-    for (int i = lane; i < K; i += 64) xs[i] = bf16_bits_to_f32(x[i]);
+__device__ __forceinline__ void unpack8(uint4 v, float (&f)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = bf16_bits_to_f32(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu);
+}
+
+__device__ __forceinline__ uint4 pack8(const uint16_t (&b)[8]) {
+    return uint4{b[0] | ((uint32_t)b[1] << 16), b[2] | ((uint32_t)b[3] << 16), b[4] | ((uint32_t)b[5] << 16),
+                 b[6] | ((uint32_t)b[7] << 16)};
+}
+
+__device__ __forceinline__ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// xs[0, K) = float(x[0, K)); all threads, then a barrier.
+__device__ void stage_row(const uint16_t* x, float* xs, int K, int tid) {
+    if (al16(x) && K % 8 == 0) {
+        for (int v = tid; v < K / 8; v += kRowThreads) {
+            float f[8];
+            unpack8(reinterpret_cast<const uint4*>(x)[v], f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xs[8 * v + e] = f[e];
+        }
+    } else {
+        for (int i = tid; i < K; i += kRowThreads) xs[i] = bf16_bits_to_f32(x[i]);
+    }
     __syncthreads();
 }
 
-// bf16(x * inv * w) (w may be null), in place.
-__device__ __forceinline__ void norm_apply(float* xs, int K, float inv, const float* w, int lane) {
-    for (int i = lane; i < K; i += 64) {
-        const float t = __fmul_rn(xs[i], inv);
-        xs[i] = bf16r(w ? __fmul_rn(t, w[i]) : t);
+// out[0, pad) = bf16(xs * inv * w) for i < K (w may be null), 0 past K.
+__device__ void write_norm(const float* xs, int K, int pad, float inv, const float* w, uint16_t* out, int tid) {
+    if (al16(out) && al16(w) && K % 8 == 0 && pad % 8 == 0) {
+        for (int v = tid; v < pad / 8; v += kRowThreads) {
+            uint16_t b[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (8 * v < K) {
+                float wf[8];
+                if (w) {
+                    const float4 w0 = reinterpret_cast<const float4*>(w)[2 * v];
+                    const float4 w1 = reinterpret_cast<const float4*>(w)[2 * v + 1];
+                    wf[0] = w0.x; wf[1] = w0.y; wf[2] = w0.z; wf[3] = w0.w;
+                    wf[4] = w1.x; wf[5] = w1.y; wf[6] = w1.z; wf[7] = w1.w;
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float t = __fmul_rn(xs[8 * v + e], inv);
+                    b[e] = bf16_rne_bits(w ? __fmul_rn(t, wf[e]) : t);
+                }
+            }
+            reinterpret_cast<uint4*>(out)[v] = pack8(b);
+        }
+    } else {
+        for (int i = tid; i < pad; i += kRowThreads) {
+            uint16_t b = 0;
+            if (i < K) {
+                const float t = __fmul_rn(xs[i], inv);
+                b = bf16_rne_bits(w ? __fmul_rn(t, w[i]) : t);
+            }
+            out[i] = b;
+        }
     }
-    __syncthreads();
 }
 
 // ---- alv_rmsnorm ---------------------------------------------------------------
 
-__global__ void __launch_bounds__(64) rmsnorm_kernel(const uint16_t* x, int ldx, const float* w, uint16_t* out,
-                                                     int ldo, int K, int pad, float eps) {
+__global__ void __launch_bounds__(kRowThreads) rmsnorm_kernel(const uint16_t* x, int ldx, const float* w, uint16_t* out,
+                                                              int ldo, int K, int pad, float eps) {
     extern __shared__ __align__(16) float lds[];
-    float* xs = lds;
-    float* sq = lds + ((K + 3) & ~3);
-    const int lane = threadIdx.x;
+    float* red = lds;
+    float* xs = lds + 128;
+    const int tid = threadIdx.x;
     const size_t row = blockIdx.x;
-    stage_bf16(x + row * ldx, xs, K, lane);
-    const float inv = rms_inv(xs, sq, K, eps, lane);
-    uint16_t* o = out + row * ldo;
-    for (int i = lane; i < pad; i += 64) {
-        uint16_t b = 0;
-        if (i < K) {
-            const float t = __fmul_rn(xs[i], inv);
-            b = bf16_rne_bits(w ? __fmul_rn(t, w[i]) : t);
-        }
-        o[i] = b;
-    }
+    stage_row(x + row * ldx, xs, K, tid);
+    const float inv = rms_inv(xs, K, eps, red, tid);
+    write_norm(xs, K, pad, inv, w, out + row * ldo, tid);
 }
 
 // ---- alv_qkv_post --------------------------------------------------------------
@@ -217,120 +289,153 @@ struct QkvPostArgs {
 };
 
 // Block b: q head b, k head b - heads, or v head b - heads - kv_heads.
-__global__ void __launch_bounds__(64) qkv_post_kernel(QkvPostArgs a) {
+__global__ void __launch_bounds__(kRowThreads) qkv_post_kernel(QkvPostArgs a) {
     extern __shared__ __align__(16) float lds[];
+    float* red = lds;
+    float* xs = lds + 128;
     const int D = a.D;
-    float* xs = lds;
-    float* sq = lds + ((D + 3) & ~3);
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x;
     const int b = blockIdx.x;
     const int pos = *a.pos;
     if (pos < 0 || pos >= a.max_seq) return;
     const int role = b < a.heads ? 0 : (b < a.heads + a.kv_heads ? 1 : 2);
     const int h = role == 0 ? b : (role == 1 ? b - a.heads : b - a.heads - a.kv_heads);
     const int src = role == 0 ? h * D : (role == 1 || a.v_off < 0 ? a.k_off + h * D : a.v_off + h * D);
-    stage_bf16(a.qkv + src, xs, D, lane);
+    stage_row(a.qkv + src, xs, D, tid);
     const int norm = role == 0 ? a.norm_q : (role == 1 ? a.norm_k : a.norm_v);
     if (norm) {
-        const float inv = rms_inv(xs, sq, D, a.eps, lane);
-        norm_apply(xs, D, inv, role == 0 ? a.q_w : (role == 1 ? a.k_w : nullptr), lane);
+        const float inv = rms_inv(xs, D, a.eps, red, tid);
+        const float* w = role == 0 ? a.q_w : (role == 1 ? a.k_w : nullptr);
+        for (int i = tid; i < D; i += kRowThreads) {
+            const float t = __fmul_rn(xs[i], inv);
+            xs[i] = bf16r(w ? __fmul_rn(t, w[i]) : t);
+        }
+        __syncthreads();
     }
     uint16_t* dst = role == 0 ? a.q_out + (size_t)h * D
                               : (role == 1 ? a.kcache : a.vcache) + ((size_t)h * a.max_seq + pos) * D;
     if (role < 2 && a.rope) {
         // run_rope_cpu_gemma (model.py:549-575): y1 = x1 c - x2 s, y2 = x2 c + x1 s.
         const uint16_t* row = a.rope + (size_t)pos * a.rope_stride;
-        for (int i = lane; i < a.half; i += 64) {
+        for (int i = tid; i < a.half; i += kRowThreads) {
             const float c = bf16_bits_to_f32(row[a.cos_off + i]);
             const float s = bf16_bits_to_f32(row[a.sin_off + i]);
             const float x1 = xs[i], x2 = xs[i + a.half];
             dst[i] = bf16_rne_bits(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s)));
             dst[i + a.half] = bf16_rne_bits(__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s)));
         }
-        for (int i = 2 * a.half + lane; i < D; i += 64) dst[i] = bf16_rne_bits(xs[i]);
+        for (int i = 2 * a.half + tid; i < D; i += kRowThreads) dst[i] = bf16_rne_bits(xs[i]);
     } else {
-        for (int i = lane; i < D; i += 64) dst[i] = bf16_rne_bits(xs[i]);
+        for (int i = tid; i < D; i += kRowThreads) dst[i] = bf16_rne_bits(xs[i]);
     }
 }
 
 // ---- alv_attention -------------------------------------------------------------
 
-constexpr int kAttnChunk = 64;     // cache positions per workgroup
+constexpr int kAttnChunk = 64;    // cache positions per workgroup
 constexpr int kAttnThreads = 256;
-constexpr int kAttnMaxGroup = 16;  // q heads per kv head
-constexpr int kAttnMaxD = 512;
+constexpr int kAttnHeads = 4;     // q heads per workgroup
+constexpr int kAttnMaxChunks = 1024;
 
 struct AttnArgs {
     const uint16_t* q;  // [heads][D]
     const uint16_t* kcache;
     const uint16_t* vcache;
     uint16_t* out;      // [heads][D]
-    int heads, kv_heads, D, max_seq, window;
+    int heads, kv_heads, D, max_seq, window, hg;
     float scale;
     const int* pos;
     int nchunk;          // grid.x: chunks the largest window can need
-    float* part;         // [kv_heads][nchunk][g][D + 2]
-    uint32_t* cnt;       // [kv_heads]
+    float* part;         // [kv_heads][nchunk][g][D + 2]: weighted V sums, max, exp-sum
 };
 
-__global__ void __launch_bounds__(kAttnThreads) attention_kernel(AttnArgs a) {
-    __shared__ __align__(16) float qs[kAttnMaxGroup * kAttnMaxD];
-    __shared__ float es[kAttnMaxGroup][kAttnChunk];
-    __shared__ float ms[kAttnMaxGroup], ls[kAttnMaxGroup];
-    __shared__ int last;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int c = blockIdx.x, kvh = blockIdx.y;
-    const int D = a.D, g = a.heads / a.kv_heads;
-    const int pos = *a.pos;
-    if (pos < 0 || pos >= a.max_seq) return;
+struct AttnSpan {
+    int start, W, nch;
+};
+
+__device__ __forceinline__ AttnSpan attn_span(const AttnArgs& a, int pos) {
     const int seq = pos + 1;
     const int start = a.window > 0 && seq > a.window ? seq - a.window : 0;
     const int W = seq - start;
-    const int nch = (W + kAttnChunk - 1) / kAttnChunk;
-    if (c >= nch) return;
-    const int p0 = c * kAttnChunk;
-    const int np = min(kAttnChunk, W - p0);
+    return {start, W, (W + kAttnChunk - 1) / kAttnChunk};
+}
 
-    // q of the group's heads, float32.
-    for (int i = tid; i < g * D; i += kAttnThreads) qs[i] = bf16_bits_to_f32(a.q[(size_t)kvh * g * D + i]);
+// Chunk c of kv head blockIdx.y for q heads [hg * blockIdx.z, + hg) of its
+// group. D is a template parameter so that every thread issues all of its K
+// and V loads (D/32 16-byte pieces each) before it needs any of them.
+template <int D>
+__global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnArgs a) {
+    constexpr int QD = D / 4;                // score slice per thread (4 threads per position)
+    constexpr int NK = QD / 8;               // its 16-byte K pieces
+    constexpr int DV = D / 8;                // 16-byte column pieces of a V row
+    constexpr int PG = kAttnThreads / DV;    // position groups of the V sum
+    constexpr int NV = kAttnChunk / PG;      // positions per thread in the V sum
+    __shared__ __align__(16) float qs[kAttnHeads * D];
+    __shared__ float es[kAttnHeads][kAttnChunk];
+    __shared__ float ms[kAttnHeads], ls[kAttnHeads];
+    __shared__ __align__(16) float red[8 * kAttnThreads * kAttnHeads];  // [pg][head][D]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = blockIdx.x, kvh = blockIdx.y;
+    const int g = a.heads / a.kv_heads, hg = a.hg;
+    const int h0 = blockIdx.z * hg;
+    const int pos = *a.pos;
+    if (pos < 0 || pos >= a.max_seq) return;
+    const AttnSpan sp = attn_span(a, pos);
+    if (c >= sp.nch) return;
+    const int p0 = c * kAttnChunk;
+    const int np = min(kAttnChunk, sp.W - p0);
+    const size_t row0 = (size_t)kvh * a.max_seq + sp.start + p0;
+
+    // Every load of the workgroup up front: K slices, V pieces, q.
+    const int p = tid >> 2, part = tid & 3;
+    const int dv = tid % DV, pg = tid / DV;
+    uint4 kreg[NK], vreg[NV];
+    {
+        const uint4* kr = reinterpret_cast<const uint4*>(a.kcache + (row0 + min(p, np - 1)) * D + part * QD);
+#pragma unroll
+        for (int i = 0; i < NK; ++i) kreg[i] = kr[i];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int pp = min(pg + j * PG, np - 1);
+            vreg[j] = reinterpret_cast<const uint4*>(a.vcache + (row0 + pp) * D)[dv];
+        }
+    }
+    const uint4* qv = reinterpret_cast<const uint4*>(a.q + ((size_t)kvh * g + h0) * D);
+    for (int i = tid; i < hg * DV; i += kAttnThreads) {
+        float f[8];
+        unpack8(qv[i], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qs[8 * i + e] = f[e];
+    }
     __syncthreads();
 
-    // Scores: 4 threads per position, each a quarter of the row (D % 32 == 0:
-    // the quarter is whole 16-byte pieces).
+    // Scores: 4 threads per position, each a quarter of the row.
     {
-        const int p = tid >> 2, part = tid & 3;
-        const int qd = D / 4;
-        float acc[kAttnMaxGroup];
+        float acc[kAttnHeads] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const float* qp = qs + part * QD;
 #pragma unroll
-        for (int h = 0; h < kAttnMaxGroup; ++h) acc[h] = 0.0f;
-        if (p < np) {
-            const uint4* kr = reinterpret_cast<const uint4*>(
-                a.kcache + ((size_t)kvh * a.max_seq + start + p0 + p) * D + part * qd);
-            const float* qp = qs + part * qd;
-            for (int c8 = 0; c8 < qd / 8; ++c8) {
-                const uint4 v = kr[c8];
-                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+        for (int i = 0; i < NK; ++i) {
+            float kf[8];
+            unpack8(kreg[i], kf);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float kv = bf16_bits_to_f32(e & 1 ? w4[e >> 1] >> 16 : w4[e >> 1] & 0xFFFFu);
+            for (int e = 0; e < 8; ++e)
 #pragma unroll
-                    for (int h = 0; h < kAttnMaxGroup; ++h)
-                        if (h < g) acc[h] = fmaf(kv, qp[h * D + c8 * 8 + e], acc[h]);
-                }
-            }
+                for (int h = 0; h < kAttnHeads; ++h)
+                    if (h < hg) acc[h] = fmaf(kf[e], qp[h * D + i * 8 + e], acc[h]);
         }
 #pragma unroll
-        for (int h = 0; h < kAttnMaxGroup; ++h) {
+        for (int h = 0; h < kAttnHeads; ++h) {
             float v = acc[h];
             v += __shfl_xor(v, 1);
             v += __shfl_xor(v, 2);
-            if (h < g && part == 0) es[h][p] = p < np ? v * a.scale : -__builtin_inff();
+            if (h < hg && part == 0) es[h][p] = p < np ? v * a.scale : -__builtin_inff();
         }
     }
     __syncthreads();
 
-    // Chunk softmax pieces: one wave per head.
-    for (int h = wave; h < g; h += kAttnThreads / 64) {
+    // The chunk's softmax pieces: one wave per head.
+    if (wave < hg) {
+        const int h = wave;
         const float s = es[h][lane];
         float m = s;
         for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
@@ -345,76 +450,84 @@ __global__ void __launch_bounds__(kAttnThreads) attention_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // Weighted V sum of the chunk, then the chunk's partial to scratch.
-    const int gstride = D + 2;
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.part, (uint32_t)((size_t)a.kv_heads * a.nchunk * g * gstride * 4));
-    const uint32_t mybase = (uint32_t)((((size_t)kvh * a.nchunk + c) * g) * gstride * 4);
-    for (int d = tid; d < D; d += kAttnThreads) {
-        float o[kAttnMaxGroup];
+    // Weighted V sum: thread (pg, dv) over positions pg, pg + PG, ...; the PG
+    // partial sums then added in order.
+    {
+        float acc[kAttnHeads][8];
 #pragma unroll
-        for (int h = 0; h < kAttnMaxGroup; ++h) o[h] = 0.0f;
-        const uint16_t* vr = a.vcache + ((size_t)kvh * a.max_seq + start + p0) * D + d;
-        for (int p = 0; p < np; ++p) {
-            const float vv = bf16_bits_to_f32(vr[(size_t)p * D]);
+        for (int h = 0; h < kAttnHeads; ++h)
 #pragma unroll
-            for (int h = 0; h < kAttnMaxGroup; ++h)
-                if (h < g) o[h] = fmaf(es[h][p], vv, o[h]);
+            for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int pp = pg + j * PG;
+            if (pp >= np) continue;
+            float vf[8];
+            unpack8(vreg[j], vf);
+#pragma unroll
+            for (int h = 0; h < kAttnHeads; ++h) {
+                if (h >= hg) continue;
+                const float w = es[h][pp];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(w, vf[e], acc[h][e]);
+            }
         }
 #pragma unroll
-        for (int h = 0; h < kAttnMaxGroup; ++h) {
-            if (h < g)
-                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, o[h]), rp,
-                                                  mybase + (uint32_t)((h * gstride + d) * 4), 0, 16);
+        for (int h = 0; h < kAttnHeads; ++h) {
+            if (h >= hg) continue;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) red[((size_t)pg * hg + h) * D + dv * 8 + e] = acc[h][e];
         }
     }
-    if (tid < g) {
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, ms[tid]), rp,
-                                              mybase + (uint32_t)((tid * gstride + D) * 4), 0, 16);
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, ls[tid]), rp,
-                                              mybase + (uint32_t)((tid * gstride + D + 1) * 4), 0, 16);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (tid == 0)
-        last = __hip_atomic_fetch_add(&a.cnt[kvh], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-               (uint32_t)(nch - 1);
-    __syncthreads();
-    if (!last) return;
-
-    // Last workgroup of this kv head: merge the chunks. Per head, the chunk
-    // maxima give M, the weights f_c = exp(m_c - M) go to LDS (the q slots,
-    // free now) and L = sum l_c f_c; then O[d] = sum o_c[d] f_c and out = O / L.
-    // Fixed lane assignment and reduction order: deterministic.
-    const uint32_t hbase = (uint32_t)(((size_t)kvh * a.nchunk * g) * gstride * 4);
-    float* fs = qs;  // [g][nch]
-    for (int h = wave; h < g; h += kAttnThreads / 64) {
-        float M = -__builtin_inff();
-        for (int q = lane; q < nch; q += 64)
-            M = fmaxf(M, __builtin_bit_cast(float, buf_load4_sc1(rp, hbase + (uint32_t)(((q * g + h) * gstride + D) * 4))));
-        for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-        float L = 0.0f;
-        for (int q = lane; q < nch; q += 64) {
-            const uint32_t b0 = hbase + (uint32_t)(((q * g + h) * gstride + D) * 4);
-            const float m = __builtin_bit_cast(float, buf_load4_sc1(rp, b0));
-            const float l = __builtin_bit_cast(float, buf_load4_sc1(rp, b0 + 4u));
-            const float f = expf(m - M);
-            fs[h * nch + q] = f;
-            L = fmaf(l, f, L);
-        }
-        for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o);
-        if (lane == 0) ls[h] = L;
-    }
-    __syncthreads();
-    for (int i = tid; i < g * D; i += kAttnThreads) {
+    constexpr int gstride = D + 2;
+    float* out = a.part + (((size_t)kvh * a.nchunk + c) * g + h0) * gstride;
+    for (int i = tid; i < hg * D; i += kAttnThreads) {
         const int h = i / D, d = i - h * D;
-        float O = 0.0f;
-#pragma unroll 8
-        for (int q = 0; q < nch; ++q)
-            O = fmaf(__builtin_bit_cast(float, buf_load4_sc1(rp, hbase + (uint32_t)(((q * g + h) * gstride + d) * 4))),
-                     fs[h * nch + q], O);
-        a.out[((size_t)kvh * g + h) * D + d] = bf16_rne_bits(__fdiv_rn(O, ls[h]));
+        float o = 0.0f;
+#pragma unroll
+        for (int q = 0; q < PG; ++q) o += red[((size_t)q * hg + h) * D + d];
+        out[(size_t)h * gstride + d] = o;
     }
-    if (tid == 0) __hip_atomic_store(&a.cnt[kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < hg) {
+        out[(size_t)tid * gstride + D] = ms[tid];
+        out[(size_t)tid * gstride + D + 1] = ls[tid];
+    }
+}
+
+// Head blockIdx.x, columns [256 blockIdx.y, + 256): the chunks merged in order,
+// out = sum_c o_c f_c / sum_c l_c f_c with f_c = exp(m_c - max_c m_c).
+__global__ void __launch_bounds__(kAttnThreads) attn_merge_kernel(AttnArgs a) {
+    __shared__ float fs[kAttnMaxChunks];
+    __shared__ float Ls;
+    const int tid = threadIdx.x;
+    const int hq = blockIdx.x;
+    const int g = a.heads / a.kv_heads, kvh = hq / g, hl = hq - kvh * g;
+    const int D = a.D, gstride = D + 2;
+    const int pos = *a.pos;
+    if (pos < 0 || pos >= a.max_seq) return;
+    const int nch = attn_span(a, pos).nch;
+    const float* base = a.part + ((size_t)kvh * a.nchunk * g + hl) * gstride;  // chunk q at + q * g * gstride
+    for (int q = tid; q < nch; q += kAttnThreads) fs[q] = base[(size_t)q * g * gstride + D];
+    __syncthreads();
+    if (tid == 0) {
+        float M = -__builtin_inff();
+        for (int q = 0; q < nch; ++q) M = fmaxf(M, fs[q]);
+        float L = 0.0f;
+        for (int q = 0; q < nch; ++q) {
+            const float f = expf(fs[q] - M);
+            L = fmaf(base[(size_t)q * g * gstride + D + 1], f, L);
+            fs[q] = f;
+        }
+        Ls = L;
+    }
+    __syncthreads();
+    const int d = blockIdx.y * kAttnThreads + tid;
+    if (d >= D) return;
+    float O = 0.0f;
+#pragma unroll 8
+    for (int q = 0; q < nch; ++q) O = fmaf(base[(size_t)q * g * gstride + d], fs[q], O);
+    a.out[(size_t)hq * D + d] = bf16_rne_bits(__fdiv_rn(O, Ls));
 }
 
 // ---- alv_add_norm --------------------------------------------------------------
@@ -435,54 +548,88 @@ struct AddNormArgs {
     float eps;
 };
 
-__global__ void __launch_bounds__(64) add_norm_kernel(AddNormArgs a) {
+__global__ void __launch_bounds__(kRowThreads) add_norm_kernel(AddNormArgs a) {
     extern __shared__ __align__(16) float lds[];
+    float* red = lds;
+    float* xs = lds + 128;
     const int K = a.K;
-    float* xs = lds;
-    float* sq = lds + ((K + 3) & ~3);
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x;
     const size_t row = blockIdx.x;
-    stage_bf16(a.y + row * a.ldy, xs, K, lane);
-    if (a.norm_y) {
-        const float inv = rms_inv(xs, sq, K, a.eps, lane);
-        norm_apply(xs, K, inv, a.w_y, lane);
-    }
+    stage_row(a.y + row * a.ldy, xs, K, tid);
+    float inv = 1.0f;
+    if (a.norm_y) inv = rms_inv(xs, K, a.eps, red, tid);
     const uint16_t* r = a.resid + row * a.ldr;
     uint16_t* so = a.sum_out + row * a.ld_sum;
-    for (int i = lane; i < K; i += 64) {
-        const float sum = __fadd_rn(bf16_bits_to_f32(r[i]), xs[i]);
-        float v;
-        if (a.scale_mode == 1)
-            v = bf16r(__fmul_rn(bf16r(sum), a.scale));
-        else if (a.scale_mode == 2)
-            v = bf16r(__fmul_rn(sum, a.scale));
-        else
-            v = bf16r(sum);
-        so[i] = bf16_rne_bits(v);
-        xs[i] = v;
+    // s = bf16(r + t) (scaled), t = bf16(y * inv * w_y) or y.
+    auto step = [&](float x, float rv, float w) -> float {
+        float t = x;
+        if (a.norm_y) {
+            t = __fmul_rn(t, inv);
+            t = bf16r(a.w_y ? __fmul_rn(t, w) : t);
+        }
+        const float sum = __fadd_rn(rv, t);
+        if (a.scale_mode == 1) return bf16r(__fmul_rn(bf16r(sum), a.scale));
+        if (a.scale_mode == 2) return bf16r(__fmul_rn(sum, a.scale));
+        return bf16r(sum);
+    };
+    if (al16(r) && al16(so) && al16(a.w_y) && K % 8 == 0) {
+        for (int v = tid; v < K / 8; v += kRowThreads) {
+            float rf[8], wf[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            unpack8(reinterpret_cast<const uint4*>(r)[v], rf);
+            if (a.norm_y && a.w_y) {
+                const float4 w0 = reinterpret_cast<const float4*>(a.w_y)[2 * v];
+                const float4 w1 = reinterpret_cast<const float4*>(a.w_y)[2 * v + 1];
+                wf[0] = w0.x; wf[1] = w0.y; wf[2] = w0.z; wf[3] = w0.w;
+                wf[4] = w1.x; wf[5] = w1.y; wf[6] = w1.z; wf[7] = w1.w;
+            }
+            uint16_t b[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v2 = step(xs[8 * v + e], rf[e], wf[e]);
+                b[e] = bf16_rne_bits(v2);
+                xs[8 * v + e] = v2;
+            }
+            reinterpret_cast<uint4*>(so)[v] = pack8(b);
+        }
+    } else {
+        for (int i = tid; i < K; i += kRowThreads) {
+            const float v2 = step(xs[i], bf16_bits_to_f32(r[i]), a.norm_y && a.w_y ? a.w_y[i] : 0.0f);
+            so[i] = bf16_rne_bits(v2);
+            xs[i] = v2;
+        }
     }
     __syncthreads();
     if (!a.norm_out) return;
-    const float inv = rms_inv(xs, sq, K, a.eps, lane);
-    uint16_t* no = a.norm_out + row * a.ldn;
-    for (int i = lane; i < a.pad; i += 64) {
+    const float inv2 = rms_inv(xs, K, a.eps, red, tid);
+    write_norm(xs, K, a.pad, inv2, a.w_out, a.norm_out + row * a.ldn, tid);
+}
+
+// ---- alv_embed -------------------------------------------------------------------
+
+// out = bf16(float(double(table[token]) * scale)): the reference's lookup
+// (token_embd[token_id].astype(np.float32) * np.sqrt(hidden_size) is a float64
+// product, cast to bf16 through float32, runtime/py/model.py:891). A token
+// outside the table writes zeros.
+__global__ void __launch_bounds__(256) embed_kernel(const uint16_t* table, int vocab, int H, const int32_t* token,
+                                                    double scale, uint16_t* out) {
+    const int t = *token;
+    const bool ok = t >= 0 && t < vocab;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < H; i += gridDim.x * blockDim.x) {
         uint16_t b = 0;
-        if (i < K) {
-            const float t = __fmul_rn(xs[i], inv);
-            b = bf16_rne_bits(a.w_out ? __fmul_rn(t, a.w_out[i]) : t);
+        if (ok) {
+            const float e = (float)__builtin_bit_cast(_Float16, table[(size_t)t * H + i]);
+            b = bf16_rne_bits((float)__dmul_rn((double)e, scale));
         }
-        no[i] = b;
+        out[i] = b;
     }
 }
 
-size_t row_lds(int K) { return (size_t)2 * ((K + 3) & ~3) * sizeof(float); }
+size_t row_lds(int K) { return (size_t)(128 + ((K + 3) & ~3)) * sizeof(float); }
 
 hipError_t set_lds(const void* k, size_t lds) {
     if (lds <= 64 * 1024) return hipSuccess;
     return hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
 }
-
-constexpr int kMaxRowK = 20480;  // 2 x 80 KiB of LDS per row
 
 }  // namespace
 
@@ -500,7 +647,8 @@ extern "C" int alv_rmsnorm(const uint16_t* x, const float* w, uint16_t* out, int
         return fail(ALV_ERR_ALIGN, "x and out need 2-byte, w 4-byte alignment");
     const size_t lds = row_lds(K);
     if (int rc = hip_check(set_lds(reinterpret_cast<const void*>(&rmsnorm_kernel), lds), "hipFuncSetAttribute")) return rc;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(64), lds, (hipStream_t)stream, x, ldx, w, out, ldo, K, pad, eps);
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kRowThreads), lds, (hipStream_t)stream, x, ldx, w, out, ldo, K,
+                       pad, eps);
     return hip_check(hipGetLastError(), "rmsnorm_kernel launch");
 }
 
@@ -522,7 +670,7 @@ extern "C" int alv_qkv_post(const uint16_t* qkv, int k_off, int v_off, int heads
                   rope, rope_stride, cos_off, sin_off, half, pos_dev, max_seq, q_out, kcache, vcache};
     const size_t lds = row_lds(D);
     if (int rc = hip_check(set_lds(reinterpret_cast<const void*>(&qkv_post_kernel), lds), "hipFuncSetAttribute")) return rc;
-    hipLaunchKernelGGL(qkv_post_kernel, dim3(heads + 2 * kv_heads), dim3(64), lds, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(qkv_post_kernel, dim3(heads + 2 * kv_heads), dim3(kRowThreads), lds, (hipStream_t)stream, a);
     return hip_check(hipGetLastError(), "qkv_post_kernel launch");
 }
 
@@ -530,29 +678,35 @@ extern "C" int alv_attention(const uint16_t* q, const uint16_t* kcache, const ui
                              int heads, int kv_heads, int D, int max_seq, int window, float scale, const int* pos_dev,
                              void* stream) {
     if (!q || !kcache || !vcache || !out || !pos_dev) return fail(ALV_ERR_ARG, "null pointer");
-    if (heads < 1 || kv_heads < 1 || heads % kv_heads || heads / kv_heads > kAttnMaxGroup || D < 32 || D % 32 ||
-        D > kAttnMaxD || max_seq < 1 || window < 0)
+    if (heads < 1 || kv_heads < 1 || heads % kv_heads || (D != 64 && D != 128 && D != 256 && D != 512) ||
+        max_seq < 1 || window < 0)
         return fail(ALV_ERR_ARG, "bad attention shape heads=%d kv_heads=%d D=%d max_seq=%d window=%d "
-                    "(group <= %d, D a multiple of 32 up to %d)", heads, kv_heads, D, max_seq, window, kAttnMaxGroup, kAttnMaxD);
-    if (reinterpret_cast<uintptr_t>(kcache) % 16 || reinterpret_cast<uintptr_t>(q) % 2 ||
-        reinterpret_cast<uintptr_t>(vcache) % 2 || reinterpret_cast<uintptr_t>(out) % 2)
-        return fail(ALV_ERR_ALIGN, "kcache needs 16-byte alignment");
+                    "(D one of 64, 128, 256, 512)", heads, kv_heads, D, max_seq, window);
+    if (reinterpret_cast<uintptr_t>(kcache) % 16 || reinterpret_cast<uintptr_t>(vcache) % 16 ||
+        reinterpret_cast<uintptr_t>(q) % 16 || reinterpret_cast<uintptr_t>(out) % 2)
+        return fail(ALV_ERR_ALIGN, "q, kcache and vcache need 16-byte alignment");
     hipStream_t s = (hipStream_t)stream;
     const int span = window > 0 ? std::min(window, max_seq) : max_seq;
     const int nchunk = (span + kAttnChunk - 1) / kAttnChunk;
+    if (nchunk > kAttnMaxChunks)
+        return fail(ALV_ERR_RANGE, "a span of %d positions exceeds the %d the merge takes", span, kAttnMaxChunks * kAttnChunk);
     const int g = heads / kv_heads;
-    if ((size_t)g * nchunk > (size_t)kAttnMaxGroup * kAttnMaxD)
-        return fail(ALV_ERR_RANGE, "a span of %d positions in %d-head groups exceeds the merge's %d chunk weights", span, g,
-                    kAttnMaxGroup * kAttnMaxD);
+    const int hg = g % 4 == 0 ? 4 : (g % 2 == 0 ? 2 : 1);
     const size_t part_bytes = (size_t)kv_heads * nchunk * g * (D + 2) * sizeof(float);
-    if (part_bytes >= 0xFFFFF000ull) return fail(ALV_ERR_RANGE, "attention partials exceed the 4 GiB buffer range");
-    const size_t cnt_bytes = ((size_t)kv_heads * sizeof(uint32_t) + 255) & ~(size_t)255;
     void* sc = nullptr;
-    if (int rc = get_scratch(s, kScratchAttn, cnt_bytes + part_bytes, &sc)) return rc;
-    AttnArgs a{q, kcache, vcache, out, heads, kv_heads, D, max_seq, window, scale, pos_dev, nchunk,
-               reinterpret_cast<float*>(static_cast<uint8_t*>(sc) + cnt_bytes), static_cast<uint32_t*>(sc)};
-    hipLaunchKernelGGL(attention_kernel, dim3(nchunk, kv_heads), dim3(kAttnThreads), 0, s, a);
-    return hip_check(hipGetLastError(), "attention_kernel launch");
+    if (int rc = get_scratch(s, kScratchAttn, part_bytes, &sc)) return rc;
+    AttnArgs a{q, kcache, vcache, out, heads, kv_heads, D, max_seq, window, hg, scale, pos_dev, nchunk,
+               static_cast<float*>(sc)};
+    const dim3 grid(nchunk, kv_heads, g / hg);
+    switch (D) {
+        case 64: hipLaunchKernelGGL(attn_partial_kernel<64>, grid, dim3(kAttnThreads), 0, s, a); break;
+        case 128: hipLaunchKernelGGL(attn_partial_kernel<128>, grid, dim3(kAttnThreads), 0, s, a); break;
+        case 256: hipLaunchKernelGGL(attn_partial_kernel<256>, grid, dim3(kAttnThreads), 0, s, a); break;
+        default: hipLaunchKernelGGL(attn_partial_kernel<512>, grid, dim3(kAttnThreads), 0, s, a); break;
+    }
+    if (int rc = hip_check(hipGetLastError(), "attn_partial_kernel launch")) return rc;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(heads, (D + kAttnThreads - 1) / kAttnThreads), dim3(kAttnThreads), 0, s, a);
+    return hip_check(hipGetLastError(), "attn_merge_kernel launch");
 }
 
 extern "C" int alv_add_norm(const uint16_t* resid, int ldr, const uint16_t* y, int ldy, const float* w_y, int norm_y,
@@ -566,6 +720,15 @@ extern "C" int alv_add_norm(const uint16_t* resid, int ldr, const uint16_t* y, i
                   K, norm_out ? pad : K, eps};
     const size_t lds = row_lds(K);
     if (int rc = hip_check(set_lds(reinterpret_cast<const void*>(&add_norm_kernel), lds), "hipFuncSetAttribute")) return rc;
-    hipLaunchKernelGGL(add_norm_kernel, dim3(rows), dim3(64), lds, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(add_norm_kernel, dim3(rows), dim3(kRowThreads), lds, (hipStream_t)stream, a);
     return hip_check(hipGetLastError(), "add_norm_kernel launch");
+}
+
+extern "C" int alv_embed(const uint16_t* table_f16, int vocab, int H, const int32_t* token_dev, double scale,
+                         uint16_t* out, void* stream) {
+    if (!table_f16 || !token_dev || !out) return fail(ALV_ERR_ARG, "null pointer");
+    if (vocab < 1 || H < 1) return fail(ALV_ERR_ARG, "bad embedding shape vocab=%d H=%d", vocab, H);
+    hipLaunchKernelGGL(embed_kernel, dim3(std::min((H + 255) / 256, 64)), dim3(256), 0, (hipStream_t)stream,
+                       table_f16, vocab, H, token_dev, scale, out);
+    return hip_check(hipGetLastError(), "embed_kernel launch");
 }

@@ -32,7 +32,9 @@ import numpy as np
 import torch
 
 from ._lib import check, lib
-from .ops import FfnWeights, Q4Weight, _need_gpu, _stream
+import math
+
+from .ops import FfnWeights, Q4Weight, _need_gpu, _stream, lm_head
 
 _GEMMA_EPS = 1e-6
 
@@ -183,6 +185,25 @@ def ffn_fused_bf16(F: FfnWeights, X: torch.Tensor, Y: torch.Tensor | None = None
     return Y
 
 
+def embed(table: torch.Tensor, token_dev: torch.Tensor, scale: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16(float(double(table[token]) * scale)) for the token in device memory
+    (the Gemma-4 lookup with scale sqrt(hidden), runtime/py/model.py:889-891);
+    table is float16 (vocab, H)."""
+    dev = _need_gpu(table)
+    if table.dtype != torch.float16 or table.dim() != 2 or not table.is_contiguous():
+        raise ValueError("table must be a contiguous 2-D float16 tensor")
+    if token_dev.dtype != torch.int32 or token_dev.device != dev:
+        raise ValueError("token_dev must be an int32 tensor on the table's device")
+    vocab, H = table.shape
+    if out is None:
+        out = torch.empty(H, dtype=torch.bfloat16, device=dev)
+    _bf16(out, "out", H)
+    with torch.cuda.device(dev):
+        check(lib().alv_embed(table.data_ptr(), vocab, H, token_dev.data_ptr(), ctypes.c_double(scale), out.data_ptr(),
+                              _stream(table)), "alv_embed")
+    return out
+
+
 def cos_sin_table_gemma(base: float, dim: int, max_seq_len: int, gemma4: bool = True) -> np.ndarray:
     """The reference's RoPE table (precompute_cos_sin_table_gemma,
     runtime/py/model.py:263-280): float32 rows [cos(pos f) | sin(pos f)] in
@@ -210,7 +231,7 @@ class Gemma4DecodeLayer:
     takes and returns bf16 [H] device tensors and updates the KV caches."""
 
     def __init__(self, *, qkv, o, gate, up, down, norms: dict, scale: float, sliding: bool, H: int, I: int,
-                 max_seq: int, device, rope_table=None):
+                 max_seq: int, device, rope_table=None, pos_dev: torch.Tensor | None = None):
         dev = torch.device(device)
         self.sliding, self.H, self.I, self.max_seq, self.device = sliding, H, I, max_seq, dev
         self.heads = 16
@@ -235,7 +256,7 @@ class Gemma4DecodeLayer:
         bf = dict(dtype=torch.bfloat16, device=dev)
         self.kcache = torch.zeros((self.kv_heads, max_seq, self.D), **bf)
         self.vcache = torch.zeros((self.kv_heads, max_seq, self.D), **bf)
-        self.pos_dev = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.pos_dev = torch.zeros(1, dtype=torch.int32, device=dev) if pos_dev is None else pos_dev
         # Intermediates (kept for inspection and for graph capture: fixed addresses).
         self.x_norm = torch.empty(H, **bf)
         self.qkv_out = torch.empty(self.n_qkv, **bf)
@@ -247,10 +268,14 @@ class Gemma4DecodeLayer:
         self.down = torch.empty(H, **bf)
         self.y = torch.empty(H, **bf)
 
-    def enqueue(self, x: torch.Tensor) -> torch.Tensor:
-        """The layer's launches for the position already in ``pos_dev``."""
+    def enqueue(self, x: torch.Tensor, normed: bool = False, next_norm=None) -> torch.Tensor:
+        """The layer's launches for the position already in ``pos_dev``.
+        ``normed``: ``x_norm`` already holds the input norm (written by the
+        previous layer's last launch). ``next_norm`` = (weights, out, pad): the
+        last launch also writes the next norm of the output into ``out``."""
         H, n = self.H, self.norms
-        rmsnorm(x, n["attn"], K=H, out=self.x_norm)
+        if not normed:
+            rmsnorm(x, n["attn"], K=H, out=self.x_norm)
         gemv_bf16(self.w_qkv, self.x_norm, self.qkv_out)
         qkv_post(self.qkv_out, self.pos_dev, self.kcache, self.vcache, heads=self.heads, kv_heads=self.kv_heads,
                  D=self.D, k_off=self.q_size, v_off=self.q_size + self.k_size if self.sliding else -1,
@@ -261,7 +286,12 @@ class Gemma4DecodeLayer:
         add_norm(x, self.attn_proj, K=H, w_y=n["post_attn"], w_out=n["ffn"], norm_out=True, sum_out=self.x_post,
                  norm_buf=self.x_norm2)
         ffn_fused_bf16(self.ffn, self.x_norm2, self.down)
-        add_norm(self.x_post, self.down, K=H, w_y=n["post_ffw"], scale=self.scale, scale_mode=1, sum_out=self.y)
+        if next_norm is None:
+            add_norm(self.x_post, self.down, K=H, w_y=n["post_ffw"], scale=self.scale, scale_mode=1, sum_out=self.y)
+        else:
+            w_next, out_next, pad_next = next_norm
+            add_norm(self.x_post, self.down, K=H, w_y=n["post_ffw"], scale=self.scale, scale_mode=1, sum_out=self.y,
+                     w_out=w_next, norm_out=True, norm_buf=out_next, pad=pad_next)
         return self.y
 
     def forward(self, x: torch.Tensor, pos: int) -> torch.Tensor:
@@ -274,3 +304,77 @@ class Gemma4DecodeLayer:
         self.w_qkv.close()
         self.w_o.close()
         self.ffn.close()
+
+
+class Gemma4Decoder:
+    """A whole Gemma-4 decode step on the device (runtime/py/model.py:889-915):
+    embedding of the token in ``token_dev``, every layer, the final RMSNorm
+    (zero-padded to the head's K), the LM head with the 30 tanh(x / 30)
+    softcap, and the greedy token (np.argmax, runtime/py/sampler.py:9) written
+    back into ``token_dev``; then ``pos_dev`` advances. The next step therefore
+    needs nothing from the host: a captured step replays token after token."""
+
+    def __init__(self, layers: list, embed_table: torch.Tensor, final_norm, head: Q4Weight, vocab: int,
+                 softcap: float = 30.0):
+        self.layers = layers
+        self.device = head.device
+        self.H = layers[0].H
+        self.pos_dev = layers[0].pos_dev
+        for L in layers:
+            if L.pos_dev is not self.pos_dev:
+                raise ValueError("the layers must share one pos_dev")
+        self.table = embed_table
+        self.final_norm = _f32(final_norm, "final_norm", self.H, self.device)
+        self.head, self.vocab, self.softcap = head, vocab, softcap
+        self.scale = math.sqrt(self.H)
+        self.token_dev = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self.x = torch.empty(self.H, dtype=torch.bfloat16, device=self.device)
+        self.x_norm = torch.empty(head.K, dtype=torch.bfloat16, device=self.device)
+        self.x_f32 = torch.empty(head.K, dtype=torch.float32, device=self.device)
+        self.logits = torch.empty(vocab, dtype=torch.float32, device=self.device)
+        # Steps run on the decoder's own stream: the per-stream scratch that
+        # eager steps size is then the scratch a captured step uses.
+        self.stream = torch.cuda.Stream(device=self.device)
+
+    def enqueue(self) -> None:
+        embed(self.table, self.token_dev, self.scale, out=self.x)
+        h = self.x
+        n = len(self.layers)
+        # Each layer's last launch also writes the next layer's input norm (the
+        # final norm, zero-padded to the head's K, after the last layer).
+        for i, L in enumerate(self.layers):
+            nxt = self.layers[i + 1] if i + 1 < n else None
+            next_norm = ((nxt.norms["attn"], nxt.x_norm, self.H) if nxt is not None
+                         else (self.final_norm, self.x_norm, self.head.K))
+            h = L.enqueue(h, normed=i > 0, next_norm=next_norm)
+        if n == 0:
+            rmsnorm(h, self.final_norm, K=self.H, pad=self.head.K, out=self.x_norm)
+        self.x_f32.copy_(self.x_norm)
+        lm_head(self.head, self.x_f32, self.vocab, self.softcap, self.logits, token=self.token_dev)
+        self.pos_dev.add_(1)
+
+    def step(self, token: int | None = None, pos: int | None = None) -> int:
+        """One eager step (from `token` at `pos` when given, else from the
+        device state); returns the greedy next token."""
+        self.stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(self.stream):
+            if token is not None:
+                self.token_dev.fill_(int(token))
+            if pos is not None:
+                self.pos_dev.fill_(int(pos))
+            self.enqueue()
+            tok = int(self.token_dev.item())
+        torch.cuda.current_stream(self.device).wait_stream(self.stream)
+        return tok
+
+    def capture(self) -> torch.cuda.CUDAGraph:
+        """A HIP graph of one step on the decoder's stream (run one eager
+        step first: it sizes the stream's scratch, which cannot grow during
+        capture). Each replay advances the device state by one token; replay
+        it with ``graph.replay()`` under ``torch.cuda.stream(decoder.stream)``
+        or after synchronising."""
+        self.stream.wait_stream(torch.cuda.current_stream(self.device))
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=self.stream):
+            self.enqueue()
+        return g

@@ -398,7 +398,7 @@ def chain_run(ops, M: int = 1) -> None:
 
 
 def lm_head(W: "Q4Weight", x: torch.Tensor, vocab: int | None = None, softcap: float = 30.0,
-            logits: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+            logits: torch.Tensor | None = None, token: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """LM head of a decode step (alv_lm_head): logits[:vocab] =
     softcap * tanh(bf16(W x) / softcap) in float32 (softcap 0: the bf16
     logits) and the greedy token, np.argmax of the logits, as a 1-element
@@ -416,7 +416,10 @@ def lm_head(W: "Q4Weight", x: torch.Tensor, vocab: int | None = None, softcap: f
     if logits.dtype != torch.float32 or not logits.is_contiguous():
         raise TypeError("logits must be a contiguous float32 tensor")
     _too_small("logits", logits.numel(), vocab)
-    token = torch.empty(1, dtype=torch.int32, device=W.device)
+    if token is None:
+        token = torch.empty(1, dtype=torch.int32, device=W.device)
+    if token.dtype != torch.int32 or token.device != W.device:
+        raise TypeError("token must be an int32 tensor on the weights' device")
     with torch.cuda.device(W.device):
         check(lib().alv_lm_head(W.handle, xv.data_ptr(), logits.data_ptr(), vocab, float(softcap),
                                 token.data_ptr(), _stream(xv)), "alv_lm_head")

@@ -24,7 +24,8 @@ import statistics
 import sys
 from collections import defaultdict
 
-Q4_KERNELS = ("q4_gemv1_kernel", "gemm_q4_kernel", "tile_kernel")
+Q4_KERNELS = ("q4_gemv1_kernel", "gemm_q4_kernel", "tile_kernel", "rmsnorm_kernel", "qkv_post_kernel",
+              "attention_kernel", "add_norm_kernel", "embed_kernel", "head_kernel", "head_fold_kernel", "quant_kernel")
 CALIBRATION = "MulFunctor"  # the profile pass's copy: torch.mul(src, 1.0, out=dst)
 
 

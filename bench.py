@@ -33,6 +33,7 @@ import time
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 H, I_FF = 3840, 15360
+VOC, KH = 262144, 4096  # Gemma-4 LM head: vocabulary x padded hidden
 N_QKV, K_O = 8192, 4096
 LAYERS = 48
 
@@ -208,6 +209,74 @@ def profile_pass(torch, aa, dev) -> int:
 
 
 _CAPTURE_STREAM = None
+
+
+def decode_step(torch, aa, dev, nl: int = 48, pos: int = 1500, reps: int = 10) -> dict:
+    """A whole Gemma-4-shaped decode step on the device (alveare_amd.layer):
+    token embedding, nl layers -- every sixth global (q 8192 + k 512 rows,
+    O 3840x8192, one 512-wide kv head), the rest sliding (QKV 8192x3840, O
+    3840x4096, window 1024) -- each with its norms, RoPE, KV-cache insert and
+    attention over `pos` positions of synthetic cache, the FFN 3840<->15360,
+    then the final norm, the 262144x4096 LM head, softcap and greedy token.
+    One HIP graph per token, replayed `reps` times (each replay advances the
+    position)."""
+    import numpy as np
+
+    from alveare_amd import layer
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0xA1E00700)
+    rng = np.random.default_rng(0xA1E00700)
+    pos_dev = torch.zeros(1, dtype=torch.int32, device=dev)
+    tables = {s: layer.cos_sin_table_gemma(1e4 if s else 1e6, 256 if s else 512, 2048) for s in (True, False)}
+    layers, wbytes = [], 0
+    for l in range(nl):
+        sliding = (l + 1) % 6 != 0
+        D = 256 if sliding else 512
+        n_qkv = 8192 if sliding else 8192 + 512
+        q_size = 16 * D
+        norms = {k: rng.uniform(0.5, 1.5, D if k in ("q", "k") else H).astype(np.float32)
+                 for k in ("attn", "q", "k", "post_attn", "ffn", "post_ffw")}
+        L = layer.Gemma4DecodeLayer(qkv=synth_q4_dev(torch, n_qkv, H, gen, dev), o=synth_q4_dev(torch, H, q_size, gen, dev),
+                                    gate=synth_q4_dev(torch, I_FF, H, gen, dev), up=synth_q4_dev(torch, I_FF, H, gen, dev),
+                                    down=synth_q4_dev(torch, H, I_FF, gen, dev), norms=norms, scale=0.9, sliding=sliding,
+                                    H=H, I=I_FF, max_seq=2048, device=dev, rope_table=tables[sliding], pos_dev=pos_dev)
+        L.kcache.normal_(generator=gen)
+        L.vcache.normal_(generator=gen)
+        layers.append(L)
+        wbytes += q4_bytes(n_qkv, H) + q4_bytes(H, q_size) + 3 * q4_bytes(I_FF, H)
+        torch.cuda.empty_cache()
+    head = aa.Q4Weight(synth_q4_dev(torch, VOC, KH, gen, dev), VOC, KH)
+    wbytes += q4_bytes(VOC, KH)
+    table = (torch.randn(VOC, H, device=dev, generator=gen) * 0.05).half()
+    dec = layer.Gemma4Decoder(layers, table, np.ones(H, np.float32), head, VOC, softcap=30.0)
+    torch.cuda.empty_cache()
+    dec.step(token=1, pos=pos)  # eager step: sizes the decoder stream's scratch
+    torch.cuda.synchronize()
+    g = dec.capture()
+    dec.token_dev.fill_(1)
+    pos_dev.fill_(pos)
+    with torch.cuda.stream(dec.stream):
+        for _ in range(2):
+            g.replay()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            g.replay()
+        b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / reps
+    end_pos = int(pos_dev.item())
+    del g
+    for L in layers:
+        L.close()
+    head.close()
+    del layers, dec, table
+    torch.cuda.empty_cache()
+    return {"us_per_token": round(us, 1), "tokens_per_s": round(1e6 / us, 1), "layers": nl, "context_pos": pos,
+            "end_pos": end_pos, "weight_GB_per_token": round(wbytes / 1e9, 3), "GBps_weights": round(wbytes / us / 1e3, 1),
+            "note": "embedding, 48 layers with attention over the cache, final norm, LM head, softcap and argmax; "
+                    "one HIP graph per token, device-resident token and position"}
 
 
 def read_floor(torch, aa, dev) -> dict:
@@ -432,7 +501,6 @@ def main() -> int:
 
         # LM head: the reference's 262144 x 4096 Q4 head (671 MB, beyond the
         # Infinity Cache), GEMV + softcap 30 + greedy argmax per call.
-        VOC, KH = 262144, 4096
         gen = torch.Generator(device=dev)
         gen.manual_seed(0xA1E00600)
         head = aa.Q4Weight(synth_q4_dev(torch, VOC, KH, gen, dev), VOC, KH)
@@ -465,6 +533,8 @@ def main() -> int:
         extra["quantize_262144x3840_to_4096"] = {"us": round(us, 1), "GBps": round(qb / us / 1e3, 1)}
         del wq, qout
         torch.cuda.empty_cache()
+
+        extra["decode_step_gemma4_48l"] = decode_step(torch, aa, dev)
 
     from alveare_amd import profiling
 

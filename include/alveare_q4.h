@@ -281,9 +281,10 @@ int alv_qkv_post(const uint16_t* qkv, int k_off, int v_off, int heads, int kv_he
  * out[h] = softmax(scale * K q[h]) V over cache positions [start, pos] of kv
  * head h / (heads / kv_heads), start = pos + 1 - window for a sliding layer
  * (window > 0), else 0; float32 scores and softmax, bf16 out [heads][D].
- * run_attention_host (runtime/py/model.py:577-628; model.cpp:185-262). D a
- * multiple of 32 up to 512, at most 16 q heads per kv head; kcache 16-byte
- * aligned. Uses per-stream scratch (grown outside graph capture).
+ * run_attention_host (runtime/py/model.py:577-628; model.cpp:185-262). D one
+ * of 64, 128, 256, 512; q, kcache and vcache 16-byte aligned; at most 65536
+ * positions in the window. Two launches (chunk partials, then their merge);
+ * uses per-stream scratch (grown outside graph capture).
  */
 int alv_attention(const uint16_t* q, const uint16_t* kcache, const uint16_t* vcache, uint16_t* out, int heads,
                   int kv_heads, int D, int max_seq, int window, float scale, const int* pos_dev, void* stream);
@@ -299,6 +300,16 @@ int alv_attention(const uint16_t* q, const uint16_t* kcache, const uint16_t* vca
 int alv_add_norm(const uint16_t* resid, int ldr, const uint16_t* y, int ldy, const float* w_y, int norm_y,
                  float scale, int scale_mode, uint16_t* sum_out, int ld_sum, const float* w_out, uint16_t* norm_out,
                  int ld_norm, int rows, int K, int pad, float eps, void* stream);
+
+/*
+ * out[:H] = bf16(float(double(table_f16[*token_dev]) * scale)), the Gemma-4
+ * embedding lookup with scale = sqrt(hidden_size) (runtime/py/model.py:889-891:
+ * a float64 product cast to bf16 through float32). The token is read from
+ * device memory (the previous step's argmax); a token outside [0, vocab)
+ * writes zeros.
+ */
+int alv_embed(const uint16_t* table_f16, int vocab, int H, const int32_t* token_dev, double scale, uint16_t* out,
+              void* stream);
 
 /*
  * One op of a chain: a registered projection (y = W x) or a registered FFN

@@ -279,3 +279,75 @@ def test_gemma4_layer_stagewise(orc, dev, sliding):
         y_ref = qn.bf16_rne(qn.bf16_rne(x_post + qn.rmsnorm_cpu(g["down"], norms["post_ffw"])) * scale)
         assert np.array_equal(bf_np(y), y_ref)
     L.close()
+
+
+# ---- a whole decode step on the device (model.py:889-915) ---------------------------
+
+def test_gemma4_decoder_step_and_graph(orc, dev):
+    """Embedding, two layers (sliding, global), final norm, head and greedy
+    token entirely on the device: the embedding and final norm bit-exact, the
+    head's bf16 logits within the GEMV bound, the token their np.argmax; a
+    captured step replayed from the same state gives the eager steps' logits
+    and tokens bit for bit."""
+    import math
+
+    import alveare_amd as aa
+    from alveare_amd import layer
+
+    H, I, S, V = 512, 1024, 32, 1000
+    rng = np.random.default_rng(400)
+    pos_dev = torch.zeros(1, dtype=torch.int32, device=dev)
+    layers = []
+    for sliding in (True, False):
+        D, kv = (256, 8) if sliding else (512, 1)
+        n_qkv = 16 * D + (2 if sliding else 1) * kv * D
+        norms = {k: rng.uniform(0.5, 1.5, D if k in ("q", "k") else H).astype(np.float32)
+                 for k in ("attn", "q", "k", "post_attn", "ffn", "post_ffw")}
+        layers.append(layer.Gemma4DecodeLayer(
+            qkv=orc.synth_q4(n_qkv, H, 401 + sliding), o=orc.synth_q4(H, 16 * D, 403 + sliding),
+            gate=orc.synth_q4(I, H, 405), up=orc.synth_q4(I, H, 406), down=orc.synth_q4(H, I, 407), norms=norms,
+            scale=0.7, sliding=sliding, H=H, I=I, max_seq=S, device=dev, pos_dev=pos_dev))
+    table_np = rng.normal(0, 0.05, (V, H)).astype(np.float16)
+    fnorm = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    Wh = orc.synth_q4(V, H, 408)
+    head = aa.Q4Weight(torch.from_numpy(Wh).to(dev), V, H)
+    dec = layer.Gemma4Decoder(layers, torch.from_numpy(table_np).to(dev), fnorm, head, V, softcap=0.0)
+
+    def reset():
+        torch.cuda.synchronize()
+        for L in layers:
+            L.kcache.zero_()
+            L.vcache.zero_()
+        dec.token_dev.fill_(7)
+        pos_dev.fill_(0)
+        torch.cuda.synchronize()
+
+    reset()
+    eager = []
+    for step in range(4):
+        _say(f"decoder eager step {step}")
+        tok_in = int(dec.token_dev.item())
+        tok = dec.step()
+        torch.cuda.synchronize()
+        x = (table_np[tok_in].astype(np.float32) * np.sqrt(H)).astype(np.float32)
+        assert np.array_equal(bf_np(dec.x), qn.bf16_rne(x))
+        xn = bf_np(dec.x_norm)
+        assert np.array_equal(xn[:H], qn.rmsnorm_cpu(bf_np(layers[-1].y), fnorm))
+        logits = dec.logits.cpu().numpy()
+        parity.gemv_bf16_check(orc, Wh, xn, parity.f32_bits_bf16(logits), V, H)
+        assert tok == int(np.argmax(logits))
+        eager.append((logits.copy(), tok))
+    reset()
+    g = dec.capture()
+    reset()
+    for step in range(4):
+        _say(f"decoder graph replay {step}")
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(dec.logits.cpu().numpy(), eager[step][0])
+        assert int(dec.token_dev.item()) == eager[step][1]
+        assert int(pos_dev.item()) == step + 1
+    del g
+    for L in layers:
+        L.close()
+    head.close()
