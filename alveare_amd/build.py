@@ -16,9 +16,16 @@ import subprocess
 import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libalveare_q4.so")
+# The reference runtime's C++ registry interface over LIB (alveare::NpuRegistry)
+# and the program that drives it in the tests.
+NPU_SRC = os.path.join(HERE, "cpp", "npu_registry.cpp")
+NPU_LIB = os.path.join(HERE, "libalveare_npu.so")
+CHECK_SRC = os.path.join(ROOT, "tests", "cpp", "npu_registry_check.cpp")
+CHECK_BIN = os.path.join(HERE, "npu_registry_check")
 ARCH = os.environ.get("ALV_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -67,7 +74,34 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    build_adapter(verbose)
     return LIB
+
+
+def _run(cmd: list[str], what: str) -> None:
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"{what} failed:\n{r.stderr}")
+
+
+def build_adapter(verbose: bool = True) -> str:
+    """libalveare_npu.so (alveare::NpuRegistry over libalveare_q4.so) and, when
+    the tests are present, the program that drives it."""
+    # Host code only (the HIP runtime API, no kernels): the system C++ compiler.
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    cxx = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-Wall", "-D__HIP_PLATFORM_AMD__",
+           "-I", os.path.join(HERE, "cpp"), "-I", os.path.join(ROOT, "include"), "-I", os.path.join(rocm, "include")]
+    link = ["-L", HERE, "-L", os.path.join(rocm, "lib"), "-Wl,-rpath,$ORIGIN", "-Wl,-rpath," + os.path.join(rocm, "lib")]
+    tmp = NPU_LIB + ".tmp"
+    _run([*cxx, "-fPIC", "-shared", NPU_SRC, "-o", tmp, *link, "-lalveare_q4", "-lamdhip64"], "adapter build")
+    os.replace(tmp, NPU_LIB)
+    if os.path.exists(CHECK_SRC):
+        tmp = CHECK_BIN + ".tmp"
+        _run([*cxx, CHECK_SRC, "-o", tmp, *link, "-lalveare_npu", "-lalveare_q4", "-lamdhip64"], "adapter check build")
+        os.replace(tmp, CHECK_BIN)
+    if verbose:
+        print(f"built {NPU_LIB}")
+    return NPU_LIB
 
 
 if __name__ == "__main__":

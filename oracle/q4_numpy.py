@@ -236,3 +236,59 @@ def gemma4_decode_layer(x: np.ndarray, pos: int, sliding: bool, w: dict, qkv_pro
     y = bf16_rne(x_post + down_normed)
     st["y"] = y = bf16_rne(y * np.float32(w["scale"]))
     return y
+
+
+def pack_ffn_fused_weights_ref(w_gate: np.ndarray, w_up: np.ndarray, w_down: np.ndarray, H: int, I: int,
+                               m_I: int = 32, k_tile: int = 256) -> np.ndarray:
+    """The reference's registration-time FFN packing
+    (runtime/cpp/src/weights.cpp:94-190), restated: per NPU core, gate and up
+    tiles of m_I rows x k_tile columns for every I-block, then four passes of
+    down tiles of k_tile rows x m_I columns; cores concatenated (<= 8) or
+    interleaved tile by tile per column of 8 (16 or 32 cores). Produces the
+    blob NpuRegistry::create_ffn_fused_weight receives."""
+    m_H = k_tile
+    n_cores = 1
+    for c in (32, 16, 8, 4, 2):
+        if I % (c * m_I) == 0:
+            n_cores = c
+            break
+    I_div = I // n_cores
+    nb_I = I_div // m_I
+    cpg = k_tile // 32
+    gs, ds = H // 32 * 20, I // 32 * 20
+    g = np.asarray(w_gate, np.uint8).reshape(-1)
+    u = np.asarray(w_up, np.uint8).reshape(-1)
+    d = np.asarray(w_down, np.uint8).reshape(-1)
+    tile = m_I * cpg * 20
+    n_passes = 4
+    dtpp = (H // m_H) // n_passes
+    per_core = []
+    for c in range(n_cores):
+        parts = []
+        start_I = c * I_div
+
+        def tile_rows(w, r0, r1, b0, b1, stride):
+            for r in range(r0, r1):
+                parts.append(w[r * stride + b0:r * stride + b1])
+
+        for b in range(nb_I):
+            r0 = start_I + b * m_I
+            for hb in range(H // k_tile):
+                tile_rows(g, r0, r0 + m_I, hb * cpg * 20, (hb + 1) * cpg * 20, gs)
+                tile_rows(u, r0, r0 + m_I, hb * cpg * 20, (hb + 1) * cpg * 20, gs)
+        for p in range(n_passes):
+            for b in range(nb_I):
+                c0 = (start_I // 32) * 20 + b * (m_I // 32) * 20
+                for hd in range(p * dtpp, (p + 1) * dtpp):
+                    tile_rows(d, hd * m_H, (hd + 1) * m_H, c0, c0 + (m_I // 32) * 20, ds)
+        per_core.append(np.concatenate(parts))
+    if n_cores in (16, 32):
+        rows_per_col = n_cores // 8
+        n_tiles = len(per_core[0]) // tile
+        out = []
+        for col in range(8):
+            for t in range(n_tiles):
+                for r in range(rows_per_col):
+                    out.append(per_core[rows_per_col * col + r][t * tile:(t + 1) * tile])
+        return np.concatenate(out)
+    return np.concatenate(per_core)
