@@ -125,6 +125,20 @@ int get_scratch(hipStream_t s, int slot, size_t bytes, void** out) {
     return ALV_OK;
 }
 
+int small_wg_per_cu() {
+    const char* e = getenv("ALV_GEMM_SMALL_WG_PER_CU");
+    if (!e || !*e) return 1;
+    const long v = strtol(e, nullptr, 10);
+    return v >= 1 && v <= 16 ? (int)v : 1;
+}
+
+int small_tile_max_m() {
+    const char* e = getenv("ALV_GEMM_SMALL_TILE_MAX_M");
+    if (!e || !*e) return kSmallTileMaxM;
+    const long v = strtol(e, nullptr, 10);
+    return v >= 0 && v <= (1 << 30) ? (int)v : kSmallTileMaxM;
+}
+
 int tiled_min_m() {
     const char* e = getenv("ALV_TILED_MIN_M");
     if (!e || !*e) return kTiledMinM;

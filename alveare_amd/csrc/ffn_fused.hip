@@ -12,7 +12,7 @@
 //   2. down = Wd * a, with a single bf16 term per activation value (it is
 //      bf16 by construction), summed entirely on the device -- the reference
 //      sums per-core partials on the host (runtime/cpp/src/npu.cpp:360-377).
-// Prefill (M >= 64): the same two steps with the MFMA tiled kernel (gemm_q.hip);
+// Prefill (M >= 32): the same two steps with the MFMA tiled kernel (gemm_q.hip);
 // the M x I activation lives in the stream's prefill scratch (q4_host.h).
 #include <string.h>
 

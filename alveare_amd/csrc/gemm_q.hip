@@ -1,26 +1,31 @@
-// MFMA Q4 GEMM for prefill-sized batches (gfx950): the M >= 64 path of
+// MFMA Q4 GEMM for prefill-sized batches (gfx950): the M >= 32 path of
 // alv_gemm_q, alv_gemv and alv_ffn_fused (gate/up with the GLU epilogue, then
 // down).
 //
 // C[M, N] = X[M, K] * dequant(W)[N, K]^T. A workgroup of 8 waves owns a
-// 256-token x 128-weight-row tile and walks K 64 at a time (two Q4 blocks per
-// row):
+// TM-token x 128-weight-row tile -- TM = 256, or 64 up to 128 tokens (a
+// quarter of the MFMA and LDS work per weight tile; measured 1.6-1.8x faster
+// at M <= 128) -- and walks K 64 at a time (two Q4 blocks per row):
 //   * the 128 x 64 weight tile is dequantized once into LDS as bf16
-//     (q4_device.h::dequant8_mix, exact), shared by 256 tokens;
-//   * the 256 x 64 activation tile goes into LDS as bf16. fp32 activations
+//     (q4_device.h::dequant8_mix, exact), shared by the TM tokens; with
+//     64-token tiles this dequantization is most of the VALU work (SQ
+//     counters: about 128 VALU instructions per wave and step against 16
+//     MFMAs), so the streaming kernel stays faster below 32 tokens;
+//   * the TM x 64 activation tile goes into LDS as bf16. fp32 activations
 //     are split exactly into up to three bf16 terms (x = t0 + t1 + t2,
 //     q4_device.h::split3), one pass over K per term: the first pass stages
 //     t0 and notes whether any activation of the token tile has bits below
 //     bf16 precision; only then do passes for t1 and t2 follow. Activations
 //     that are already bf16-valued -- the reference's callers pass bf16
 //     (runtime/py/model.py:399-485) -- cost one pass;
-//   * each wave computes a 64 x 64 sub-tile with v_mfma_f32_16x16x32_bf16
-//     (fp32 accumulation);
-//   * the global loads of step k + 2 are issued before the MFMAs of step k
-//     (two register stages for bf16 activations, one for fp32) and land in
-//     the other half of a double-buffered LDS, so one barrier per step
-//     separates them; the dequantization of step k + 1 sits between the two
-//     k-halves of step k's MFMAs;
+//   * each wave computes a 64-token x (64, or 16 for TM = 64) row sub-tile
+//     with v_mfma_f32_16x16x32_bf16 (fp32 accumulation);
+//   * the global loads of step k + S are issued before the MFMAs of step k
+//     (S = 2 register stages for 256-token tiles, 4 for 64-token ones; one
+//     stage for fp32 activations split in the kernel) and land in the other
+//     half of a double-buffered LDS, so one barrier per step separates them;
+//     the dequantization of step k + 1 sits between the two k-halves of step
+//     k's MFMAs;
 //   * fp32 activations are first split into three bf16 term arrays by
 //     split_x_kernel (half the bytes per re-read, the token tile fits the
 //     L2), with a per-token flag for the second and third terms;
@@ -47,14 +52,26 @@ namespace alv {
 
 namespace {
 
-constexpr int TM = 256;  // tokens per tile
 constexpr int TN = 128;  // weight rows per tile
 constexpr int TK = 64;   // k per step (two Q4 blocks)
 constexpr int KP = TK / 8;    // octet planes per step
 constexpr int kGemmThreads = 512;
 
+// Token tile TM (256, or 64 for small batches): the 8 waves form a
+// (TM / 64) x (8 / (TM / 64)) grid over (tokens, weight rows); each wave
+// computes 64 tokens x (TN / waves across rows) rows per matrix.
+template <int TM>
+struct GemmTile {
+    static constexpr int WAVES_M = TM / 64;
+    static constexpr int WAVES_N = 8 / WAVES_M;
+    static constexpr int WN = TN / WAVES_N;   // weight rows per wave
+    static constexpr int JJ = WN / 16;        // 16-row blocks per wave
+    static constexpr int XI = TM / 64;        // activation loads per thread (64 tokens per pass)
+};
+
 // bf16 offset of 16-byte slot `row` of plane p in a tile of `rows` rows.
 __device__ __forceinline__ size_t wslot(int p, int row) { return ((size_t)p * TN + row) * 8; }
+template <int TM>
 __device__ __forceinline__ size_t xslot(int p, int token) { return ((size_t)p * TM + (token ^ (2 * p))) * 8; }
 
 struct GemmArgs {
@@ -78,8 +95,10 @@ struct GemmArgs {
     uint32_t* cnt;
 };
 
-template <int NT, bool TILED, bool XF32>
+template <int NT, bool TILED, bool XF32, int TM>
 __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
+    using G = GemmTile<TM>;
+    constexpr int JJ = G::JJ, XI = G::XI;
     extern __shared__ __align__(16) unsigned char smem[];
     // [buffer][matrix][plane][row] weights, then [buffer][plane][token] activations.
     __bf16* wsm = reinterpret_cast<__bf16*>(smem);
@@ -88,7 +107,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 waves of 64 x 64
+    const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
     const int m0 = blockIdx.x * TM;
     const int n0 = blockIdx.y * TN;
     const int nsteps_all = (a.K + TK - 1) / TK;
@@ -117,27 +136,26 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
     const uint32_t wv = wstage && wrow < a.N ? (TILED ? (uint32_t)(wrow >> 4) * a.tg.rtb + (uint32_t)(wrow & 15) * 16u
                                                       : (uint32_t)wrow * rs)
                                              : a.wbytes;
-    uint32_t xv[4];
+    uint32_t xv[XI];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < XI; ++i) {
         const int m = m0 + (tid >> 3) + 64 * i;
         xv[i] = m < a.M ? (uint32_t)(((size_t)m * a.ldx + (tid & 7) * 8) * (XF32 ? 4 : 2)) : a.xbytes;
     }
 
-    f32x4 acc[NT][4][4];
+    f32x4 acc[NT][4][JJ];
 #pragma unroll
     for (int n = 0; n < NT; ++n)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) acc[n][i][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int jj = 0; jj < JJ; ++jj) acc[n][i][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     constexpr int XV = XF32 ? 2 : 1;  // 16-byte loads per 8 activations
-    // Two register stages (bf16 activations): the loads of step s + 2 are
-    // issued while step s is computed from LDS and step s + 1 waits in the
-    // other stage.
-    uint32_t wreg0[5], wreg1[5];
-    u32x4 xreg0[4][XV], xreg1[4][XV];
+    // One register stage for fp32 activations (twice the registers per
+    // stage); bf16 activations keep S stages (below).
+    uint32_t wreg0[5];
+    u32x4 xreg0[XI][XV];
     uint32_t lowbits = 0;  // OR of all fp32 activation bits seen by the first pass
 
     // Global loads of step s (absolute) of activation term p into registers.
@@ -146,7 +164,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
     // path -- past the last step (in = false) the loads read past the buffers
     // and return zeros -- so the compiler's wait counts stay exact and a wait
     // for one register stage never drains the other.
-    auto load = [&](int s, bool in, int p, uint32_t (&wreg)[5], u32x4 (&xreg)[4][XV]) __attribute__((always_inline)) {
+    auto load = [&](int s, bool in, int p, uint32_t (&wreg)[5], u32x4 (&xreg)[XI][XV]) __attribute__((always_inline)) {
         const int kb = s * 2 + wb;
         const bool ok = in && kb < (a.K >> 5);
 #pragma unroll
@@ -168,7 +186,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
         const uint32_t xo = __builtin_amdgcn_readfirstlane(
             in ? (uint32_t)(((size_t)s * TK + (XF32 ? 0 : (size_t)p * a.tstride)) * (XF32 ? 4 : 2)) : a.xbytes);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < XI; ++i)
 #pragma unroll
             for (int v = 0; v < XV; ++v)
                 xreg[i][v] = __builtin_amdgcn_raw_buffer_load_b128(rx, xv[i] + 16 * v, xo, 0);
@@ -182,11 +200,11 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
             for (int t = 0; t < 4; ++t) *reinterpret_cast<bf16x8*>(tile + wslot(4 * wb + t, wr)) = dequant8_mix(wreg[t], sc);
         }
     };
-    auto store_x = [&](int b, int p, const u32x4 (&xreg)[4][XV]) __attribute__((always_inline)) {
+    auto store_x = [&](int b, int p, const u32x4 (&xreg)[XI][XV]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < XI; ++i) {
             const int r = (tid >> 3) + 64 * i, o = tid & 7;
-            u32x4* dst = reinterpret_cast<u32x4*>(xsm + (size_t)b * KP * TM * 8 + xslot(o, r));
+            u32x4* dst = reinterpret_cast<u32x4*>(xsm + (size_t)b * KP * TM * 8 + xslot<TM>(o, r));
             if constexpr (XF32) {
                 bf16x8 t;
 #pragma unroll
@@ -207,7 +225,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
             }
         }
     };
-    auto store = [&](int b, int p, const uint32_t (&wreg)[5], const u32x4 (&xreg)[4][XV]) __attribute__((always_inline)) {
+    auto store = [&](int b, int p, const uint32_t (&wreg)[5], const u32x4 (&xreg)[XI][XV]) __attribute__((always_inline)) {
         store_w(b, wreg);
         store_x(b, p, xreg);
     };
@@ -220,21 +238,21 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
     }
     auto compute_kk = [&](int b, int kk) __attribute__((always_inline)) {
         {
-            bf16x8 bv[NT][4];
+            bf16x8 bv[NT][JJ];
 #pragma unroll
             for (int n = 0; n < NT; ++n)
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj)
+                for (int jj = 0; jj < JJ; ++jj)
                     bv[n][jj] = *reinterpret_cast<const bf16x8*>(
-                        wsm + (size_t)(b * NT + n) * KP * TN * 8 + wslot(kk * 4 + g, wn * 64 + jj * 16 + j));
+                        wsm + (size_t)(b * NT + n) * KP * TN * 8 + wslot(kk * 4 + g, wn * G::WN + jj * 16 + j));
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const bf16x8 av = *reinterpret_cast<const bf16x8*>(
-                    xsm + (size_t)b * KP * TM * 8 + xslot(kk * 4 + g, wm * 64 + i * 16 + j));
+                    xsm + (size_t)b * KP * TM * 8 + xslot<TM>(kk * 4 + g, wm * 64 + i * 16 + j));
 #pragma unroll
                 for (int n = 0; n < NT; ++n)
 #pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) acc[n][i][jj] = mfma16x16x32(av, bv[n][jj], acc[n][i][jj]);
+                    for (int jj = 0; jj < JJ; ++jj) acc[n][i][jj] = mfma16x16x32(av, bv[n][jj], acc[n][i][jj]);
             }
         }
     };
@@ -257,29 +275,33 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
                 __syncthreads();
             }
         } else {
-            load(st0, true, p, wreg0, xreg0);
-            load(st0 + 1, nsteps > 1, p, wreg1, xreg1);
-            store(0, p, wreg0, xreg0);
+            // S register stages: stage t % S holds step t from its load (issued
+            // S steps ahead) until its store into LDS buffer t & 1 during step
+            // t - 1; then it is reloaded with step t + S. Step t computes
+            // buffer t & 1 while the dequantization and activation stores of
+            // step t + 1 sit between its two k halves, so VALU and matrix work
+            // of one wave overlap. 64-token tiles take short steps and need
+            // the deeper prefetch to cover the loads' latency.
+            constexpr int S = TM == 64 ? 4 : 2;
+            uint32_t wst[S][5];
+            u32x4 xst[S][XI][XV];
+#pragma unroll
+            for (int q = 0; q < S; ++q) load(st0 + q, q < nsteps, p, wst[q], xst[q]);
+            store(0, p, wst[0], xst[0]);
             __syncthreads();
-            // Steps in pairs: even steps compute LDS buffer 0 (stage 1 holds
-            // the next step), odd steps buffer 1 (stage 0 holds the next).
-            // The dequantization and activation stores of the next step sit
-            // between the two k halves of this step's MFMAs, so VALU and matrix
-            // work of one wave overlap.
-            for (int s = 0; s < nsteps; s += 2) {
-                load(st0 + s + 2, s + 2 < nsteps, p, wreg0, xreg0);
-                compute_kk(0, 0);
-                if (s + 1 < nsteps) store_w(1, wreg1);
-                compute_kk(0, 1);
-                if (s + 1 < nsteps) store_x(1, p, xreg1);
-                __syncthreads();
-                if (s + 1 >= nsteps) break;
-                load(st0 + s + 3, s + 3 < nsteps, p, wreg1, xreg1);
-                compute_kk(1, 0);
-                if (s + 2 < nsteps) store_w(0, wreg0);
-                compute_kk(1, 1);
-                if (s + 2 < nsteps) store_x(0, p, xreg0);
-                __syncthreads();
+            for (int s = 0; s < nsteps; s += S) {
+#pragma unroll
+                for (int q = 0; q < S; ++q) {
+                    const int t = s + q;
+                    if (t >= nsteps) break;
+                    const int b = q & 1;
+                    load(st0 + t + S, t + S < nsteps, p, wst[q], xst[q]);
+                    compute_kk(b, 0);
+                    if (t + 1 < nsteps) store_w(b ^ 1, wst[(q + 1) % S]);
+                    compute_kk(b, 1);
+                    if (t + 1 < nsteps) store_x(b ^ 1, p, xst[(q + 1) % S]);
+                    __syncthreads();
+                }
             }
         }
         // After the first pass: residual terms only for a token tile with
@@ -303,14 +325,14 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
         const size_t tsz = (size_t)NT * TM * TN;
         const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.part + tile * a.ks * tsz, (uint32_t)(a.ks * tsz * sizeof(float)));
         auto piece = [&](int q, int n, int i, int jj) -> uint32_t {
-            return (uint32_t)(((((size_t)q * NT + n) * 16 + 4 * i + jj) * kGemmThreads + tid) * 16);
+            return (uint32_t)(((((size_t)q * NT + n) * 4 * JJ + JJ * i + jj) * kGemmThreads + tid) * 16);
         };
 #pragma unroll
         for (int n = 0; n < NT; ++n)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj)
+                for (int jj = 0; jj < JJ; ++jj)
                     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[n][i][jj]), rp,
                                                            piece(kq, n, i, jj), 0, 16);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -326,14 +348,14 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj) acc[n][i][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int jj = 0; jj < JJ; ++jj) acc[n][i][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
         for (int q = 0; q < a.ks; ++q)
 #pragma unroll
             for (int n = 0; n < NT; ++n)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
 #pragma unroll
-                    for (int jj = 0; jj < 4; ++jj)
+                    for (int jj = 0; jj < JJ; ++jj)
                         acc[n][i][jj] += __builtin_bit_cast(f32x4, buf_load16_sc1(rp, piece(q, n, i, jj)));
         if (tid == 0) __hip_atomic_store(&a.cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -351,23 +373,23 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
         // and are finished one at a time on the float64 path, so the unrolled
         // code stays small and the accumulators stay in registers.
         __syncthreads();
-        uint32_t* stash = reinterpret_cast<uint32_t*>(smem) + (size_t)tid * 64;
+        uint32_t* stash = reinterpret_cast<uint32_t*>(smem) + (size_t)tid * (16 * JJ);
         uint64_t miss = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj)
+            for (int jj = 0; jj < JJ; ++jj)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int m = m0 + wm * 64 + i * 16 + 4 * g + r;
-                    const int n = n0 + wn * 64 + jj * 16 + j;
+                    const int n = n0 + wn * G::WN + jj * 16 + j;
                     if (m >= a.M || n >= a.N) continue;
                     const float gb = bf16_round(acc[0][i][jj][r]), ub = bf16_round(acc[1][i][jj][r]);
                     float v;
                     if (glu_fast(gb, ub, a.act, &v)) {
                         put(m, n, bf16_round(v));
                     } else {
-                        const int e = (i * 4 + jj) * 4 + r;
+                        const int e = (i * JJ + jj) * 4 + r;
                         miss |= 1ull << e;
                         stash[e] = (__builtin_bit_cast(uint32_t, gb) >> 16) | (__builtin_bit_cast(uint32_t, ub) & 0xFFFF0000u);
                     }
@@ -377,19 +399,19 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
             miss &= miss - 1;
             const uint32_t pk = stash[e];
             const float gb = __builtin_bit_cast(float, pk << 16), ub = __builtin_bit_cast(float, pk & 0xFFFF0000u);
-            const int i = e >> 4, jj = (e >> 2) & 3, r = e & 3;
-            put(m0 + wm * 64 + i * 16 + 4 * g + r, n0 + wn * 64 + jj * 16 + j, bf16_round(glu_exact(gb, ub, a.act)));
+            const int i = (e >> 2) / JJ, jj = (e >> 2) % JJ, r = e & 3;
+            put(m0 + wm * 64 + i * 16 + 4 * g + r, n0 + wn * G::WN + jj * 16 + j, bf16_round(glu_exact(gb, ub, a.act)));
         }
         return;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
+        for (int jj = 0; jj < JJ; ++jj)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + wm * 64 + i * 16 + 4 * g + r;
-                const int n = n0 + wn * 64 + jj * 16 + j;
+                const int n = n0 + wn * G::WN + jj * 16 + j;
                 if (m >= a.M || n >= a.N) continue;
                 put(m, n, acc[0][i][jj][r]);
             }
@@ -417,14 +439,14 @@ __global__ void __launch_bounds__(256) split_x_kernel(const float* X, int ldx, i
     if (threadIdx.x == 0) flags[m] = more ? 1u : 0u;
 }
 
-template <int NT, bool TILED, bool XF32>
+template <int NT, bool TILED, bool XF32, int TM>
 hipError_t launch_gemm(const GemmArgs& a, dim3 grid, hipStream_t s) {
     const size_t lds = (size_t)2 * KP * (NT * TN + TM) * 8 * sizeof(uint16_t);
     static bool attr[64] = {};
     int dev = 0;
     if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
     if (dev >= 64 || !attr[dev]) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_q4_kernel<NT, TILED, XF32>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_q4_kernel<NT, TILED, XF32, TM>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) {
             (void)hipGetLastError();
@@ -432,13 +454,15 @@ hipError_t launch_gemm(const GemmArgs& a, dim3 grid, hipStream_t s) {
         }
         if (dev < 64) attr[dev] = true;
     }
-    hipLaunchKernelGGL((gemm_q4_kernel<NT, TILED, XF32>), grid, dim3(kGemmThreads), lds, s, a);
+    hipLaunchKernelGGL((gemm_q4_kernel<NT, TILED, XF32, TM>), grid, dim3(kGemmThreads), lds, s, a);
     return hipGetLastError();
 }
 
 template <int NT, bool TILED>
-hipError_t launch_gemm_x(const GemmArgs& a, bool xf32, dim3 grid, hipStream_t s) {
-    return xf32 ? launch_gemm<NT, TILED, true>(a, grid, s) : launch_gemm<NT, TILED, false>(a, grid, s);
+hipError_t launch_gemm_x(const GemmArgs& a, bool xf32, int tm, dim3 grid, hipStream_t s) {
+    if (tm == 64)
+        return xf32 ? launch_gemm<NT, TILED, true, 64>(a, grid, s) : launch_gemm<NT, TILED, false, 64>(a, grid, s);
+    return xf32 ? launch_gemm<NT, TILED, true, 256>(a, grid, s) : launch_gemm<NT, TILED, false, 256>(a, grid, s);
 }
 
 }  // namespace
@@ -473,13 +497,20 @@ int launch_gemm_tiled(const GemvLaunch& L, hipStream_t s) {
     uint64_t xbytes = ((uint64_t)(L.M - 1) * L.ldx + L.K) * (xf32 ? 4 : 2);
     if (xbytes >= 0x7FFFFF00ull) return fail(ALV_ERR_RANGE, "activations of %llu bytes exceed the 2 GiB buffer range", (unsigned long long)xbytes);
     const int NT = L.glu ? 2 : 1;
+    // Token tile: 64 for small batches (a quarter of the MFMA and LDS work per
+    // weight tile of the 256-token tile), 256 above small_tile_max_m().
+    const int TM = L.M <= small_tile_max_m() ? 64 : 256;
     const dim3 tiles((L.M + TM - 1) / TM, (L.N + TN - 1) / TN);
     const int ntiles = (int)(tiles.x * tiles.y);
-    // Split K while the grid leaves half the CUs idle and each split keeps at
-    // least 16 steps.
+    // Split K while the grid leaves CUs idle and each split keeps enough
+    // steps: 256-token tiles aim at one workgroup per CU (16+ steps each);
+    // 64-token tiles at ALV_GEMM_SMALL_WG_PER_CU workgroups per CU (default
+    // 1; 2-4 measured no faster) with 8+ steps each.
     const int nsteps = (L.K + TK - 1) / TK;
     int ks = 1;
-    while (ntiles * ks * 2 <= device_cus() && nsteps / (ks * 2) >= 16) ks *= 2;
+    const int wg_target = TM == 64 ? small_wg_per_cu() * device_cus() : device_cus();
+    const int min_steps = TM == 64 ? 8 : 16;
+    while (ntiles * ks * 2 <= wg_target && nsteps / (ks * 2) >= min_steps) ks *= 2;
     // Scratch: split-K counters and partial tiles, then the activation terms.
     const size_t cnt_bytes = ((size_t)ntiles * 4 + 255) & ~(size_t)255;
     const size_t flag_bytes = ((size_t)L.M * 4 + 255) & ~(size_t)255;
@@ -533,9 +564,9 @@ int launch_gemm_tiled(const GemvLaunch& L, hipStream_t s) {
     const dim3 grid(tiles.x, tiles.y, ks);
     hipError_t e;
     if (L.glu)
-        e = L.tiled ? launch_gemm_x<2, true>(a, xf32, grid, s) : launch_gemm_x<2, false>(a, xf32, grid, s);
+        e = L.tiled ? launch_gemm_x<2, true>(a, xf32, TM, grid, s) : launch_gemm_x<2, false>(a, xf32, TM, grid, s);
     else
-        e = L.tiled ? launch_gemm_x<1, true>(a, xf32, grid, s) : launch_gemm_x<1, false>(a, xf32, grid, s);
+        e = L.tiled ? launch_gemm_x<1, true>(a, xf32, TM, grid, s) : launch_gemm_x<1, false>(a, xf32, TM, grid, s);
     return hip_check(e, "gemm_q4_kernel launch");
 }
 

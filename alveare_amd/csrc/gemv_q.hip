@@ -1,4 +1,4 @@
-// Entry points on the combined layout: alv_gemv_q, alv_gemm_q (M < 64 via the
+// Entry points on the combined layout: alv_gemv_q, alv_gemm_q (M < 32 via the
 // streaming kernel of gemv1_q.hip, larger M via the MFMA tiled kernel of
 // gemm_q.hip), the dequant and GLU parity kernels behind alv_dequant_q4 and
 // alv_glu.

@@ -104,11 +104,20 @@ int launch_gemm_tiled(const GemvLaunch& L, hipStream_t s);
 // streaming kernel, 16 tokens per launch): kTiledMinM, or the positive value
 // of the environment variable ALV_TILED_MIN_M, read at each call (a tuning
 // knob; the benchmark times both kernels at small M with it). Measured on the
-// 12B-class FFN: the tiled kernel takes about 300 us for any M up to one
-// 256-token tile, the streaming kernel about 88 us per 16 tokens, so the
-// streaming kernel is faster up to 48 tokens.
-constexpr int kTiledMinM = 64;
+// 12B-class FFN (3840 <-> 15360): the streaming kernel takes about 54 us per
+// 16 tokens; the tiled kernel with 64-token tiles 78-85 us for any M up to 64
+// with bf16-valued activations (one term) and 134-140 us with fp32 ones (three
+// terms). From 32 tokens the tiled kernel is faster for bf16-valued inputs
+// (81 against 107 us) and within a fifth for fp32 ones (136 against 112 us).
+constexpr int kTiledMinM = 32;
 int tiled_min_m();
+// Largest M the prefill GEMM runs with 64-token tiles (256-token tiles above);
+// ALV_GEMM_SMALL_TILE_MAX_M overrides.
+constexpr int kSmallTileMaxM = 128;
+int small_tile_max_m();
+// Workgroups per CU the 64-token prefill tiles aim at when splitting K
+// (default 1); ALV_GEMM_SMALL_WG_PER_CU overrides.
+int small_wg_per_cu();
 
 // The two launches of one FFN call on handle w (ffn_fused.hip): gate/up with
 // the GLU epilogue into the bf16 activation `act`, then down from it.
