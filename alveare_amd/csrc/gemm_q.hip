@@ -511,20 +511,29 @@ int launch_gemm_tiled(const GemvLaunch& L, hipStream_t s) {
     const int wg_target = TM == 64 ? small_wg_per_cu() * device_cus() : device_cus();
     const int min_steps = TM == 64 ? 8 : 16;
     while (ntiles * ks * 2 <= wg_target && nsteps / (ks * 2) >= min_steps) ks *= 2;
-    // Scratch: split-K counters and partial tiles, then the activation terms.
-    const size_t cnt_bytes = ((size_t)ntiles * 4 + 255) & ~(size_t)255;
+    // Split-K arrival counters: the stream's dedicated counter words (zero
+    // between launches, shared with the streaming kernel's split K), never
+    // the scratch below, whose bytes hold other launches' flags and terms.
+    Workspace ws{};
+    if (ks > 1 && (ntiles > kSplitCounters || get_workspace(s, (size_t)ntiles, &ws))) {
+        clear_error();
+        ks = 1;
+    }
+    // Scratch: token flags and partial tiles, then the activation terms.
     const size_t flag_bytes = ((size_t)L.M * 4 + 255) & ~(size_t)255;
-    const size_t part_bytes = ks > 1 ? (size_t)ntiles * ks * NT * TM * TN * sizeof(float) : 0;
     const size_t tstride = (size_t)L.M * L.K;
     const size_t term_bytes = xf32 ? 3 * tstride * sizeof(uint16_t) : 0;
     void* scratch = nullptr;
+    size_t part_bytes = 0;
     if (ks > 1 || xf32) {
-        if (6 * tstride >= 0x7FFFFF00ull || get_scratch(s, kScratchGemm, cnt_bytes + flag_bytes + part_bytes + term_bytes, &scratch)) {
+        part_bytes = ks > 1 ? (size_t)ntiles * ks * NT * TM * TN * sizeof(float) : 0;
+        if (6 * tstride >= 0x7FFFFF00ull || get_scratch(s, kScratchGemm, flag_bytes + part_bytes + term_bytes, &scratch)) {
             // No scratch (a graph capture that would have to grow it): one
             // launch over all of K, activations split inside the kernel.
             clear_error();
             scratch = nullptr;
             ks = 1;
+            part_bytes = 0;
         }
     }
     uint8_t* sb = static_cast<uint8_t*>(scratch);
@@ -546,11 +555,11 @@ int launch_gemm_tiled(const GemvLaunch& L, hipStream_t s) {
     a.tg = tile_geom(L.K);
     a.ks = ks;
     if (sb) {
-        a.cnt = reinterpret_cast<uint32_t*>(sb);
-        a.part = reinterpret_cast<float*>(sb + cnt_bytes + flag_bytes);
+        a.cnt = ks > 1 ? ws.counters : nullptr;
+        a.part = reinterpret_cast<float*>(sb + flag_bytes);
         if (xf32) {
-            uint32_t* flags = reinterpret_cast<uint32_t*>(sb + cnt_bytes);
-            uint16_t* terms = reinterpret_cast<uint16_t*>(sb + cnt_bytes + flag_bytes + part_bytes);
+            uint32_t* flags = reinterpret_cast<uint32_t*>(sb);
+            uint16_t* terms = reinterpret_cast<uint16_t*>(sb + flag_bytes + part_bytes);
             hipLaunchKernelGGL(split_x_kernel, dim3(L.M), dim3(256), 0, s, L.X, L.ldx, L.K, terms, (uint32_t)tstride, flags);
             if (int rc = hip_check(hipGetLastError(), "split_x_kernel launch")) return rc;
             a.X = terms;

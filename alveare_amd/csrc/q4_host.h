@@ -28,10 +28,13 @@ int get_workspace(hipStream_t s, size_t counters, Workspace* out);
 
 // Per-(device, stream, slot) scratch of at least `bytes`, zeroed when
 // allocated, for launches whose temporaries grow with their shape: slot 0 the
-// prefill GEMM's (counters, partial tiles, activation terms), slot 1 the
+// prefill GEMM's (token flags, partial tiles, activation terms), slot 1 the
 // streaming GEMV's split-K partial sums (rewritten by every such launch before
 // it is read), slot 2 the FFN activation of prefill-sized calls, slot 3 the
-// LM head's argmax pairs. A call that
+// LM head's argmax pairs, slot 4 attention's chunk partials. No slot holds
+// arrival counters: a slot's layout changes with the shape, so bytes one call
+// leaves behind sit where another call would count (get_workspace holds them).
+// A call that
 // fits what the slot holds allocates nothing. Growing allocates a new block
 // (at least twice the old capacity) and keeps the old one allocated for the
 // life of the process, since a HIP graph captured earlier may still use it;
@@ -41,7 +44,7 @@ constexpr int kScratchGemm = 0;
 constexpr int kScratchSplit = 1;
 constexpr int kScratchAct = 2;
 constexpr int kScratchHead = 3;  // the LM head's per-workgroup argmax pairs
-constexpr int kScratchAttn = 4;  // attention's arrival counters and chunk partials
+constexpr int kScratchAttn = 4;  // attention's chunk partials
 int get_scratch(hipStream_t s, int slot, size_t bytes, void** out);
 // Largest split-K partial-sum block of one streaming GEMV launch.
 constexpr size_t kPartMax = 256u << 20;

@@ -791,6 +791,34 @@ def test_lm_head_full_vocab(orc, dev):
     assert np.array_equal(lh, logits.cpu().numpy())
 
 
+def test_tiled_split_counters_survive_other_shapes(orc, dev, monkeypatch):
+    """The tiled kernel's split-K arrival counters are zero at every launch
+    whatever ran on the stream before: fp32 GEMMs whose token flags and
+    activation terms fill the stream's scratch alternate with a wider GEMM
+    that splits K over more tiles (a counter left non-zero makes a workgroup
+    add the partial tiles before the others have written theirs). Every result
+    matches the oracle on the first pass and is bit-identical after."""
+    import alveare_amd as aa
+
+    monkeypatch.setenv("ALV_TILED_MIN_M", "1")
+    cases = []
+    for i, (N, K) in enumerate([(3840, 15360), (15360, 3840), (3840, 4096)]):
+        W = orc.synth_q4(N, K, 7300 + i)
+        x = orc.synth_normal(K, 7310 + i)
+        cases.append((N, K, W, x, aa.Q4Weight(to_dev(W, dev), N, K), to_dev(x, dev)))
+    first = {}
+    for rep in range(4):
+        for N, K, W, x, w, xd in cases:
+            y = w(xd, M=1).cpu().numpy().reshape(-1)
+            if rep == 0:
+                parity.gemv_check(orc, W, x, y, N, K)
+                first[(N, K)] = y
+            else:
+                assert np.array_equal(y, first[(N, K)]), f"{N}x{K} pass {rep} differs from pass 0"
+    for *_, w, _ in cases:
+        w.close()
+
+
 @pytest.mark.parametrize("M", [1, 8, 16])
 def test_tiled_kernel_at_small_m(orc, dev, monkeypatch, M):
     """The MFMA tiled kernel at decode-sized M (ALV_TILED_MIN_M=1 routes every
