@@ -88,18 +88,20 @@ __device__ float pw_leaf_sq(const float* a, int n) {
     return res;
 }
 
-// The full recursion on one lane (widths whose splits are not halvings).
-__device__ float pw_serial_sq(const float* a, int n) {
-    struct Frame {
-        int off, n, stage;
-        float left;
-    };
-    Frame st[32];
+// The full recursion on one lane (widths whose splits are not halvings), its
+// frames in LDS (st: 16 frames, 256 bytes; n <= 8192 nests at most 8 deep): a
+// private array would give every launch of the kernel a scratch segment.
+struct PwFrame {
+    int off, n, stage;
+    float left;
+};
+
+__device__ float pw_serial_sq(const float* a, int n, PwFrame* st) {
     int sp = 0;
     st[0] = {0, n, 0, 0.0f};
     float ret = 0.0f;
     while (sp >= 0) {
-        Frame& f = st[sp];
+        PwFrame& f = st[sp];
         if (f.n <= 128) {
             ret = pw_leaf_sq(a + f.off, f.n);
             --sp;
@@ -125,7 +127,8 @@ __device__ float pw_serial_sq(const float* a, int n) {
 }
 
 // Pairwise sum of the squares of a[0, n), n <= 8192, by the workgroup
-// (kRowThreads threads; a and red in LDS, red >= 65 floats). Returned to all.
+// (kRowThreads threads; a and red in LDS, red >= 65 floats, 16-byte aligned: the
+// one-lane recursion keeps its frames in red[0, 64)). Returned to all.
 __device__ float pw_chunk_sq(const float* a, int n, float* red, int tid) {
     int leaf = n, leaves = 1;
     bool halving = true;
@@ -138,7 +141,7 @@ __device__ float pw_chunk_sq(const float* a, int n, float* red, int tid) {
         leaves *= 2;
     }
     if (!halving || leaves > 64) {
-        if (tid == 0) red[64] = pw_serial_sq(a, n);
+        if (tid == 0) red[64] = pw_serial_sq(a, n, reinterpret_cast<PwFrame*>(red));
     } else {
         // 8 lanes per leaf: lane j sums r[j] = a[j] + a[8 + j] + ... in order.
         const int j = tid & 7;
@@ -207,6 +210,30 @@ __device__ __forceinline__ uint4 pack8(const uint16_t (&b)[8]) {
 
 __device__ __forceinline__ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// Rows of up to 8 * kRegOct * kRowThreads values (4096: every hidden size of
+// the reference's models) keep their octets in registers, thread t holding
+// octets t and t + kRowThreads, and issue every load of the row -- values,
+// residual, norm weights -- before the first wait: one memory round trip per
+// kernel instead of one per step.
+constexpr int kRegOct = 2;
+
+__device__ __forceinline__ bool reg_row(int K, int pad) {
+    return K % 8 == 0 && pad % 8 == 0 && pad <= 8 * kRegOct * kRowThreads;
+}
+
+// Eight float32 weights w[8 v, 8 v + 8), or zeros for a null w.
+__device__ __forceinline__ void load_w8(const float* w, int v, float (&f)[8]) {
+    if (!w) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = 0.0f;
+        return;
+    }
+    const float4 w0 = reinterpret_cast<const float4*>(w)[2 * v];
+    const float4 w1 = reinterpret_cast<const float4*>(w)[2 * v + 1];
+    f[0] = w0.x; f[1] = w0.y; f[2] = w0.z; f[3] = w0.w;
+    f[4] = w1.x; f[5] = w1.y; f[6] = w1.z; f[7] = w1.w;
+}
+
 // xs[0, K) = float(x[0, K)); all threads, then a barrier.
 __device__ void stage_row(const uint16_t* x, float* xs, int K, int tid) {
     if (al16(x) && K % 8 == 0) {
@@ -264,9 +291,46 @@ __global__ void __launch_bounds__(kRowThreads) rmsnorm_kernel(const uint16_t* x,
     float* xs = lds + 128;
     const int tid = threadIdx.x;
     const size_t row = blockIdx.x;
-    stage_row(x + row * ldx, xs, K, tid);
+    const uint16_t* xr = x + row * ldx;
+    uint16_t* o = out + row * ldo;
+    if (reg_row(K, pad) && al16(xr) && al16(w) && al16(o)) {
+        uint4 xv[kRegOct];
+        float wv[kRegOct][8], f[kRegOct][8];
+#pragma unroll
+        for (int i = 0; i < kRegOct; ++i) {
+            const int v = tid + i * kRowThreads;
+            const bool in = 8 * v < K;
+            xv[i] = in ? reinterpret_cast<const uint4*>(xr)[v] : uint4{0u, 0u, 0u, 0u};
+            load_w8(in ? w : nullptr, v, wv[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kRegOct; ++i) {
+            const int v = tid + i * kRowThreads;
+            unpack8(xv[i], f[i]);
+            if (8 * v < K)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xs[8 * v + e] = f[i][e];
+        }
+        __syncthreads();
+        const float inv = rms_inv(xs, K, eps, red, tid);
+#pragma unroll
+        for (int i = 0; i < kRegOct; ++i) {
+            const int v = tid + i * kRowThreads;
+            if (8 * v >= pad) continue;
+            uint16_t b[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (8 * v < K)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float t = __fmul_rn(f[i][e], inv);
+                    b[e] = bf16_rne_bits(w ? __fmul_rn(t, wv[i][e]) : t);
+                }
+            reinterpret_cast<uint4*>(o)[v] = pack8(b);
+        }
+        return;
+    }
+    stage_row(xr, xs, K, tid);
     const float inv = rms_inv(xs, K, eps, red, tid);
-    write_norm(xs, K, pad, inv, w, out + row * ldo, tid);
+    write_norm(xs, K, pad, inv, w, o, tid);
 }
 
 // ---- alv_qkv_post --------------------------------------------------------------
@@ -301,25 +365,50 @@ __global__ void __launch_bounds__(kRowThreads) qkv_post_kernel(QkvPostArgs a) {
     const int role = b < a.heads ? 0 : (b < a.heads + a.kv_heads ? 1 : 2);
     const int h = role == 0 ? b : (role == 1 ? b - a.heads : b - a.heads - a.kv_heads);
     const int src = role == 0 ? h * D : (role == 1 || a.v_off < 0 ? a.k_off + h * D : a.v_off + h * D);
-    stage_row(a.qkv + src, xs, D, tid);
     const int norm = role == 0 ? a.norm_q : (role == 1 ? a.norm_k : a.norm_v);
+    const float* w = role == 0 ? a.q_w : (role == 1 ? a.k_w : nullptr);
+    const bool rot = role < 2 && a.rope;
+    const uint16_t* rrow = rot ? a.rope + (size_t)pos * a.rope_stride : nullptr;
+    // Heads of up to 2 x kRowThreads columns: this thread's norm weights and
+    // rotation values are loaded before the head is staged, so one memory
+    // round trip serves them all.
+    const bool pre = D <= 2 * kRowThreads;
+    float wv[2] = {0.0f, 0.0f}, cv = 0.0f, sv = 0.0f;
+    if (pre) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            if (norm && w && tid + j * kRowThreads < D) wv[j] = w[tid + j * kRowThreads];
+        if (rot && tid < a.half) {
+            cv = bf16_bits_to_f32(rrow[a.cos_off + tid]);
+            sv = bf16_bits_to_f32(rrow[a.sin_off + tid]);
+        }
+    }
+    stage_row(a.qkv + src, xs, D, tid);
     if (norm) {
         const float inv = rms_inv(xs, D, a.eps, red, tid);
-        const float* w = role == 0 ? a.q_w : (role == 1 ? a.k_w : nullptr);
-        for (int i = tid; i < D; i += kRowThreads) {
-            const float t = __fmul_rn(xs[i], inv);
-            xs[i] = bf16r(w ? __fmul_rn(t, w[i]) : t);
+        if (pre) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int i = tid + j * kRowThreads;
+                if (i >= D) continue;
+                const float t = __fmul_rn(xs[i], inv);
+                xs[i] = bf16r(w ? __fmul_rn(t, wv[j]) : t);
+            }
+        } else {
+            for (int i = tid; i < D; i += kRowThreads) {
+                const float t = __fmul_rn(xs[i], inv);
+                xs[i] = bf16r(w ? __fmul_rn(t, w[i]) : t);
+            }
         }
         __syncthreads();
     }
     uint16_t* dst = role == 0 ? a.q_out + (size_t)h * D
                               : (role == 1 ? a.kcache : a.vcache) + ((size_t)h * a.max_seq + pos) * D;
-    if (role < 2 && a.rope) {
+    if (rot) {
         // run_rope_cpu_gemma (model.py:549-575): y1 = x1 c - x2 s, y2 = x2 c + x1 s.
-        const uint16_t* row = a.rope + (size_t)pos * a.rope_stride;
         for (int i = tid; i < a.half; i += kRowThreads) {
-            const float c = bf16_bits_to_f32(row[a.cos_off + i]);
-            const float s = bf16_bits_to_f32(row[a.sin_off + i]);
+            const float c = pre ? cv : bf16_bits_to_f32(rrow[a.cos_off + i]);
+            const float s = pre ? sv : bf16_bits_to_f32(rrow[a.sin_off + i]);
             const float x1 = xs[i], x2 = xs[i + a.half];
             dst[i] = bf16_rne_bits(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s)));
             dst[i + a.half] = bf16_rne_bits(__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s)));
@@ -555,11 +644,11 @@ __global__ void __launch_bounds__(kRowThreads) add_norm_kernel(AddNormArgs a) {
     const int K = a.K;
     const int tid = threadIdx.x;
     const size_t row = blockIdx.x;
-    stage_row(a.y + row * a.ldy, xs, K, tid);
-    float inv = 1.0f;
-    if (a.norm_y) inv = rms_inv(xs, K, a.eps, red, tid);
+    const uint16_t* yr = a.y + row * a.ldy;
     const uint16_t* r = a.resid + row * a.ldr;
     uint16_t* so = a.sum_out + row * a.ld_sum;
+    uint16_t* no = a.norm_out ? a.norm_out + row * a.ldn : nullptr;
+    float inv = 1.0f;  // 1 / rms of y when it is normalised
     // s = bf16(r + t) (scaled), t = bf16(y * inv * w_y) or y.
     auto step = [&](float x, float rv, float w) -> float {
         float t = x;
@@ -572,6 +661,65 @@ __global__ void __launch_bounds__(kRowThreads) add_norm_kernel(AddNormArgs a) {
         if (a.scale_mode == 2) return bf16r(__fmul_rn(sum, a.scale));
         return bf16r(sum);
     };
+    if (reg_row(K, a.pad) && al16(yr) && al16(r) && al16(so) && al16(a.w_y) && al16(a.w_out) && al16(no)) {
+        uint4 yv[kRegOct], rv[kRegOct];
+        float wy[kRegOct][8], wo[kRegOct][8], f[kRegOct][8];
+#pragma unroll
+        for (int i = 0; i < kRegOct; ++i) {
+            const int v = tid + i * kRowThreads;
+            const bool in = 8 * v < K;
+            yv[i] = in ? reinterpret_cast<const uint4*>(yr)[v] : uint4{0u, 0u, 0u, 0u};
+            rv[i] = in ? reinterpret_cast<const uint4*>(r)[v] : uint4{0u, 0u, 0u, 0u};
+            load_w8(in && a.norm_y ? a.w_y : nullptr, v, wy[i]);
+            load_w8(in && no ? a.w_out : nullptr, v, wo[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kRegOct; ++i) {
+            const int v = tid + i * kRowThreads;
+            unpack8(yv[i], f[i]);
+            if (a.norm_y && 8 * v < K)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xs[8 * v + e] = f[i][e];
+        }
+        if (a.norm_y) {
+            __syncthreads();
+            inv = rms_inv(xs, K, a.eps, red, tid);
+        }
+#pragma unroll
+        for (int i = 0; i < kRegOct; ++i) {
+            const int v = tid + i * kRowThreads;
+            if (8 * v >= K) continue;
+            float rf[8];
+            unpack8(rv[i], rf);
+            uint16_t b[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                f[i][e] = step(f[i][e], rf[e], wy[i][e]);
+                b[e] = bf16_rne_bits(f[i][e]);
+                if (no) xs[8 * v + e] = f[i][e];
+            }
+            reinterpret_cast<uint4*>(so)[v] = pack8(b);
+        }
+        if (!no) return;
+        __syncthreads();
+        const float inv2 = rms_inv(xs, K, a.eps, red, tid);
+#pragma unroll
+        for (int i = 0; i < kRegOct; ++i) {
+            const int v = tid + i * kRowThreads;
+            if (8 * v >= a.pad) continue;
+            uint16_t b[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (8 * v < K)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float t = __fmul_rn(f[i][e], inv2);
+                    b[e] = bf16_rne_bits(a.w_out ? __fmul_rn(t, wo[i][e]) : t);
+                }
+            reinterpret_cast<uint4*>(no)[v] = pack8(b);
+        }
+        return;
+    }
+    stage_row(yr, xs, K, tid);
+    if (a.norm_y) inv = rms_inv(xs, K, a.eps, red, tid);
     if (al16(r) && al16(so) && al16(a.w_y) && K % 8 == 0) {
         for (int v = tid; v < K / 8; v += kRowThreads) {
             float rf[8], wf[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -599,9 +747,9 @@ __global__ void __launch_bounds__(kRowThreads) add_norm_kernel(AddNormArgs a) {
         }
     }
     __syncthreads();
-    if (!a.norm_out) return;
+    if (!no) return;
     const float inv2 = rms_inv(xs, K, a.eps, red, tid);
-    write_norm(xs, K, a.pad, inv2, a.w_out, a.norm_out + row * a.ldn, tid);
+    write_norm(xs, K, a.pad, inv2, a.w_out, no, tid);
 }
 
 // ---- alv_embed -------------------------------------------------------------------

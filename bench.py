@@ -349,6 +349,9 @@ def main() -> int:
     ap.add_argument("--profile-pass", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="only the headline workload (no extra_configs): the run profiled for the roofline kernel")
+    ap.add_argument("--decode-step", action="store_true",
+                    help="only the whole-decode-step measurement (its own JSON line): the run profiled for the "
+                         "decode step's kernel breakdown")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -365,6 +368,9 @@ def main() -> int:
     aa.lib()
     if args.profile_pass:
         return profile_pass(torch, aa, dev)
+    if args.decode_step:
+        print(json.dumps(decode_step(torch, aa, dev, reps=max(1, args.steps))), flush=True)
+        return 0
     nl = args.layers
     log(f"building {nl} synthetic layers on {torch.cuda.get_device_name(dev)}")
     t0 = time.time()

@@ -140,21 +140,25 @@ def test_attention_bound(dev, sliding, pos):
 
 # ---- residual steps (model.py:775-788; model.cpp:409-420) ---------------------------
 
-@pytest.mark.parametrize("mode,norm_y,norm_out", [(0, True, True), (1, True, False), (2, True, False),
-                                                   (0, False, True)])
-def test_add_norm_bit_exact(dev, mode, norm_y, norm_out):
+@pytest.mark.parametrize("mode,norm_y,norm_out,K,pad", [(0, True, True, 3840, 4096), (1, True, False, 3840, 4096),
+                                                         (2, True, False, 3840, 4096), (0, False, True, 3840, 4096),
+                                                         (0, True, True, 1152, 1152), (1, True, True, 5000, 5120),
+                                                         (0, True, True, 1001, 1008), (2, False, True, 4096, 4096)])
+def test_add_norm_bit_exact(dev, mode, norm_y, norm_out, K, pad):
+    """Rows held in registers (K a multiple of 8, pad <= 4096) and the LDS
+    paths (wider rows, K not a multiple of 8) give the reference's bits."""
     from alveare_amd import layer
 
-    _say(f"add_norm mode={mode} norm_y={norm_y} norm_out={norm_out}")
-    rng = np.random.default_rng(mode * 4 + norm_y * 2 + norm_out)
-    K, rows = 3840, 2
+    _say(f"add_norm mode={mode} norm_y={norm_y} norm_out={norm_out} K={K} pad={pad}")
+    rng = np.random.default_rng(mode * 4 + norm_y * 2 + norm_out + K)
+    rows = 2
     r = rnd_bf16(rng, (rows, K), 4.0)
     y = rnd_bf16(rng, (rows, K), 0.7)
     wy = rng.uniform(0.3, 2.0, K).astype(np.float32)
     wo = rng.uniform(0.3, 2.0, K).astype(np.float32)
     scale = np.float32(0.8125 if mode else 1.0) * np.float32(1.0001)
     s_out, n_out = layer.add_norm(bf_dev(r, dev), bf_dev(y, dev), K=K, rows=rows, w_y=wy, norm_y=norm_y,
-                                  scale=float(scale), scale_mode=mode, w_out=wo, norm_out=norm_out, pad=4096)
+                                  scale=float(scale), scale_mode=mode, w_out=wo, norm_out=norm_out, pad=pad)
     got_s = bf_np(s_out).reshape(rows, K)
     for i in range(rows):
         t = qn.rmsnorm_cpu(y[i], wy) if norm_y else y[i]
@@ -165,7 +169,7 @@ def test_add_norm_bit_exact(dev, mode, norm_y, norm_out):
             s = qn.bf16_rne((r[i] + t) * scale)
         assert np.array_equal(got_s[i], s), f"row {i}"
         if norm_out:
-            got_n = bf_np(n_out).reshape(rows, 4096)
+            got_n = bf_np(n_out).reshape(rows, pad)
             assert np.array_equal(got_n[i, :K], qn.rmsnorm_cpu(s, wo))
             assert not got_n[i, K:].any()
 
