@@ -53,6 +53,9 @@ SIGNATURES: dict[str, tuple] = {
     "alv_embed": (_i, [_vp, _i, _i, _vp, ctypes.c_double, _vp, _vp]),
     "alv_add_norm": (_i, [_vp, _i, _vp, _i, _vp, _i, ctypes.c_float, _i, _vp, _i, _vp, _vp, _i, _i, _i, _i,
                           ctypes.c_float, _vp]),
+    "alv_gemv_bf16_addnorm": (_i, [_vp, _vp, _vp, _vp, _i, ctypes.c_float, _i, _vp, _vp, ctypes.c_float, _vp, _vp]),
+    "alv_ffn_fused_bf16_addnorm": (_i, [_vp, _vp, _vp, _vp, _i, ctypes.c_float, _i, _vp, _vp, ctypes.c_float, _vp,
+                                        _vp]),
     "alv_weight_quantize": (_i, [_vp, _i, _i, _i, _i, _i, ctypes.POINTER(_vp), _vp]),
     "alv_q4_tiled_bytes": (ctypes.c_uint64, [_i, _i]),
     "alv_q4_tile": (_i, [_vp, _vp, _i, _i, _vp]),

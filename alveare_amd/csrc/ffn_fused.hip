@@ -239,6 +239,41 @@ int static_split(int dev, hipStream_t s, SplitBuf* out) {
 
 }  // namespace
 
+extern "C" int alv_ffn_fused_bf16_addnorm(alv_ffn_t w, const uint16_t* resid, const uint16_t* y, const float* w_y,
+                                          int norm_y, float scale, int scale_mode, uint16_t* sum_out,
+                                          const float* w_x, float eps, uint16_t* Y, void* stream) {
+    if (int rc = check_handle(w)) return rc;
+    if (!Y) return fail(ALV_ERR_ARG, "null output pointer");
+    if (reinterpret_cast<uintptr_t>(Y) % 2) return fail(ALV_ERR_ALIGN, "Y needs 2-byte alignment");
+    int dev = -1;
+    if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    if (dev != w->device) return fail(ALV_ERR_HANDLE, "FFN handle belongs to device %d, current device is %d", w->device, dev);
+    ResidStep st;
+    st.resid = resid;
+    st.y = y;
+    st.w_y = w_y;
+    st.norm_y = norm_y;
+    st.scale = scale;
+    st.scale_mode = scale_mode;
+    st.sum_out = sum_out;
+    st.w_x = w_x;
+    st.eps = eps;
+    hipStream_t s = (hipStream_t)stream;
+    GemvLaunch op[2];
+    ffn_ops(w, w->a, nullptr, w->H, nullptr, w->H, 1, op);
+    op[0].X = nullptr;
+    op[0].Xb = y;
+    op[0].parts = 1;
+    op[0].step = &st;
+    op[1].Y = nullptr;
+    op[1].Yb = Y;
+    if (int rc = launch_gemv(op[0], s)) return rc;
+    if (int rc = launch_gemv(op[1], s)) return rc;
+    w->last_a = w->a;
+    w->a_rows = 1;
+    return ALV_OK;
+}
+
 extern "C" int alv_ffn_fused_noalloc(alv_ffn_t w, const float* X, float* Y, int M, int ldx, int ldy,
                                      void* stream) {
     if (int rc = check_handle(w)) return rc;

@@ -41,6 +41,7 @@
 
 #include "q4_device.h"
 #include "q4_host.h"
+#include "row_norm.h"
 
 namespace alv {
 
@@ -65,6 +66,14 @@ struct Gemv1Args {
     int rt_q, rt_r;  // so group t owns rt_q + (t < rt_r) row tiles
     int ks;          // K splits: workgroup b is tile group b / ks, super-step range b % ks
     int act;
+    // Fused residual step (bf16 one-token launches; pr_r null: none).
+    const uint16_t* pr_r;
+    const uint16_t* pr_y;
+    const float* pr_wy;
+    const float* pr_wx;
+    uint16_t* pr_s;
+    float pr_scale, pr_eps;
+    int pr_norm_y, pr_mode;
 };
 
 constexpr int kXO = 4;  // activation octets per thread and staging round
@@ -226,6 +235,62 @@ __device__ __forceinline__ void stage_acts(const Gemv1Args& a, const WgWork& wk,
     if constexpr (Ph::QUAD)
         for (int sl = tid; sl < wk.nsw * 64; sl += 64 * NW)
             *reinterpret_cast<u32x4*>(xs + ((size_t)sl * Ph::SR + Ph::RM) * 8) = u32x4{0u, 0u, 0u, 0u};
+}
+
+// ---- 1'. the activation from a fused residual step -----------------------------------
+// Thread t owns octet t of the row (K <= 8 * threads, K % 8 == 0, one K split):
+// it loads y, the residual and both norm weights at once, and the workgroup
+// runs the layer's residual step exactly as alv_add_norm does -- s =
+// resid_step(y, r) with y's norm when pr_norm_y, then x = bf16(rmsnorm(s) [*
+// w_x]) -- in the float row `row` (LDS, K floats) with `red` (LDS, 128
+// floats) for the pairwise sums. Workgroup 0 writes s to pr_s. Octet t of x
+// goes to operand slot (t / 64) * 64 + (t % 16) * 4 + (t / 16) % 4 (the
+// inverse of stage_acts' slot order); octets past K are zeros.
+template <int NW>
+__device__ void fused_resid_step(const Gemv1Args& a, const WgWork& wk, __bf16* xs, float* red, float* row, int tid) {
+    constexpr int NT = 64 * NW;
+    const int K = a.K;
+    const int v = tid;
+    const bool in = 8 * v < K;
+    const uint4 yv = in ? reinterpret_cast<const uint4*>(a.pr_y)[v] : uint4{0u, 0u, 0u, 0u};
+    const uint4 rv = in ? reinterpret_cast<const uint4*>(a.pr_r)[v] : uint4{0u, 0u, 0u, 0u};
+    float wy[8], wx[8], f[8], rf[8];
+    load_w8(in && a.pr_norm_y ? a.pr_wy : nullptr, v, wy);
+    load_w8(in ? a.pr_wx : nullptr, v, wx);
+    unpack8(yv, f);
+    float inv = 1.0f;
+    if (a.pr_norm_y) {
+        if (in)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) row[8 * v + e] = f[e];
+        __syncthreads();
+        inv = rms_inv<NT>(row, K, a.pr_eps, red, tid);
+    }
+    unpack8(rv, rf);
+    uint16_t b[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        f[e] = resid_step(f[e], rf[e], wy[e], inv, a.pr_norm_y, a.pr_wy != nullptr, a.pr_mode, a.pr_scale);
+        b[e] = bf16_rne_bits(f[e]);
+    }
+    if (in) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) row[8 * v + e] = f[e];
+        if (blockIdx.x == 0) reinterpret_cast<uint4*>(a.pr_s)[v] = pack8(b);
+    }
+    __syncthreads();
+    const float inv2 = rms_inv<NT>(row, K, a.pr_eps, red, tid);
+    if (v < wk.nsw * 64) {
+        uint16_t xb[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (in)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float t = __fmul_rn(f[e], inv2);
+                xb[e] = bf16_rne_bits(a.pr_wx ? __fmul_rn(t, wx[e]) : t);
+            }
+        const int sl = (v >> 6) * 64 + ((v & 15) << 2) + ((v >> 4) & 3);
+        *reinterpret_cast<uint4*>(xs + (size_t)sl * 8) = pack8(xb);
+    }
 }
 
 // The five 16-byte pieces of unit u (u >= U: past the range, zeros and no
@@ -507,8 +572,19 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     if (tid == 0) *next = P * NW;
 
     // The activation is staged before any weight load: queued behind the
-    // weight loads of every CU it would wait for (bytes in flight) / bandwidth.
-    stage_acts<NW, R, XB, MT, TB>(a, wk, xs, tid);
+    // weight loads of every CU it would wait for (bytes in flight) / bandwidth
+    // (issuing the first weight loads ahead of a fused residual step's
+    // computation measured slower as well).
+    bool fused = false;
+    if constexpr (XB && MT == 1) {
+        if (a.pr_r) {
+            // The fused residual step's LDS follows the unit counter.
+            float* red = reinterpret_cast<float*>(next + 4);
+            fused_resid_step<NW>(a, wk, xs, red, red + 128, tid);
+            fused = true;
+        }
+    }
+    if (!fused) stage_acts<NW, R, XB, MT, TB>(a, wk, xs, tid);
     lds_barrier();
 
     // ---- 2. the first P units of this wave -----------------------------------------
@@ -780,6 +856,17 @@ int fill_args(const GemvLaunch& L, const Gemv1Plan& p, int m0, int m, hipStream_
     a.rt_r = p.rt_r;
     a.ks = p.ks;
     a.act = L.act;
+    if (const ResidStep* st = L.step) {
+        a.pr_r = st->resid;
+        a.pr_y = st->y;
+        a.pr_wy = st->w_y;
+        a.pr_wx = st->w_x;
+        a.pr_s = st->sum_out;
+        a.pr_scale = st->scale;
+        a.pr_eps = st->eps;
+        a.pr_norm_y = st->norm_y;
+        a.pr_mode = st->scale_mode;
+    }
     *out = a;
     return ALV_OK;
 }
@@ -802,7 +889,32 @@ int64_t gemv_split_bytes(const GemvLaunch& L) {
     return (int64_t)most;
 }
 
+// A one-token launch whose workgroups compute their bf16 activation from a
+// fused residual step (fused_resid_step): one K split, the float row and the
+// pairwise-sum scratch after the unit counter.
+int launch_gemv_step(const GemvLaunch& L, hipStream_t s) {
+    const ResidStep& st = *L.step;
+    if (L.M != 1 || !L.Xb || !L.tiled || L.parts != 1)
+        return fail(ALV_ERR_ARG, "a fused residual step takes one token of bf16 activations on registered weights");
+    if (L.K % 8 || L.K > kResidStepMaxK)
+        return fail(ALV_ERR_ARG, "a fused residual step takes K a multiple of 8 up to %d (got %d)", kResidStepMaxK, L.K);
+    if (!st.resid || !st.y || !st.sum_out) return fail(ALV_ERR_ARG, "null residual-step pointer");
+    if (st.scale_mode < 0 || st.scale_mode > 2) return fail(ALV_ERR_ARG, "bad scale_mode %d", st.scale_mode);
+    auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (!al(st.resid) || !al(st.y) || !al(st.sum_out) || !al(st.w_y) || !al(st.w_x))
+        return fail(ALV_ERR_ALIGN, "residual-step rows and weights need 16-byte alignment");
+    Gemv1Plan p;
+    if (!plan_gemv1(L, 1, &p)) return fail(ALV_ERR_RANGE, "streaming GEMV: no plan for N=%d K=%d", L.N, L.K);
+    if (p.ks != 1) return fail(ALV_ERR_RANGE, "a fused residual step needs the whole of K in one workgroup (K=%d)", L.K);
+    p.lds += 128 * sizeof(float) + (size_t)L.K * sizeof(float);
+    if (p.lds > dev_info().lds) return fail(ALV_ERR_RANGE, "a fused residual step at K=%d exceeds the LDS", L.K);
+    Gemv1Args a;
+    if (int rc = fill_args(L, p, 0, 1, s, &a)) return rc;
+    return hip_check(launch_shape(a, L, p.sh, p.tg * p.ks, p.lds, s), "q4_gemv1_kernel launch");
+}
+
 int launch_gemv(const GemvLaunch& L, hipStream_t s) {
+    if (L.step) return launch_gemv_step(L, s);
     if (L.M < 1 || L.M > kGemvMaxM) return fail(ALV_ERR_ARG, "streaming GEMV takes 1 <= M <= %d (got %d)", kGemvMaxM, L.M);
     if (L.parts != (L.Xb ? 1 : 3)) return fail(ALV_ERR_ARG, "fp32 activations take 3 terms, bf16 activations 1");
     const int mmax = max_tokens(L);

@@ -16,18 +16,7 @@
 // same rounding (products and sums written with the _rn intrinsics so that
 // nothing contracts into an FMA), and the one reduction whose order matters at
 // bf16 output precision -- np.mean(x ** 2) of RMSNorm -- is numpy's own
-// summation order: np.add.reduce over a contiguous float32 array is numpy's
-// pairwise_sum (numpy/_core/src/umath/loops_utils.h.src): fewer than 8 values
-// summed in order from 0; up to 128 values in eight interleaved accumulators
-// r[j] += a[8i + j], combined ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7)),
-// then the n % 8 tail in order; more values split at n2 = n/2 - (n/2) % 8 with
-// the two halves' sums added; arrays longer than numpy's 8192-element buffer
-// are summed per buffer and the buffer sums added in order. For every row
-// width whose splits are exact
-// halvings (3840, 4096, 2048, 1152, 256, 512, ...) the leaves are summed one
-// per lane and the halves combined across lanes in the recursion's own tree;
-// other widths follow the recursion on one lane. numpy >= 2 evaluates the
-// scalar steps (mean = sum / n, 1 / sqrt(var + eps)) in float32, as here.
+// summation order (row_norm.h).
 //
 // Attention is not bit-exact: the reference's scores and weighted sums are
 // BLAS dot products (np.dot) whose order is the library's. Here the positions
@@ -47,6 +36,7 @@
 
 #include "q4_device.h"
 #include "q4_host.h"
+#include "row_norm.h"
 
 namespace alv {
 
@@ -54,161 +44,6 @@ namespace {
 
 constexpr int kRowThreads = 256;
 constexpr int kMaxRowK = 32768;  // 128 KiB of float32 row in LDS
-
-__device__ __forceinline__ uint16_t bf16_rne_bits(float v) {
-    if (v != v) return 0x7FC0u;
-    const uint32_t u = __builtin_bit_cast(uint32_t, v);
-    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
-}
-
-__device__ __forceinline__ float bf16r(float v) { return bf16_bits_to_f32(bf16_rne_bits(v)); }
-
-__device__ __forceinline__ float sqv(const float* a, int i) { return __fmul_rn(a[i], a[i]); }
-
-// ---- numpy's pairwise float32 sum of squares ---------------------------------------
-
-// The leaf rule over the squares of a[0, n), n <= 128, on one lane.
-__device__ float pw_leaf_sq(const float* a, int n) {
-    if (n < 8) {
-        float r = 0.0f;
-        for (int i = 0; i < n; ++i) r = __fadd_rn(r, sqv(a, i));
-        return r;
-    }
-    float r[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] = sqv(a, j);
-    int i = 8;
-    for (; i < n - (n % 8); i += 8) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) r[j] = __fadd_rn(r[j], sqv(a, i + j));
-    }
-    float res = __fadd_rn(__fadd_rn(__fadd_rn(r[0], r[1]), __fadd_rn(r[2], r[3])),
-                          __fadd_rn(__fadd_rn(r[4], r[5]), __fadd_rn(r[6], r[7])));
-    for (; i < n; ++i) res = __fadd_rn(res, sqv(a, i));
-    return res;
-}
-
-// The full recursion on one lane (widths whose splits are not halvings), its
-// frames in LDS (st: 16 frames, 256 bytes; n <= 8192 nests at most 8 deep): a
-// private array would give every launch of the kernel a scratch segment.
-struct PwFrame {
-    int off, n, stage;
-    float left;
-};
-
-__device__ float pw_serial_sq(const float* a, int n, PwFrame* st) {
-    int sp = 0;
-    st[0] = {0, n, 0, 0.0f};
-    float ret = 0.0f;
-    while (sp >= 0) {
-        PwFrame& f = st[sp];
-        if (f.n <= 128) {
-            ret = pw_leaf_sq(a + f.off, f.n);
-            --sp;
-            continue;
-        }
-        int n2 = f.n / 2;
-        n2 -= n2 % 8;
-        if (f.stage == 0) {
-            f.stage = 1;
-            st[sp + 1] = {f.off, n2, 0, 0.0f};
-            ++sp;
-        } else if (f.stage == 1) {
-            f.left = ret;
-            f.stage = 2;
-            st[sp + 1] = {f.off + n2, f.n - n2, 0, 0.0f};
-            ++sp;
-        } else {
-            ret = __fadd_rn(f.left, ret);
-            --sp;
-        }
-    }
-    return ret;
-}
-
-// Pairwise sum of the squares of a[0, n), n <= 8192, by the workgroup
-// (kRowThreads threads; a and red in LDS, red >= 65 floats, 16-byte aligned: the
-// one-lane recursion keeps its frames in red[0, 64)). Returned to all.
-__device__ float pw_chunk_sq(const float* a, int n, float* red, int tid) {
-    int leaf = n, leaves = 1;
-    bool halving = true;
-    while (leaf > 128) {
-        if ((leaf & 1) || ((leaf / 2) % 8)) {
-            halving = false;
-            break;
-        }
-        leaf /= 2;
-        leaves *= 2;
-    }
-    if (!halving || leaves > 64) {
-        if (tid == 0) red[64] = pw_serial_sq(a, n, reinterpret_cast<PwFrame*>(red));
-    } else {
-        // 8 lanes per leaf: lane j sums r[j] = a[j] + a[8 + j] + ... in order.
-        const int j = tid & 7;
-        const int m8 = leaf - leaf % 8;
-        for (int base = 0; base < leaves; base += kRowThreads / 8) {
-            const int lf = base + (tid >> 3);
-            const bool act = lf < leaves;
-            const float* p = a + (size_t)(act ? lf : 0) * leaf;
-            float r = 0.0f;
-            if (act && leaf >= 8) {
-                r = sqv(p, j);
-                for (int i = 8 + j; i < m8; i += 8) r = __fadd_rn(r, sqv(p, i));
-            }
-            r = __fadd_rn(r, __shfl_xor(r, 1));
-            r = __fadd_rn(r, __shfl_xor(r, 2));
-            r = __fadd_rn(r, __shfl_xor(r, 4));
-            if (act && j == 0) {
-                if (leaf < 8) {
-                    r = 0.0f;
-                    for (int i = 0; i < leaf; ++i) r = __fadd_rn(r, sqv(p, i));
-                } else {
-                    for (int i = m8; i < leaf; ++i) r = __fadd_rn(r, sqv(p, i));
-                }
-                red[lf] = r;
-            }
-        }
-        __syncthreads();
-        if (tid < 64) {
-            float v = tid < leaves ? red[tid] : 0.0f;
-            for (int s = 1; s < leaves; s *= 2) {
-                const float o = __shfl_down(v, s);
-                if ((tid & (2 * s - 1)) == 0) v = __fadd_rn(v, o);
-            }
-            if (tid == 0) red[64] = v;
-        }
-    }
-    __syncthreads();
-    const float r = red[64];
-    __syncthreads();  // red is reused by the next call
-    return r;
-}
-
-// 1 / sqrt(mean(x^2) + eps) of the K values xs (LDS) in numpy's float32
-// arithmetic: np.add.reduce takes the array in buffers of 8192 elements
-// (np.getbufsize()), sums each pairwise and adds the buffer sums in order.
-__device__ float rms_inv(const float* xs, int K, float eps, float* red, int tid) {
-    constexpr int kBuf = 8192;
-    float s = pw_chunk_sq(xs, min(K, kBuf), red, tid);
-    for (int off = kBuf; off < K; off += kBuf) s = __fadd_rn(s, pw_chunk_sq(xs + off, min(K - off, kBuf), red, tid));
-    const float var = __fdiv_rn(s, (float)K);
-    // sqrtf is the correctly rounded square root here (v_sqrt_f32 plus a
-    // neighbour test); __fsqrt_rn compiles to the bare 1-ulp v_sqrt_f32.
-    return __fdiv_rn(1.0f, sqrtf(__fadd_rn(var, eps)));
-}
-
-__device__ __forceinline__ void unpack8(uint4 v, float (&f)[8]) {
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = bf16_bits_to_f32(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu);
-}
-
-__device__ __forceinline__ uint4 pack8(const uint16_t (&b)[8]) {
-    return uint4{b[0] | ((uint32_t)b[1] << 16), b[2] | ((uint32_t)b[3] << 16), b[4] | ((uint32_t)b[5] << 16),
-                 b[6] | ((uint32_t)b[7] << 16)};
-}
-
-__device__ __forceinline__ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // Rows of up to 8 * kRegOct * kRowThreads values (4096: every hidden size of
 // the reference's models) keep their octets in registers, thread t holding
@@ -219,19 +54,6 @@ constexpr int kRegOct = 2;
 
 __device__ __forceinline__ bool reg_row(int K, int pad) {
     return K % 8 == 0 && pad % 8 == 0 && pad <= 8 * kRegOct * kRowThreads;
-}
-
-// Eight float32 weights w[8 v, 8 v + 8), or zeros for a null w.
-__device__ __forceinline__ void load_w8(const float* w, int v, float (&f)[8]) {
-    if (!w) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] = 0.0f;
-        return;
-    }
-    const float4 w0 = reinterpret_cast<const float4*>(w)[2 * v];
-    const float4 w1 = reinterpret_cast<const float4*>(w)[2 * v + 1];
-    f[0] = w0.x; f[1] = w0.y; f[2] = w0.z; f[3] = w0.w;
-    f[4] = w1.x; f[5] = w1.y; f[6] = w1.z; f[7] = w1.w;
 }
 
 // xs[0, K) = float(x[0, K)); all threads, then a barrier.
@@ -312,7 +134,7 @@ __global__ void __launch_bounds__(kRowThreads) rmsnorm_kernel(const uint16_t* x,
                 for (int e = 0; e < 8; ++e) xs[8 * v + e] = f[i][e];
         }
         __syncthreads();
-        const float inv = rms_inv(xs, K, eps, red, tid);
+        const float inv = rms_inv<kRowThreads>(xs, K, eps, red, tid);
 #pragma unroll
         for (int i = 0; i < kRegOct; ++i) {
             const int v = tid + i * kRowThreads;
@@ -329,7 +151,7 @@ __global__ void __launch_bounds__(kRowThreads) rmsnorm_kernel(const uint16_t* x,
         return;
     }
     stage_row(xr, xs, K, tid);
-    const float inv = rms_inv(xs, K, eps, red, tid);
+    const float inv = rms_inv<kRowThreads>(xs, K, eps, red, tid);
     write_norm(xs, K, pad, inv, w, o, tid);
 }
 
@@ -385,7 +207,7 @@ __global__ void __launch_bounds__(kRowThreads) qkv_post_kernel(QkvPostArgs a) {
     }
     stage_row(a.qkv + src, xs, D, tid);
     if (norm) {
-        const float inv = rms_inv(xs, D, a.eps, red, tid);
+        const float inv = rms_inv<kRowThreads>(xs, D, a.eps, red, tid);
         if (pre) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
@@ -651,15 +473,7 @@ __global__ void __launch_bounds__(kRowThreads) add_norm_kernel(AddNormArgs a) {
     float inv = 1.0f;  // 1 / rms of y when it is normalised
     // s = bf16(r + t) (scaled), t = bf16(y * inv * w_y) or y.
     auto step = [&](float x, float rv, float w) -> float {
-        float t = x;
-        if (a.norm_y) {
-            t = __fmul_rn(t, inv);
-            t = bf16r(a.w_y ? __fmul_rn(t, w) : t);
-        }
-        const float sum = __fadd_rn(rv, t);
-        if (a.scale_mode == 1) return bf16r(__fmul_rn(bf16r(sum), a.scale));
-        if (a.scale_mode == 2) return bf16r(__fmul_rn(sum, a.scale));
-        return bf16r(sum);
+        return resid_step(x, rv, w, inv, a.norm_y, a.w_y != nullptr, a.scale_mode, a.scale);
     };
     if (reg_row(K, a.pad) && al16(yr) && al16(r) && al16(so) && al16(a.w_y) && al16(a.w_out) && al16(no)) {
         uint4 yv[kRegOct], rv[kRegOct];
@@ -683,7 +497,7 @@ __global__ void __launch_bounds__(kRowThreads) add_norm_kernel(AddNormArgs a) {
         }
         if (a.norm_y) {
             __syncthreads();
-            inv = rms_inv(xs, K, a.eps, red, tid);
+            inv = rms_inv<kRowThreads>(xs, K, a.eps, red, tid);
         }
 #pragma unroll
         for (int i = 0; i < kRegOct; ++i) {
@@ -702,7 +516,7 @@ __global__ void __launch_bounds__(kRowThreads) add_norm_kernel(AddNormArgs a) {
         }
         if (!no) return;
         __syncthreads();
-        const float inv2 = rms_inv(xs, K, a.eps, red, tid);
+        const float inv2 = rms_inv<kRowThreads>(xs, K, a.eps, red, tid);
 #pragma unroll
         for (int i = 0; i < kRegOct; ++i) {
             const int v = tid + i * kRowThreads;
@@ -719,7 +533,7 @@ __global__ void __launch_bounds__(kRowThreads) add_norm_kernel(AddNormArgs a) {
         return;
     }
     stage_row(yr, xs, K, tid);
-    if (a.norm_y) inv = rms_inv(xs, K, a.eps, red, tid);
+    if (a.norm_y) inv = rms_inv<kRowThreads>(xs, K, a.eps, red, tid);
     if (al16(r) && al16(so) && al16(a.w_y) && K % 8 == 0) {
         for (int v = tid; v < K / 8; v += kRowThreads) {
             float rf[8], wf[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -748,7 +562,7 @@ __global__ void __launch_bounds__(kRowThreads) add_norm_kernel(AddNormArgs a) {
     }
     __syncthreads();
     if (!no) return;
-    const float inv2 = rms_inv(xs, K, a.eps, red, tid);
+    const float inv2 = rms_inv<kRowThreads>(xs, K, a.eps, red, tid);
     write_norm(xs, K, a.pad, inv2, a.w_out, no, tid);
 }
 

@@ -67,6 +67,25 @@ struct SplitBuf {
 // fp32 (X) or bf16 bit patterns (Xb, parts = 1, no GLU); the output is fp32
 // (Y) or bf16 bit patterns (Yb). Weights in the tiled layout (q4_device.h) or,
 // for fp32 activations without a GLU, the combined layout.
+// A decode layer's residual step fused ahead of a one-token bf16 GEMV: the
+// workgroups compute the activation x = bf16(rmsnorm(s) [* w_x]) themselves
+// from s = resid_step(y, resid) (row_norm.h), workgroup 0 also writing s to
+// sum_out, so the separate alv_add_norm launch and its output round trip go.
+struct ResidStep {
+    const uint16_t* resid = nullptr;
+    const uint16_t* y = nullptr;
+    const float* w_y = nullptr;  // null: y's norm has no weight
+    int norm_y = 1;
+    float scale = 1.0f;
+    int scale_mode = 0;
+    uint16_t* sum_out = nullptr;
+    const float* w_x = nullptr;  // null: the activation's norm has no weight
+    float eps = 1e-6f;
+};
+// Widest row a fused residual step takes (one octet per thread of the
+// 1024-thread workgroup, the float row in LDS).
+constexpr int kResidStepMaxK = 8192;
+
 struct GemvLaunch {
     const uint8_t* W0 = nullptr;
     const uint8_t* W1 = nullptr;
@@ -82,6 +101,7 @@ struct GemvLaunch {
     bool tiled = false;  // weights in the tiled layout (q4_device.h) instead of the combined one
     int act = ALV_ACT_GELU_TANH;
     const SplitBuf* split = nullptr;  // caller's split-K temporaries (nullptr: the stream's)
+    const ResidStep* step = nullptr;  // fused residual step (M = 1, bf16 activation; nullptr: X / Xb as given)
 };
 int launch_gemv(const GemvLaunch& L, hipStream_t s);
 // The split-K partial-sum bytes launch_gemv(L) needs (0: no launch splits K),

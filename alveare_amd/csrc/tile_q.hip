@@ -190,6 +190,40 @@ extern "C" int alv_gemv_bf16(alv_weight_t w, const uint16_t* X, uint16_t* Y, int
     return ALV_OK;
 }
 
+extern "C" int alv_gemv_bf16_addnorm(alv_weight_t w, const uint16_t* resid, const uint16_t* y, const float* w_y,
+                                     int norm_y, float scale, int scale_mode, uint16_t* sum_out, const float* w_x,
+                                     float eps, uint16_t* Y, void* stream) {
+    if (int rc = check_weight(w)) return rc;
+    if (!Y) return fail(ALV_ERR_ARG, "null output pointer");
+    if (reinterpret_cast<uintptr_t>(Y) % 2) return fail(ALV_ERR_ALIGN, "Y needs 2-byte alignment");
+    int dev = -1;
+    if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    if (dev != w->device) return fail(ALV_ERR_HANDLE, "weight handle belongs to device %d, current device is %d", w->device, dev);
+    ResidStep st;
+    st.resid = resid;
+    st.y = y;
+    st.w_y = w_y;
+    st.norm_y = norm_y;
+    st.scale = scale;
+    st.scale_mode = scale_mode;
+    st.sum_out = sum_out;
+    st.w_x = w_x;
+    st.eps = eps;
+    GemvLaunch L;
+    L.W0 = w->w;
+    L.Xb = y;
+    L.ldx = w->K;
+    L.Yb = Y;
+    L.ldy = w->N;
+    L.M = 1;
+    L.N = w->N;
+    L.K = w->K;
+    L.parts = 1;
+    L.tiled = true;
+    L.step = &st;
+    return launch_gemv(L, (hipStream_t)stream);
+}
+
 extern "C" void alv_weight_release(alv_weight_t w) {
     if (!w || w->magic != kWeightMagic) return;
     int cur = -1;

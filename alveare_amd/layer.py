@@ -185,6 +185,49 @@ def ffn_fused_bf16(F: FfnWeights, X: torch.Tensor, Y: torch.Tensor | None = None
     return Y
 
 
+def _step_args(resid, y, K, w_y, norm_y, scale, scale_mode, sum_out, w_x, eps, dev):
+    _bf16(resid, "resid", K)
+    _bf16(y, "y", K)
+    _bf16(sum_out, "sum_out", K)
+    if sum_out.data_ptr() in (resid.data_ptr(), y.data_ptr()):
+        raise ValueError("sum_out must not alias resid or y")
+    w_y = _f32(w_y, "w_y", K, dev)
+    w_x = _f32(w_x, "w_x", K, dev)
+    return (resid.data_ptr(), y.data_ptr(), _ptr(w_y), int(norm_y), ctypes.c_float(scale), scale_mode,
+            sum_out.data_ptr(), _ptr(w_x), ctypes.c_float(eps)), (w_y, w_x)
+
+
+def gemv_bf16_addnorm(W: Q4Weight, resid: torch.Tensor, y: torch.Tensor, *, sum_out: torch.Tensor, w_y=None,
+                      norm_y: bool = True, scale: float = 1.0, scale_mode: int = 0, w_x=None, eps: float = _GEMMA_EPS,
+                      Y: torch.Tensor | None = None) -> torch.Tensor:
+    """add_norm(resid, y, ...) of one row (sum_out = s) and Y = gemv_bf16(W,
+    rmsnorm(s) * w_x) in one launch: the matmul's workgroups compute the
+    normalised activation themselves, bit for bit as the two calls do."""
+    args, keep = _step_args(resid, y, W.K, w_y, norm_y, scale, scale_mode, sum_out, w_x, eps, W.device)
+    if Y is None:
+        Y = torch.empty(W.N, dtype=torch.bfloat16, device=W.device)
+    _bf16(Y, "Y", W.N)
+    with torch.cuda.device(W.device):
+        check(lib().alv_gemv_bf16_addnorm(W.handle, *args, Y.data_ptr(), _stream(y)), "alv_gemv_bf16_addnorm")
+    return Y
+
+
+def ffn_fused_bf16_addnorm(F: FfnWeights, resid: torch.Tensor, y: torch.Tensor, *, sum_out: torch.Tensor, w_y=None,
+                           norm_y: bool = True, scale: float = 1.0, scale_mode: int = 0, w_x=None,
+                           eps: float = _GEMMA_EPS, Y: torch.Tensor | None = None) -> torch.Tensor:
+    """add_norm(resid, y, ...) of one row (sum_out = s) and Y =
+    ffn_fused_bf16(F, rmsnorm(s) * w_x), the residual step inside the FFN's
+    gate/up launch."""
+    args, keep = _step_args(resid, y, F.H, w_y, norm_y, scale, scale_mode, sum_out, w_x, eps, F.device)
+    if Y is None:
+        Y = torch.empty(F.H, dtype=torch.bfloat16, device=F.device)
+    _bf16(Y, "Y", F.H)
+    with torch.cuda.device(F.device):
+        check(lib().alv_ffn_fused_bf16_addnorm(F.handle, *args, Y.data_ptr(), _stream(y)),
+              "alv_ffn_fused_bf16_addnorm")
+    return Y
+
+
 def embed(table: torch.Tensor, token_dev: torch.Tensor, scale: float, out: torch.Tensor | None = None) -> torch.Tensor:
     """bf16(float(double(table[token]) * scale)) for the token in device memory
     (the Gemma-4 lookup with scale sqrt(hidden), runtime/py/model.py:889-891);
@@ -231,9 +274,10 @@ class Gemma4DecodeLayer:
     takes and returns bf16 [H] device tensors and updates the KV caches."""
 
     def __init__(self, *, qkv, o, gate, up, down, norms: dict, scale: float, sliding: bool, H: int, I: int,
-                 max_seq: int, device, rope_table=None, pos_dev: torch.Tensor | None = None):
+                 max_seq: int, device, rope_table=None, pos_dev: torch.Tensor | None = None, fuse: bool = True):
         dev = torch.device(device)
         self.sliding, self.H, self.I, self.max_seq, self.device = sliding, H, I, max_seq, dev
+        self.fuse = fuse
         self.heads = 16
         self.kv_heads = 8 if sliding else 1
         self.D = 256 if sliding else 512
@@ -268,24 +312,43 @@ class Gemma4DecodeLayer:
         self.down = torch.empty(H, **bf)
         self.y = torch.empty(H, **bf)
 
-    def enqueue(self, x: torch.Tensor, normed: bool = False, next_norm=None) -> torch.Tensor:
+    def enqueue(self, x: torch.Tensor, normed: bool = False, next_norm=None, step_in: dict | None = None,
+                defer: bool = False):
         """The layer's launches for the position already in ``pos_dev``.
         ``normed``: ``x_norm`` already holds the input norm (written by the
         previous layer's last launch). ``next_norm`` = (weights, out, pad): the
-        last launch also writes the next norm of the output into ``out``."""
+        last launch also writes the next norm of the output into ``out``.
+        ``step_in``: the previous layer's deferred residual step (its
+        ``defer`` result), run inside this layer's QKV launch, which computes
+        the input norm itself (``x`` is that step's sum_out). ``defer``: leave
+        this layer's last residual step to the next layer's QKV launch and
+        return (y, step) instead of y. With ``fuse`` the post-attention step
+        runs inside the FFN's gate/up launch (``x_norm2`` is then not written)."""
         H, n = self.H, self.norms
-        if not normed:
-            rmsnorm(x, n["attn"], K=H, out=self.x_norm)
-        gemv_bf16(self.w_qkv, self.x_norm, self.qkv_out)
+        if step_in is not None:
+            gemv_bf16_addnorm(self.w_qkv, step_in["resid"], step_in["y"], sum_out=step_in["sum_out"],
+                              w_y=step_in["w_y"], scale=step_in["scale"], scale_mode=step_in["scale_mode"],
+                              w_x=n["attn"], Y=self.qkv_out)
+        else:
+            if not normed:
+                rmsnorm(x, n["attn"], K=H, out=self.x_norm)
+            gemv_bf16(self.w_qkv, self.x_norm, self.qkv_out)
         qkv_post(self.qkv_out, self.pos_dev, self.kcache, self.vcache, heads=self.heads, kv_heads=self.kv_heads,
                  D=self.D, k_off=self.q_size, v_off=self.q_size + self.k_size if self.sliding else -1,
                  q_w=n["q"], k_w=n["k"], norm_v=True, rope=self.rope, q_out=self.q_rope)
         attention(self.q_rope, self.kcache, self.vcache, self.pos_dev, heads=self.heads, window=self.window,
                   out=self.attn_out)
         gemv_bf16(self.w_o, self.attn_out, self.attn_proj)
-        add_norm(x, self.attn_proj, K=H, w_y=n["post_attn"], w_out=n["ffn"], norm_out=True, sum_out=self.x_post,
-                 norm_buf=self.x_norm2)
-        ffn_fused_bf16(self.ffn, self.x_norm2, self.down)
+        if self.fuse:
+            ffn_fused_bf16_addnorm(self.ffn, x, self.attn_proj, sum_out=self.x_post, w_y=n["post_attn"], w_x=n["ffn"],
+                                   Y=self.down)
+        else:
+            add_norm(x, self.attn_proj, K=H, w_y=n["post_attn"], w_out=n["ffn"], norm_out=True, sum_out=self.x_post,
+                     norm_buf=self.x_norm2)
+            ffn_fused_bf16(self.ffn, self.x_norm2, self.down)
+        if defer:
+            return self.y, {"resid": self.x_post, "y": self.down, "w_y": n["post_ffw"], "scale": self.scale,
+                            "scale_mode": 1, "sum_out": self.y}
         if next_norm is None:
             add_norm(self.x_post, self.down, K=H, w_y=n["post_ffw"], scale=self.scale, scale_mode=1, sum_out=self.y)
         else:
@@ -315,8 +378,9 @@ class Gemma4Decoder:
     needs nothing from the host: a captured step replays token after token."""
 
     def __init__(self, layers: list, embed_table: torch.Tensor, final_norm, head: Q4Weight, vocab: int,
-                 softcap: float = 30.0):
+                 softcap: float = 30.0, fuse: bool = True):
         self.layers = layers
+        self.fuse = fuse
         self.device = head.device
         self.H = layers[0].H
         self.pos_dev = layers[0].pos_dev
@@ -340,13 +404,20 @@ class Gemma4Decoder:
         embed(self.table, self.token_dev, self.scale, out=self.x)
         h = self.x
         n = len(self.layers)
-        # Each layer's last launch also writes the next layer's input norm (the
-        # final norm, zero-padded to the head's K, after the last layer).
+        # fuse: each layer's last residual step runs inside the next layer's QKV
+        # launch (which computes its input norm itself); the last layer's
+        # writes the final norm, zero-padded to the head's K. Unfused: each
+        # layer's last launch writes the next layer's input norm.
+        step = None
         for i, L in enumerate(self.layers):
             nxt = self.layers[i + 1] if i + 1 < n else None
+            if self.fuse and nxt is not None:
+                h, step = L.enqueue(h, normed=i > 0 and step is None, step_in=step, defer=True)
+                continue
             next_norm = ((nxt.norms["attn"], nxt.x_norm, self.H) if nxt is not None
                          else (self.final_norm, self.x_norm, self.head.K))
-            h = L.enqueue(h, normed=i > 0, next_norm=next_norm)
+            h = L.enqueue(h, normed=i > 0 and step is None, next_norm=next_norm, step_in=step)
+            step = None
         if n == 0:
             rmsnorm(h, self.final_norm, K=self.H, pad=self.head.K, out=self.x_norm)
         self.x_f32.copy_(self.x_norm)

@@ -302,6 +302,27 @@ int alv_add_norm(const uint16_t* resid, int ldr, const uint16_t* y, int ldy, con
                  int ld_norm, int rows, int K, int pad, float eps, void* stream);
 
 /*
+ * The residual step fused into the next one-token matmul: alv_add_norm of one
+ * row (resid, y, w_y, norm_y, scale, scale_mode -> sum_out; w_x the next
+ * norm's weights, pad = K) followed by alv_gemv_bf16 / alv_ffn_fused_bf16 of
+ * that norm at M = 1, in the matmul's own launch -- its workgroups compute the
+ * normalised activation themselves (the same float32 steps and numpy
+ * summation order, so every output bit equals the two-call sequence); no
+ * launch, and no activation round trip through memory, sits between them.
+ * This is how a decode layer moves from its attention output into the FFN
+ * (runtime/py/model.py:775-788 then :797-806; model.cpp:409-420 then the FFN)
+ * and from the FFN into the next layer's QKV (:783-788 then :705-713).
+ * K = the weight's K (the FFN's H), a multiple of 8 up to 8192; rows and
+ * weights 16-byte aligned; sum_out must not alias resid or y.
+ */
+int alv_gemv_bf16_addnorm(alv_weight_t w, const uint16_t* resid, const uint16_t* y, const float* w_y, int norm_y,
+                          float scale, int scale_mode, uint16_t* sum_out, const float* w_x, float eps, uint16_t* Y,
+                          void* stream);
+int alv_ffn_fused_bf16_addnorm(alv_ffn_t w, const uint16_t* resid, const uint16_t* y, const float* w_y, int norm_y,
+                               float scale, int scale_mode, uint16_t* sum_out, const float* w_x, float eps,
+                               uint16_t* Y, void* stream);
+
+/*
  * out[:H] = bf16(float(double(table_f16[*token_dev]) * scale)), the Gemma-4
  * embedding lookup with scale = sqrt(hidden_size) (runtime/py/model.py:889-891:
  * a float64 product cast to bf16 through float32). The token is read from

@@ -226,8 +226,11 @@ def test_ffn_fused_bf16(orc, dev, H, I, M):
 
 # ---- the whole layer, stage by stage (model.py:705-790) -----------------------------
 
-@pytest.mark.parametrize("sliding", [True, False])
-def test_gemma4_layer_stagewise(orc, dev, sliding):
+@pytest.mark.parametrize("sliding,fuse", [(True, True), (False, True), (True, False)])
+def test_gemma4_layer_stagewise(orc, dev, sliding, fuse):
+    """Every stage of a layer against the reference's arithmetic; fused, the
+    post-attention residual step runs inside the FFN's launch (x_norm2 is
+    then the reference's norm of the GPU's x_post, never written)."""
     from alveare_amd import layer
 
     H, I, S = 512, 1024, 64
@@ -243,7 +246,7 @@ def test_gemma4_layer_stagewise(orc, dev, sliding):
              for k in ("attn", "q", "k", "post_attn", "ffn", "post_ffw")}
     scale = np.float32(0.6)
     L = layer.Gemma4DecodeLayer(qkv=Wqkv, o=Wo, gate=Wg, up=Wu, down=Wd, norms=norms, scale=float(scale),
-                                sliding=sliding, H=H, I=I, max_seq=S, device=dev)
+                                sliding=sliding, H=H, I=I, max_seq=S, device=dev, fuse=fuse)
     table = qn.cos_sin_table_gemma(10000.0 if sliding else 1e6, D, S)
     kc = np.zeros((kv, S, D), np.float32)
     vc = np.zeros((kv, S, D), np.float32)
@@ -271,6 +274,8 @@ def test_gemma4_layer_stagewise(orc, dev, sliding):
         parity.gemv_bf16_check(orc, Wo, g["attn_out"], parity.bf16_bits(L.attn_proj), H, q_size)
         x_post = qn.bf16_rne(x + qn.rmsnorm_cpu(g["attn_proj"], norms["post_attn"]))
         assert np.array_equal(g["x_post"], x_post)
+        if fuse:
+            g["x_norm2"] = qn.rmsnorm_cpu(x_post, norms["ffn"])
         assert np.array_equal(g["x_norm2"], qn.rmsnorm_cpu(x_post, norms["ffn"]))
         # FFN from the GPU's x_norm2: the layer's bf16 FFN is the rounding of the
         # float32 FFN on the same input, which meets the flip-aware FFN bar.
@@ -316,6 +321,9 @@ def test_gemma4_decoder_step_and_graph(orc, dev):
     Wh = orc.synth_q4(V, H, 408)
     head = aa.Q4Weight(torch.from_numpy(Wh).to(dev), V, H)
     dec = layer.Gemma4Decoder(layers, torch.from_numpy(table_np).to(dev), fnorm, head, V, softcap=0.0)
+    # The same layers unfused (separate residual-step launches): the fused
+    # step must give every bit the unfused one gives.
+    ref = layer.Gemma4Decoder(layers, torch.from_numpy(table_np).to(dev), fnorm, head, V, softcap=0.0, fuse=False)
 
     def reset():
         torch.cuda.synchronize()
@@ -326,6 +334,22 @@ def test_gemma4_decoder_step_and_graph(orc, dev):
         pos_dev.fill_(0)
         torch.cuda.synchronize()
 
+    def reset_ref():
+        reset()
+        ref.token_dev.fill_(7)
+        torch.cuda.synchronize()
+
+    reset_ref()
+    unfused = []
+    for L in layers:
+        L.fuse = False
+    for step in range(4):
+        tok = ref.step()
+        torch.cuda.synchronize()
+        unfused.append((ref.logits.cpu().numpy().copy(), tok, [bf_np(L.y).copy() for L in layers]))
+    for L in layers:
+        L.fuse = True
+
     reset()
     eager = []
     for step in range(4):
@@ -333,6 +357,10 @@ def test_gemma4_decoder_step_and_graph(orc, dev):
         tok_in = int(dec.token_dev.item())
         tok = dec.step()
         torch.cuda.synchronize()
+        assert np.array_equal(dec.logits.cpu().numpy(), unfused[step][0]), f"step {step}: fused logits differ"
+        assert tok == unfused[step][1]
+        for L, y_ref in zip(layers, unfused[step][2]):
+            assert np.array_equal(bf_np(L.y), y_ref)
         x = (table_np[tok_in].astype(np.float32) * np.sqrt(H)).astype(np.float32)
         assert np.array_equal(bf_np(dec.x), qn.bf16_rne(x))
         xn = bf_np(dec.x_norm)
