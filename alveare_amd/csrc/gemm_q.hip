@@ -467,21 +467,6 @@ hipError_t launch_gemm_x(const GemmArgs& a, bool xf32, int tm, dim3 grid, hipStr
 
 }  // namespace
 
-namespace {
-
-int device_cus() {
-    static int cus[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cus[dev]) {
-        int n = 0;
-        cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
-    }
-    return cus[dev];
-}
-
-}  // namespace
-
 int launch_gemm_tiled(const GemvLaunch& L, hipStream_t s) {
     const uint64_t wbytes = L.tiled ? tile_bytes(L.N, L.K) : (uint64_t)L.N * (uint64_t)(L.K / 32) * kBlockBytes;
     // Lane offset + step offset of a load must not wrap 32 bits: weights below

@@ -33,6 +33,8 @@
 // graph replays for every token; positions at or past the cache length write
 // nothing and leave the outputs unchanged.
 #include <algorithm>
+#include <cstdlib>
+#include <type_traits>
 
 #include "q4_device.h"
 #include "q4_host.h"
@@ -271,24 +273,29 @@ __device__ __forceinline__ AttnSpan attn_span(const AttnArgs& a, int pos) {
     return {start, W, (W + kAttnChunk - 1) / kAttnChunk};
 }
 
-// Chunk c of kv head blockIdx.y for q heads [hg * blockIdx.z, + hg) of its
-// group. D is a template parameter so that every thread issues all of its K
-// and V loads (D/32 16-byte pieces each) before it needs any of them.
-template <int D>
+// Chunk c of kv head blockIdx.y for q heads [HG * blockIdx.z, + HG) of its
+// group. D and HG are template parameters so that every thread issues all of
+// its K and V loads (D/32 16-byte pieces each) before it needs any of them, and
+// the per-head loops carry no branches (a branch per head around each
+// multiply-add serialises its LDS read).
+template <int D, int HG>
 __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnArgs a) {
     constexpr int QD = D / 4;                // score slice per thread (4 threads per position)
     constexpr int NK = QD / 8;               // its 16-byte K pieces
     constexpr int DV = D / 8;                // 16-byte column pieces of a V row
     constexpr int PG = kAttnThreads / DV;    // position groups of the V sum
     constexpr int NV = kAttnChunk / PG;      // positions per thread in the V sum
-    __shared__ __align__(16) float qs[kAttnHeads * D];
-    __shared__ float es[kAttnHeads][kAttnChunk];
-    __shared__ float ms[kAttnHeads], ls[kAttnHeads];
-    __shared__ __align__(16) float red[8 * kAttnThreads * kAttnHeads];  // [pg][head][D]
+    // q in LDS, each head's quarters 4 floats apart so that the four threads
+    // of a position read different banks.
+    constexpr int QQ = QD + 4, QS = 4 * QQ;
+    __shared__ __align__(16) float qs[HG * QS];
+    __shared__ float es[HG][kAttnChunk];
+    __shared__ float ms[HG], ls[HG];
+    __shared__ __align__(16) float red[PG * HG * D];  // [pg][head][D]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = blockIdx.x, kvh = blockIdx.y;
-    const int g = a.heads / a.kv_heads, hg = a.hg;
-    const int h0 = blockIdx.z * hg;
+    const int g = a.heads / a.kv_heads;
+    const int h0 = blockIdx.z * HG;
     const int pos = *a.pos;
     if (pos < 0 || pos >= a.max_seq) return;
     const AttnSpan sp = attn_span(a, pos);
@@ -312,40 +319,47 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnArgs a) 
         }
     }
     const uint4* qv = reinterpret_cast<const uint4*>(a.q + ((size_t)kvh * g + h0) * D);
-    for (int i = tid; i < hg * DV; i += kAttnThreads) {
+    for (int i = tid; i < HG * DV; i += kAttnThreads) {
         float f[8];
         unpack8(qv[i], f);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qs[8 * i + e] = f[e];
+        const int h = i / DV, d = (i - h * DV) * 8;
+        float4* dst = reinterpret_cast<float4*>(qs + h * QS + (d / QD) * QQ + d % QD);
+        dst[0] = float4{f[0], f[1], f[2], f[3]};
+        dst[1] = float4{f[4], f[5], f[6], f[7]};
     }
     __syncthreads();
 
     // Scores: 4 threads per position, each a quarter of the row.
     {
-        float acc[kAttnHeads] = {0.0f, 0.0f, 0.0f, 0.0f};
-        const float* qp = qs + part * QD;
+        float acc[HG];
+#pragma unroll
+        for (int h = 0; h < HG; ++h) acc[h] = 0.0f;
 #pragma unroll
         for (int i = 0; i < NK; ++i) {
             float kf[8];
             unpack8(kreg[i], kf);
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
+            for (int h = 0; h < HG; ++h) {
+                const float4* qp = reinterpret_cast<const float4*>(qs + h * QS + part * QQ + i * 8);
+                const float4 q0 = qp[0], q1 = qp[1];
+                const float qf[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
-                for (int h = 0; h < kAttnHeads; ++h)
-                    if (h < hg) acc[h] = fmaf(kf[e], qp[h * D + i * 8 + e], acc[h]);
+                for (int e = 0; e < 8; ++e) acc[h] = fmaf(kf[e], qf[e], acc[h]);
+            }
         }
 #pragma unroll
-        for (int h = 0; h < kAttnHeads; ++h) {
+        for (int h = 0; h < HG; ++h) {
             float v = acc[h];
             v += __shfl_xor(v, 1);
             v += __shfl_xor(v, 2);
-            if (h < hg && part == 0) es[h][p] = p < np ? v * a.scale : -__builtin_inff();
+            if (part == 0) es[h][p] = p < np ? v * a.scale : -__builtin_inff();
         }
     }
     __syncthreads();
 
-    // The chunk's softmax pieces: one wave per head.
-    if (wave < hg) {
+    // The chunk's softmax pieces: one wave per head; positions past the
+    // chunk's end weigh zero.
+    if (wave < HG) {
         const int h = wave;
         const float s = es[h][lane];
         float m = s;
@@ -361,46 +375,45 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnArgs a) 
     }
     __syncthreads();
 
-    // Weighted V sum: thread (pg, dv) over positions pg, pg + PG, ...; the PG
-    // partial sums then added in order.
+    // Weighted V sum: thread (pg, dv) over positions pg, pg + PG, ... (those
+    // past the chunk's end weigh zero and read a valid row); the PG partial
+    // sums then added in order.
     {
-        float acc[kAttnHeads][8];
+        float acc[HG][8];
 #pragma unroll
-        for (int h = 0; h < kAttnHeads; ++h)
+        for (int h = 0; h < HG; ++h)
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int pp = pg + j * PG;
-            if (pp >= np) continue;
             float vf[8];
             unpack8(vreg[j], vf);
 #pragma unroll
-            for (int h = 0; h < kAttnHeads; ++h) {
-                if (h >= hg) continue;
+            for (int h = 0; h < HG; ++h) {
                 const float w = es[h][pp];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(w, vf[e], acc[h][e]);
             }
         }
 #pragma unroll
-        for (int h = 0; h < kAttnHeads; ++h) {
-            if (h >= hg) continue;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) red[((size_t)pg * hg + h) * D + dv * 8 + e] = acc[h][e];
+        for (int h = 0; h < HG; ++h) {
+            float4* dst = reinterpret_cast<float4*>(red + ((size_t)pg * HG + h) * D + dv * 8);
+            dst[0] = float4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+            dst[1] = float4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
         }
     }
     __syncthreads();
     constexpr int gstride = D + 2;
     float* out = a.part + (((size_t)kvh * a.nchunk + c) * g + h0) * gstride;
-    for (int i = tid; i < hg * D; i += kAttnThreads) {
+    for (int i = tid; i < HG * D; i += kAttnThreads) {
         const int h = i / D, d = i - h * D;
         float o = 0.0f;
 #pragma unroll
-        for (int q = 0; q < PG; ++q) o += red[((size_t)q * hg + h) * D + d];
+        for (int q = 0; q < PG; ++q) o += red[((size_t)q * HG + h) * D + d];
         out[(size_t)h * gstride + d] = o;
     }
-    if (tid < hg) {
+    if (tid < HG) {
         out[(size_t)tid * gstride + D] = ms[tid];
         out[(size_t)tid * gstride + D + 1] = ls[tid];
     }
@@ -409,7 +422,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnArgs a) 
 // Head blockIdx.x, columns [256 blockIdx.y, + 256): the chunks merged in order,
 // out = sum_c o_c f_c / sum_c l_c f_c with f_c = exp(m_c - max_c m_c).
 __global__ void __launch_bounds__(kAttnThreads) attn_merge_kernel(AttnArgs a) {
-    __shared__ float fs[kAttnMaxChunks];
+    __shared__ float fs[kAttnMaxChunks], lsum[kAttnMaxChunks];
     __shared__ float Ls;
     const int tid = threadIdx.x;
     const int hq = blockIdx.x;
@@ -419,7 +432,10 @@ __global__ void __launch_bounds__(kAttnThreads) attn_merge_kernel(AttnArgs a) {
     if (pos < 0 || pos >= a.max_seq) return;
     const int nch = attn_span(a, pos).nch;
     const float* base = a.part + ((size_t)kvh * a.nchunk * g + hl) * gstride;  // chunk q at + q * g * gstride
-    for (int q = tid; q < nch; q += kAttnThreads) fs[q] = base[(size_t)q * g * gstride + D];
+    for (int q = tid; q < nch; q += kAttnThreads) {
+        fs[q] = base[(size_t)q * g * gstride + D];
+        lsum[q] = base[(size_t)q * g * gstride + D + 1];
+    }
     __syncthreads();
     if (tid == 0) {
         float M = -__builtin_inff();
@@ -427,7 +443,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_merge_kernel(AttnArgs a) {
         float L = 0.0f;
         for (int q = 0; q < nch; ++q) {
             const float f = expf(fs[q] - M);
-            L = fmaf(base[(size_t)q * g * gstride + D + 1], f, L);
+            L = fmaf(lsum[q], f, L);
             fs[q] = f;
         }
         Ls = L;
@@ -653,19 +669,40 @@ extern "C" int alv_attention(const uint16_t* q, const uint16_t* kcache, const ui
     if (nchunk > kAttnMaxChunks)
         return fail(ALV_ERR_RANGE, "a span of %d positions exceeds the %d the merge takes", span, kAttnMaxChunks * kAttnChunk);
     const int g = heads / kv_heads;
-    const int hg = g % 4 == 0 ? 4 : (g % 2 == 0 ? 2 : 1);
+    // q heads per workgroup: the divisor of g (1, 2 or 4) whose grid at the
+    // longest span comes closest to one workgroup per CU (measured: 16 heads
+    // on one kv head of 512, 2048 positions: 13.5 us at 2 heads per
+    // workgroup, 14.6 at 1, 21.7 at 4; 8 kv heads of 256, window 1024: 10.3
+    // at 1, 11.1 at 2).
+    const int cus = device_cus();
+    int hg = 1;
+    for (int c = 2; c <= kAttnHeads; c *= 2) {
+        if (g % c) break;
+        const long grid_c = (long)nchunk * kv_heads * (g / c), grid_h = (long)nchunk * kv_heads * (g / hg);
+        if (std::labs(grid_c - cus) <= std::labs(grid_h - cus)) hg = c;
+    }
     const size_t part_bytes = (size_t)kv_heads * nchunk * g * (D + 2) * sizeof(float);
     void* sc = nullptr;
     if (int rc = get_scratch(s, kScratchAttn, part_bytes, &sc)) return rc;
     AttnArgs a{q, kcache, vcache, out, heads, kv_heads, D, max_seq, window, hg, scale, pos_dev, nchunk,
                static_cast<float*>(sc)};
     const dim3 grid(nchunk, kv_heads, g / hg);
+    const void* k = nullptr;
+    auto pick = [&](auto d) {
+        constexpr int DD = decltype(d)::value;
+        k = hg == 4 ? reinterpret_cast<const void*>(&attn_partial_kernel<DD, 4>)
+                    : hg == 2 ? reinterpret_cast<const void*>(&attn_partial_kernel<DD, 2>)
+                              : reinterpret_cast<const void*>(&attn_partial_kernel<DD, 1>);
+    };
     switch (D) {
-        case 64: hipLaunchKernelGGL(attn_partial_kernel<64>, grid, dim3(kAttnThreads), 0, s, a); break;
-        case 128: hipLaunchKernelGGL(attn_partial_kernel<128>, grid, dim3(kAttnThreads), 0, s, a); break;
-        case 256: hipLaunchKernelGGL(attn_partial_kernel<256>, grid, dim3(kAttnThreads), 0, s, a); break;
-        default: hipLaunchKernelGGL(attn_partial_kernel<512>, grid, dim3(kAttnThreads), 0, s, a); break;
+        case 64: pick(std::integral_constant<int, 64>{}); break;
+        case 128: pick(std::integral_constant<int, 128>{}); break;
+        case 256: pick(std::integral_constant<int, 256>{}); break;
+        default: pick(std::integral_constant<int, 512>{}); break;
     }
+    void* kargs[] = {&a};
+    if (int rc = hip_check(hipLaunchKernel(k, grid, dim3(kAttnThreads), kargs, 0, s), "attn_partial_kernel launch"))
+        return rc;
     if (int rc = hip_check(hipGetLastError(), "attn_partial_kernel launch")) return rc;
     hipLaunchKernelGGL(attn_merge_kernel, dim3(heads, (D + kAttnThreads - 1) / kAttnThreads), dim3(kAttnThreads), 0, s, a);
     return hip_check(hipGetLastError(), "attn_merge_kernel launch");

@@ -141,6 +141,8 @@ int small_tile_max_m();
 // Workgroups per CU the 64-token prefill tiles aim at when splitting K
 // (default 1); ALV_GEMM_SMALL_WG_PER_CU overrides.
 int small_wg_per_cu();
+// Compute units of the current device (cached per device).
+int device_cus();
 
 // The two launches of one FFN call on handle w (ffn_fused.hip): gate/up with
 // the GLU epilogue into the bf16 activation `act`, then down from it.

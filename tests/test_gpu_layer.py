@@ -138,6 +138,25 @@ def test_attention_bound(dev, sliding, pos):
     assert mism <= 16 * D // 50
 
 
+@pytest.mark.parametrize("D,kv,S,window,pos", [(512, 1, 65536, 0, 60000), (128, 4, 4096, 0, 3000),
+                                                (64, 16, 2048, 512, 1800), (128, 2, 1024, 0, 0)])
+def test_attention_head_groups(dev, D, kv, S, window, pos):
+    """Other head widths and the other head groupings per workgroup (4 q
+    heads over a 65536-position cache, 4 at D 128, 1 with one q head per kv
+    head) within the same bound."""
+    from alveare_amd import layer
+
+    _say(f"attention D={D} kv={kv} S={S} window={window} pos={pos}")
+    rng = np.random.default_rng(D + kv + pos)
+    kc = rnd_bf16(rng, (kv, S, D), 1.0)
+    vc = rnd_bf16(rng, (kv, S, D), 1.0)
+    q = rnd_bf16(rng, 16 * D, 0.15)
+    pos_dev = torch.tensor([pos], dtype=torch.int32, device=dev)
+    out = layer.attention(bf_dev(q, dev), bf_dev(kc, dev), bf_dev(vc, dev), pos_dev, heads=16, window=window)
+    mism = _attn_check(q, kc, vc, pos, 16, kv, D, window, parity.bf16_bits(out))
+    assert mism <= 16 * D // 50
+
+
 # ---- residual steps (model.py:775-788; model.cpp:409-420) ---------------------------
 
 @pytest.mark.parametrize("mode,norm_y,norm_out,K,pad", [(0, True, True, 3840, 4096), (1, True, False, 3840, 4096),
