@@ -285,8 +285,8 @@ __device__ void fused_resid_step(const Gemv1Args& a, const WgWork& wk, __bf16* x
         if (in)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float t = __fmul_rn(f[e], inv2);
-                xb[e] = bf16_rne_bits(a.pr_wx ? __fmul_rn(t, wx[e]) : t);
+                const float t = mul_rn(f[e], inv2);
+                xb[e] = bf16_rne_bits(a.pr_wx ? mul_rn(t, wx[e]) : t);
             }
         const int sl = (v >> 6) * 64 + ((v & 15) << 2) + ((v >> 4) & 3);
         *reinterpret_cast<uint4*>(xs + (size_t)sl * 8) = pack8(xb);

@@ -13,8 +13,8 @@
 //
 // Bit-exact parts. The reference computes with numpy in float32 on bf16
 // arrays. Every elementwise step here is the same float32 operation with the
-// same rounding (products and sums written with the _rn intrinsics so that
-// nothing contracts into an FMA), and the one reduction whose order matters at
+// same rounding (floating-point contraction is off in this file: nothing
+// fuses a product and a sum into one FMA), and the one reduction whose order matters at
 // bf16 output precision -- np.mean(x ** 2) of RMSNorm -- is numpy's own
 // summation order (row_norm.h).
 //
@@ -39,6 +39,9 @@
 #include "q4_device.h"
 #include "q4_host.h"
 #include "row_norm.h"
+
+#pragma clang fp contract(off)
+
 
 namespace alv {
 
@@ -88,8 +91,8 @@ __device__ void write_norm(const float* xs, int K, int pad, float inv, const flo
                 }
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float t = __fmul_rn(xs[8 * v + e], inv);
-                    b[e] = bf16_rne_bits(w ? __fmul_rn(t, wf[e]) : t);
+                    const float t = mul_rn(xs[8 * v + e], inv);
+                    b[e] = bf16_rne_bits(w ? mul_rn(t, wf[e]) : t);
                 }
             }
             reinterpret_cast<uint4*>(out)[v] = pack8(b);
@@ -98,8 +101,8 @@ __device__ void write_norm(const float* xs, int K, int pad, float inv, const flo
         for (int i = tid; i < pad; i += kRowThreads) {
             uint16_t b = 0;
             if (i < K) {
-                const float t = __fmul_rn(xs[i], inv);
-                b = bf16_rne_bits(w ? __fmul_rn(t, w[i]) : t);
+                const float t = mul_rn(xs[i], inv);
+                b = bf16_rne_bits(w ? mul_rn(t, w[i]) : t);
             }
             out[i] = b;
         }
@@ -145,8 +148,8 @@ __global__ void __launch_bounds__(kRowThreads) rmsnorm_kernel(const uint16_t* x,
             if (8 * v < K)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float t = __fmul_rn(f[i][e], inv);
-                    b[e] = bf16_rne_bits(w ? __fmul_rn(t, wv[i][e]) : t);
+                    const float t = mul_rn(f[i][e], inv);
+                    b[e] = bf16_rne_bits(w ? mul_rn(t, wv[i][e]) : t);
                 }
             reinterpret_cast<uint4*>(o)[v] = pack8(b);
         }
@@ -215,13 +218,13 @@ __global__ void __launch_bounds__(kRowThreads) qkv_post_kernel(QkvPostArgs a) {
             for (int j = 0; j < 2; ++j) {
                 const int i = tid + j * kRowThreads;
                 if (i >= D) continue;
-                const float t = __fmul_rn(xs[i], inv);
-                xs[i] = bf16r(w ? __fmul_rn(t, wv[j]) : t);
+                const float t = mul_rn(xs[i], inv);
+                xs[i] = bf16r(w ? mul_rn(t, wv[j]) : t);
             }
         } else {
             for (int i = tid; i < D; i += kRowThreads) {
-                const float t = __fmul_rn(xs[i], inv);
-                xs[i] = bf16r(w ? __fmul_rn(t, w[i]) : t);
+                const float t = mul_rn(xs[i], inv);
+                xs[i] = bf16r(w ? mul_rn(t, w[i]) : t);
             }
         }
         __syncthreads();
@@ -234,8 +237,8 @@ __global__ void __launch_bounds__(kRowThreads) qkv_post_kernel(QkvPostArgs a) {
             const float c = pre ? cv : bf16_bits_to_f32(rrow[a.cos_off + i]);
             const float s = pre ? sv : bf16_bits_to_f32(rrow[a.sin_off + i]);
             const float x1 = xs[i], x2 = xs[i + a.half];
-            dst[i] = bf16_rne_bits(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s)));
-            dst[i + a.half] = bf16_rne_bits(__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s)));
+            dst[i] = bf16_rne_bits(sub_rn(mul_rn(x1, c), mul_rn(x2, s)));
+            dst[i + a.half] = bf16_rne_bits(add_rn(mul_rn(x2, c), mul_rn(x1, s)));
         }
         for (int i = 2 * a.half + tid; i < D; i += kRowThreads) dst[i] = bf16_rne_bits(xs[i]);
     } else {
@@ -541,8 +544,8 @@ __global__ void __launch_bounds__(kRowThreads) add_norm_kernel(AddNormArgs a) {
             if (8 * v < K)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float t = __fmul_rn(f[i][e], inv2);
-                    b[e] = bf16_rne_bits(a.w_out ? __fmul_rn(t, wo[i][e]) : t);
+                    const float t = mul_rn(f[i][e], inv2);
+                    b[e] = bf16_rne_bits(a.w_out ? mul_rn(t, wo[i][e]) : t);
                 }
             reinterpret_cast<uint4*>(no)[v] = pack8(b);
         }

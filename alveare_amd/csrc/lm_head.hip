@@ -52,7 +52,7 @@ __device__ __forceinline__ float head_logit(float y, float cap) {
     if (!(cap > 0.0f)) return l;
     const float q = __fdiv_rn(l, cap);
     const float t = (float)tanh((double)q);
-    return __fmul_rn(cap, t);
+    return cap * t;
 }
 
 // Fold (v, i) across the workgroup in a fixed tree: shuffles within each

@@ -14,13 +14,30 @@
 // the leaves are summed with 8 lanes each and the halves combined across lanes
 // in the recursion's own tree; other widths follow the recursion on one lane.
 // numpy >= 2 evaluates the scalar steps (mean = sum / n, 1 / sqrt(var + eps))
-// in float32, as here.
+// in float32, as here. Every product and sum goes through add_rn / mul_rn,
+// which no FMA contraction can fuse (one rounding where numpy makes two).
 #pragma once
 
 #include "q4_device.h"
 
 namespace alv {
 namespace {
+
+// float32 +, -, * rounded on their own: compiled with contraction off, so
+// that no product and sum that use them fuse into one FMA (HIP's
+// __fmul_rn / __fadd_rn are plain operators that do fuse).
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a + b;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a - b;
+}
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
 
 __device__ __forceinline__ uint16_t bf16_rne_bits(float v) {
     if (v != v) return 0x7FC0u;
@@ -30,7 +47,7 @@ __device__ __forceinline__ uint16_t bf16_rne_bits(float v) {
 
 __device__ __forceinline__ float bf16r(float v) { return bf16_bits_to_f32(bf16_rne_bits(v)); }
 
-__device__ __forceinline__ float sqv(const float* a, int i) { return __fmul_rn(a[i], a[i]); }
+__device__ __forceinline__ float sqv(const float* a, int i) { return mul_rn(a[i], a[i]); }
 
 // ---- numpy's pairwise float32 sum of squares ---------------------------------------
 
@@ -38,7 +55,7 @@ __device__ __forceinline__ float sqv(const float* a, int i) { return __fmul_rn(a
 __device__ float pw_leaf_sq(const float* a, int n) {
     if (n < 8) {
         float r = 0.0f;
-        for (int i = 0; i < n; ++i) r = __fadd_rn(r, sqv(a, i));
+        for (int i = 0; i < n; ++i) r = add_rn(r, sqv(a, i));
         return r;
     }
     float r[8];
@@ -47,11 +64,11 @@ __device__ float pw_leaf_sq(const float* a, int n) {
     int i = 8;
     for (; i < n - (n % 8); i += 8) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) r[j] = __fadd_rn(r[j], sqv(a, i + j));
+        for (int j = 0; j < 8; ++j) r[j] = add_rn(r[j], sqv(a, i + j));
     }
-    float res = __fadd_rn(__fadd_rn(__fadd_rn(r[0], r[1]), __fadd_rn(r[2], r[3])),
-                          __fadd_rn(__fadd_rn(r[4], r[5]), __fadd_rn(r[6], r[7])));
-    for (; i < n; ++i) res = __fadd_rn(res, sqv(a, i));
+    float res = add_rn(add_rn(add_rn(r[0], r[1]), add_rn(r[2], r[3])),
+                       add_rn(add_rn(r[4], r[5]), add_rn(r[6], r[7])));
+    for (; i < n; ++i) res = add_rn(res, sqv(a, i));
     return res;
 }
 
@@ -86,7 +103,7 @@ __device__ float pw_serial_sq(const float* a, int n, PwFrame* st) {
             st[sp + 1] = {f.off + n2, f.n - n2, 0, 0.0f};
             ++sp;
         } else {
-            ret = __fadd_rn(f.left, ret);
+            ret = add_rn(f.left, ret);
             --sp;
         }
     }
@@ -121,17 +138,17 @@ __device__ __forceinline__ float pw_chunk_sq(const float* a, int n, float* red, 
             float r = 0.0f;
             if (act && leaf >= 8) {
                 r = sqv(p, j);
-                for (int i = 8 + j; i < m8; i += 8) r = __fadd_rn(r, sqv(p, i));
+                for (int i = 8 + j; i < m8; i += 8) r = add_rn(r, sqv(p, i));
             }
-            r = __fadd_rn(r, __shfl_xor(r, 1));
-            r = __fadd_rn(r, __shfl_xor(r, 2));
-            r = __fadd_rn(r, __shfl_xor(r, 4));
+            r = add_rn(r, __shfl_xor(r, 1));
+            r = add_rn(r, __shfl_xor(r, 2));
+            r = add_rn(r, __shfl_xor(r, 4));
             if (act && j == 0) {
                 if (leaf < 8) {
                     r = 0.0f;
-                    for (int i = 0; i < leaf; ++i) r = __fadd_rn(r, sqv(p, i));
+                    for (int i = 0; i < leaf; ++i) r = add_rn(r, sqv(p, i));
                 } else {
-                    for (int i = m8; i < leaf; ++i) r = __fadd_rn(r, sqv(p, i));
+                    for (int i = m8; i < leaf; ++i) r = add_rn(r, sqv(p, i));
                 }
                 red[lf] = r;
             }
@@ -141,7 +158,7 @@ __device__ __forceinline__ float pw_chunk_sq(const float* a, int n, float* red, 
             float v = tid < leaves ? red[tid] : 0.0f;
             for (int s = 1; s < leaves; s *= 2) {
                 const float o = __shfl_down(v, s);
-                if ((tid & (2 * s - 1)) == 0) v = __fadd_rn(v, o);
+                if ((tid & (2 * s - 1)) == 0) v = add_rn(v, o);
             }
             if (tid == 0) red[64] = v;
         }
@@ -159,11 +176,12 @@ template <int NT>
 __device__ __forceinline__ float rms_inv(const float* xs, int K, float eps, float* red, int tid) {
     constexpr int kBuf = 8192;
     float s = pw_chunk_sq<NT>(xs, min(K, kBuf), red, tid);
-    for (int off = kBuf; off < K; off += kBuf) s = __fadd_rn(s, pw_chunk_sq<NT>(xs + off, min(K - off, kBuf), red, tid));
+    for (int off = kBuf; off < K; off += kBuf)
+        s = add_rn(s, pw_chunk_sq<NT>(xs + off, min(K - off, kBuf), red, tid));
     const float var = __fdiv_rn(s, (float)K);
     // sqrtf is the correctly rounded square root here (v_sqrt_f32 plus a
     // neighbour test); __fsqrt_rn compiles to the bare 1-ulp v_sqrt_f32.
-    return __fdiv_rn(1.0f, sqrtf(__fadd_rn(var, eps)));
+    return __fdiv_rn(1.0f, sqrtf(add_rn(var, eps)));
 }
 
 __device__ __forceinline__ void unpack8(uint4 v, float (&f)[8]) {
@@ -200,12 +218,12 @@ __device__ __forceinline__ float resid_step(float x, float r, float w, float inv
                                             int scale_mode, float scale) {
     float t = x;
     if (norm_y) {
-        t = __fmul_rn(t, inv);
-        t = bf16r(has_w ? __fmul_rn(t, w) : t);
+        t = mul_rn(t, inv);
+        t = bf16r(has_w ? mul_rn(t, w) : t);
     }
-    const float sum = __fadd_rn(r, t);
-    if (scale_mode == 1) return bf16r(__fmul_rn(bf16r(sum), scale));
-    if (scale_mode == 2) return bf16r(__fmul_rn(sum, scale));
+    const float sum = add_rn(r, t);
+    if (scale_mode == 1) return bf16r(mul_rn(bf16r(sum), scale));
+    if (scale_mode == 2) return bf16r(mul_rn(sum, scale));
     return bf16r(sum);
 }
 
