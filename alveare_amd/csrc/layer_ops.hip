@@ -677,9 +677,12 @@ extern "C" int alv_attention(const uint16_t* q, const uint16_t* kcache, const ui
     // on one kv head of 512, 2048 positions: 13.5 us at 2 heads per
     // workgroup, 14.6 at 1, 21.7 at 4; 8 kv heads of 256, window 1024: 10.3
     // at 1, 11.1 at 2).
+    // (At D = 512 at most 2: four heads' accumulators beside every K and V
+    // load of the chunk would spill.)
     const int cus = device_cus();
+    const int max_hg = D == 512 ? 2 : kAttnHeads;
     int hg = 1;
-    for (int c = 2; c <= kAttnHeads; c *= 2) {
+    for (int c = 2; c <= max_hg; c *= 2) {
         if (g % c) break;
         const long grid_c = (long)nchunk * kv_heads * (g / c), grid_h = (long)nchunk * kv_heads * (g / hg);
         if (std::labs(grid_c - cus) <= std::labs(grid_h - cus)) hg = c;
@@ -693,9 +696,14 @@ extern "C" int alv_attention(const uint16_t* q, const uint16_t* kcache, const ui
     const void* k = nullptr;
     auto pick = [&](auto d) {
         constexpr int DD = decltype(d)::value;
-        k = hg == 4 ? reinterpret_cast<const void*>(&attn_partial_kernel<DD, 4>)
-                    : hg == 2 ? reinterpret_cast<const void*>(&attn_partial_kernel<DD, 2>)
-                              : reinterpret_cast<const void*>(&attn_partial_kernel<DD, 1>);
+        if constexpr (DD < 512) {
+            if (hg == 4) {
+                k = reinterpret_cast<const void*>(&attn_partial_kernel<DD, 4>);
+                return;
+            }
+        }
+        k = hg == 2 ? reinterpret_cast<const void*>(&attn_partial_kernel<DD, 2>)
+                    : reinterpret_cast<const void*>(&attn_partial_kernel<DD, 1>);
     };
     switch (D) {
         case 64: pick(std::integral_constant<int, 64>{}); break;

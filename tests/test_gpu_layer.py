@@ -141,9 +141,9 @@ def test_attention_bound(dev, sliding, pos):
 @pytest.mark.parametrize("D,kv,S,window,pos", [(512, 1, 65536, 0, 60000), (128, 4, 4096, 0, 3000),
                                                 (64, 16, 2048, 512, 1800), (128, 2, 1024, 0, 0)])
 def test_attention_head_groups(dev, D, kv, S, window, pos):
-    """Other head widths and the other head groupings per workgroup (4 q
-    heads over a 65536-position cache, 4 at D 128, 1 with one q head per kv
-    head) within the same bound."""
+    """Other head widths and the other head groupings per workgroup (2 q
+    heads of 512 over a 65536-position cache, 1024 chunks to merge; 4 at
+    D 128; 1 with one q head per kv head) within the same bound."""
     from alveare_amd import layer
 
     _say(f"attention D={D} kv={kv} S={S} window={window} pos={pos}")
