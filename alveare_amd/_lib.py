@@ -50,6 +50,8 @@ SIGNATURES: dict[str, tuple] = {
     "alv_qkv_post": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _i, ctypes.c_float, _vp, _i, _i, _i, _i,
                           _vp, _i, _vp, _vp, _vp, _vp]),
     "alv_attention": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, ctypes.c_float, _vp, _vp]),
+    "alv_qkv_attention": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _i, ctypes.c_float, _vp, _i, _i, _i, _i,
+                               _vp, _i, _vp, _vp, _vp, _i, ctypes.c_float, _vp, _vp]),
     "alv_embed": (_i, [_vp, _i, _i, _vp, ctypes.c_double, _vp, _vp]),
     "alv_add_norm": (_i, [_vp, _i, _vp, _i, _vp, _i, ctypes.c_float, _i, _vp, _i, _vp, _vp, _i, _i, _i, _i,
                           ctypes.c_float, _vp]),

@@ -263,6 +263,9 @@ struct AttnArgs {
     const int* pos;
     int nchunk;          // grid.x: chunks the largest window can need
     float* part;         // [kv_heads][nchunk][g][D + 2]: weighted V sums, max, exp-sum
+    // Fused q/k/v post-processing (alv_qkv_attention): the QKV projection's
+    // output in place of q, and alv_qkv_post's parameters.
+    QkvPostArgs post;
 };
 
 struct AttnSpan {
@@ -281,7 +284,14 @@ __device__ __forceinline__ AttnSpan attn_span(const AttnArgs& a, int pos) {
 // its K and V loads (D/32 16-byte pieces each) before it needs any of them, and
 // the per-head loops carry no branches (a branch per head around each
 // multiply-add serialises its LDS read).
-template <int D, int HG>
+// FQ: the q/k/v post-processing of alv_qkv_post runs here, per workgroup,
+// while the chunk's K and V loads are in flight: every workgroup normalises
+// and rotates its HG q heads from the QKV output (each wave a row, the
+// pairwise sums wave-wide), and the workgroups of the chunk that holds pos
+// also the kv head's k and v rows, which they use in place of the cache row
+// they loaded (workgroup z = 0 writes them into the caches; chunk 0 writes
+// the rotated q). Bit for bit alv_qkv_post's arithmetic.
+template <int D, int HG, bool FQ>
 __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnArgs a) {
     constexpr int QD = D / 4;                // score slice per thread (4 threads per position)
     constexpr int NK = QD / 8;               // its 16-byte K pieces
@@ -307,6 +317,44 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnArgs a) 
     const int np = min(kAttnChunk, sp.W - p0);
     const size_t row0 = (size_t)kvh * a.max_seq + sp.start + p0;
 
+    // Fused post-processing: the rows this workgroup normalises, loaded
+    // before the K and V loads (a wait for them then waits for nothing else).
+    constexpr int RW = D / 64;  // row elements per lane, lane l: [RW l, RW l + RW)
+    const bool lastc = c == sp.nch - 1;
+    const int nrows = FQ ? HG + (lastc ? 2 : 0) : 0;
+    __shared__ __align__(16) uint16_t kvn[2][D];  // the new k and v rows (bf16)
+    // Raw bits only: every load unconditional (addresses of unused values
+    // clamped to valid memory) and nothing converted until the K and V loads
+    // are issued, so that no wait for these loads comes before them.
+    uint32_t xraw[2][RW], wraw[2][RW], craw[2][RW], sraw[2][RW];
+    int role[2], hrow[2];
+    if constexpr (FQ) {
+        const QkvPostArgs& pa = a.post;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int r = wave + 4 * t;
+            // role 0: q head kvh g + h0 + r; 1: k of kv head kvh; 2: v (raw k when v_off < 0)
+            role[t] = r < HG ? 0 : (r == HG ? 1 : 2);
+            hrow[t] = role[t] == 0 ? kvh * g + h0 + r : kvh;
+            const int src = role[t] == 0 ? hrow[t] * D
+                                         : (role[t] == 1 || pa.v_off < 0 ? pa.k_off + kvh * D : pa.v_off + kvh * D);
+            const float* w = role[t] == 0 ? pa.q_w : (role[t] == 1 ? pa.k_w : nullptr);
+            const uint32_t* wp = w ? reinterpret_cast<const uint32_t*>(w) : reinterpret_cast<const uint32_t*>(pa.qkv);
+            const uint16_t* rr = pa.rope ? pa.rope + (size_t)pos * pa.rope_stride : pa.qkv;
+            const int co = pa.rope ? pa.cos_off : 0, so = pa.rope ? pa.sin_off : 0, hf = pa.rope ? pa.half : 1;
+#pragma unroll
+            for (int e = 0; e < RW; ++e) {
+                const int d = RW * lane + e;
+                const int i = d % hf;
+                xraw[t][e] = pa.qkv[src + d];
+                wraw[t][e] = wp[w ? d : 0];
+                craw[t][e] = rr[co + i];
+                sraw[t][e] = rr[so + i];
+            }
+        }
+        asm volatile("" ::: "memory");  // these loads go out before the K and V loads
+    }
+
     // Every load of the workgroup up front: K slices, V pieces, q.
     const int p = tid >> 2, part = tid & 3;
     const int dv = tid % DV, pg = tid / DV;
@@ -321,16 +369,84 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnArgs a) 
             vreg[j] = reinterpret_cast<const uint4*>(a.vcache + (row0 + pp) * D)[dv];
         }
     }
-    const uint4* qv = reinterpret_cast<const uint4*>(a.q + ((size_t)kvh * g + h0) * D);
-    for (int i = tid; i < HG * DV; i += kAttnThreads) {
-        float f[8];
-        unpack8(qv[i], f);
-        const int h = i / DV, d = (i - h * DV) * 8;
-        float4* dst = reinterpret_cast<float4*>(qs + h * QS + (d / QD) * QQ + d % QD);
-        dst[0] = float4{f[0], f[1], f[2], f[3]};
-        dst[1] = float4{f[4], f[5], f[6], f[7]};
+    if constexpr (FQ) {
+        // Each wave its rows: the float row in LDS (red is free until the V
+        // sum), the wave-wide pairwise sum, the norm, RoPE from the row.
+        const QkvPostArgs& pa = a.post;
+        float* rowb = red + wave * D;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            if (wave + 4 * t >= nrows) break;
+            const int norm = role[t] == 0 ? pa.norm_q : (role[t] == 1 ? pa.norm_k : pa.norm_v);
+            const bool hasw = role[t] == 0 ? pa.q_w != nullptr : (role[t] == 1 ? pa.k_w != nullptr : false);
+            float xrow[RW], crow[RW], srow[RW];
+#pragma unroll
+            for (int e = 0; e < RW; ++e) {
+                xrow[e] = bf16_bits_to_f32(xraw[t][e]);
+                crow[e] = bf16_bits_to_f32(craw[t][e]);
+                srow[e] = bf16_bits_to_f32(sraw[t][e]);
+                rowb[RW * lane + e] = xrow[e];
+            }
+            if (norm) {
+                const float inv = rms_inv_wave(rowb, D, pa.eps, lane);
+#pragma unroll
+                for (int e = 0; e < RW; ++e) {
+                    const float tt = mul_rn(xrow[e], inv);
+                    rowb[RW * lane + e] = bf16r(hasw ? mul_rn(tt, __builtin_bit_cast(float, wraw[t][e])) : tt);
+                }
+            }
+            uint16_t ob[RW];
+            const bool rot = role[t] < 2 && pa.rope;
+#pragma unroll
+            for (int e = 0; e < RW; ++e) {
+                const int d = RW * lane + e;
+                float y = rowb[d];
+                if (rot && d < 2 * pa.half) {
+                    // run_rope_cpu_gemma (model.py:549-575): y1 = x1 c - x2 s, y2 = x2 c + x1 s.
+                    const int i = d < pa.half ? d : d - pa.half;
+                    y = d < pa.half ? sub_rn(mul_rn(rowb[i], crow[e]), mul_rn(rowb[i + pa.half], srow[e]))
+                                    : add_rn(mul_rn(rowb[d], crow[e]), mul_rn(rowb[i], srow[e]));
+                }
+                ob[e] = bf16_rne_bits(y);
+            }
+#pragma unroll
+            for (int e = 0; e < RW; ++e) {
+                const int d = RW * lane + e;
+                if (role[t] == 0) {
+                    const int hl = hrow[t] - kvh * g - h0;
+                    qs[hl * QS + (d / QD) * QQ + d % QD] = bf16_bits_to_f32(ob[e]);
+                    if (c == 0 && pa.q_out) pa.q_out[(size_t)hrow[t] * D + d] = ob[e];
+                } else {
+                    kvn[role[t] - 1][d] = ob[e];
+                    if (blockIdx.z == 0)
+                        (role[t] == 1 ? pa.kcache : pa.vcache)[((size_t)kvh * a.max_seq + pos) * D + d] = ob[e];
+                }
+            }
+        }
+    } else {
+        const uint4* qv = reinterpret_cast<const uint4*>(a.q + ((size_t)kvh * g + h0) * D);
+        for (int i = tid; i < HG * DV; i += kAttnThreads) {
+            float f[8];
+            unpack8(qv[i], f);
+            const int h = i / DV, d = (i - h * DV) * 8;
+            float4* dst = reinterpret_cast<float4*>(qs + h * QS + (d / QD) * QQ + d % QD);
+            dst[0] = float4{f[0], f[1], f[2], f[3]};
+            dst[1] = float4{f[4], f[5], f[6], f[7]};
+        }
     }
     __syncthreads();
+    if constexpr (FQ) {
+        // The chunk that holds pos: its last row (and every clamped load of
+        // it) is the new k and v, not what the cache held.
+        if (lastc) {
+            if (p >= np - 1)
+#pragma unroll
+                for (int i = 0; i < NK; ++i) kreg[i] = reinterpret_cast<const uint4*>(kvn[0] + part * QD)[i];
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+                if (pg + j * PG >= np - 1) vreg[j] = reinterpret_cast<const uint4*>(kvn[1])[dv];
+        }
+    }
 
     // Scores: 4 threads per position, each a quarter of the row.
     {
@@ -655,19 +771,14 @@ extern "C" int alv_qkv_post(const uint16_t* qkv, int k_off, int v_off, int heads
     return hip_check(hipGetLastError(), "qkv_post_kernel launch");
 }
 
-extern "C" int alv_attention(const uint16_t* q, const uint16_t* kcache, const uint16_t* vcache, uint16_t* out,
-                             int heads, int kv_heads, int D, int max_seq, int window, float scale, const int* pos_dev,
-                             void* stream) {
-    if (!q || !kcache || !vcache || !out || !pos_dev) return fail(ALV_ERR_ARG, "null pointer");
-    if (heads < 1 || kv_heads < 1 || heads % kv_heads || (D != 64 && D != 128 && D != 256 && D != 512) ||
-        max_seq < 1 || window < 0)
-        return fail(ALV_ERR_ARG, "bad attention shape heads=%d kv_heads=%d D=%d max_seq=%d window=%d "
-                    "(D one of 64, 128, 256, 512)", heads, kv_heads, D, max_seq, window);
-    if (reinterpret_cast<uintptr_t>(kcache) % 16 || reinterpret_cast<uintptr_t>(vcache) % 16 ||
-        reinterpret_cast<uintptr_t>(q) % 16 || reinterpret_cast<uintptr_t>(out) % 2)
-        return fail(ALV_ERR_ALIGN, "q, kcache and vcache need 16-byte alignment");
-    hipStream_t s = (hipStream_t)stream;
-    const int span = window > 0 ? std::min(window, max_seq) : max_seq;
+namespace alv {
+namespace {
+
+// The attention launches for args a (q or the fused post-processing already
+// set): the head group, the partial kernel, the merge.
+int launch_attention(AttnArgs& a, bool fused, hipStream_t s) {
+    const int heads = a.heads, kv_heads = a.kv_heads, D = a.D;
+    const int span = a.window > 0 ? std::min(a.window, a.max_seq) : a.max_seq;
     const int nchunk = (span + kAttnChunk - 1) / kAttnChunk;
     if (nchunk > kAttnMaxChunks)
         return fail(ALV_ERR_RANGE, "a span of %d positions exceeds the %d the merge takes", span, kAttnMaxChunks * kAttnChunk);
@@ -690,33 +801,107 @@ extern "C" int alv_attention(const uint16_t* q, const uint16_t* kcache, const ui
     const size_t part_bytes = (size_t)kv_heads * nchunk * g * (D + 2) * sizeof(float);
     void* sc = nullptr;
     if (int rc = get_scratch(s, kScratchAttn, part_bytes, &sc)) return rc;
-    AttnArgs a{q, kcache, vcache, out, heads, kv_heads, D, max_seq, window, hg, scale, pos_dev, nchunk,
-               static_cast<float*>(sc)};
+    a.hg = hg;
+    a.nchunk = nchunk;
+    a.part = static_cast<float*>(sc);
     const dim3 grid(nchunk, kv_heads, g / hg);
     const void* k = nullptr;
-    auto pick = [&](auto d) {
+    auto pick = [&](auto d, auto f) {
         constexpr int DD = decltype(d)::value;
+        constexpr bool FQ = decltype(f)::value;
         if constexpr (DD < 512) {
             if (hg == 4) {
-                k = reinterpret_cast<const void*>(&attn_partial_kernel<DD, 4>);
+                k = reinterpret_cast<const void*>(&attn_partial_kernel<DD, 4, FQ>);
                 return;
             }
         }
-        k = hg == 2 ? reinterpret_cast<const void*>(&attn_partial_kernel<DD, 2>)
-                    : reinterpret_cast<const void*>(&attn_partial_kernel<DD, 1>);
+        k = hg == 2 ? reinterpret_cast<const void*>(&attn_partial_kernel<DD, 2, FQ>)
+                    : reinterpret_cast<const void*>(&attn_partial_kernel<DD, 1, FQ>);
     };
-    switch (D) {
-        case 64: pick(std::integral_constant<int, 64>{}); break;
-        case 128: pick(std::integral_constant<int, 128>{}); break;
-        case 256: pick(std::integral_constant<int, 256>{}); break;
-        default: pick(std::integral_constant<int, 512>{}); break;
-    }
+    auto pick_d = [&](auto f) {
+        switch (D) {
+            case 64: pick(std::integral_constant<int, 64>{}, f); break;
+            case 128: pick(std::integral_constant<int, 128>{}, f); break;
+            case 256: pick(std::integral_constant<int, 256>{}, f); break;
+            default: pick(std::integral_constant<int, 512>{}, f); break;
+        }
+    };
+    if (fused)
+        pick_d(std::true_type{});
+    else
+        pick_d(std::false_type{});
     void* kargs[] = {&a};
     if (int rc = hip_check(hipLaunchKernel(k, grid, dim3(kAttnThreads), kargs, 0, s), "attn_partial_kernel launch"))
         return rc;
-    if (int rc = hip_check(hipGetLastError(), "attn_partial_kernel launch")) return rc;
     hipLaunchKernelGGL(attn_merge_kernel, dim3(heads, (D + kAttnThreads - 1) / kAttnThreads), dim3(kAttnThreads), 0, s, a);
     return hip_check(hipGetLastError(), "attn_merge_kernel launch");
+}
+
+int attn_shape_check(int heads, int kv_heads, int D, int max_seq, int window) {
+    if (heads < 1 || kv_heads < 1 || heads % kv_heads || (D != 64 && D != 128 && D != 256 && D != 512) ||
+        max_seq < 1 || window < 0)
+        return fail(ALV_ERR_ARG, "bad attention shape heads=%d kv_heads=%d D=%d max_seq=%d window=%d "
+                    "(D one of 64, 128, 256, 512)", heads, kv_heads, D, max_seq, window);
+    return ALV_OK;
+}
+
+}  // namespace
+}  // namespace alv
+
+extern "C" int alv_attention(const uint16_t* q, const uint16_t* kcache, const uint16_t* vcache, uint16_t* out,
+                             int heads, int kv_heads, int D, int max_seq, int window, float scale, const int* pos_dev,
+                             void* stream) {
+    if (!q || !kcache || !vcache || !out || !pos_dev) return fail(ALV_ERR_ARG, "null pointer");
+    if (int rc = attn_shape_check(heads, kv_heads, D, max_seq, window)) return rc;
+    if (reinterpret_cast<uintptr_t>(kcache) % 16 || reinterpret_cast<uintptr_t>(vcache) % 16 ||
+        reinterpret_cast<uintptr_t>(q) % 16 || reinterpret_cast<uintptr_t>(out) % 2)
+        return fail(ALV_ERR_ALIGN, "q, kcache and vcache need 16-byte alignment");
+    AttnArgs a{};
+    a.q = q;
+    a.kcache = kcache;
+    a.vcache = vcache;
+    a.out = out;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.D = D;
+    a.max_seq = max_seq;
+    a.window = window;
+    a.scale = scale;
+    a.pos = pos_dev;
+    return launch_attention(a, false, (hipStream_t)stream);
+}
+
+extern "C" int alv_qkv_attention(const uint16_t* qkv, int k_off, int v_off, int heads, int kv_heads, int D,
+                                 const float* q_w, const float* k_w, int norm_q, int norm_k, int norm_v, float eps,
+                                 const uint16_t* rope, int rope_stride, int cos_off, int sin_off, int half,
+                                 const int* pos_dev, int max_seq, uint16_t* q_out, uint16_t* kcache, uint16_t* vcache,
+                                 int window, float scale, uint16_t* out, void* stream) {
+    if (!qkv || !pos_dev || !kcache || !vcache || !out) return fail(ALV_ERR_ARG, "null pointer");
+    if (int rc = attn_shape_check(heads, kv_heads, D, max_seq, window)) return rc;
+    if (k_off < heads * D || (v_off >= 0 && v_off < k_off + kv_heads * D))
+        return fail(ALV_ERR_ARG, "bad qkv layout heads=%d kv_heads=%d D=%d k_off=%d v_off=%d", heads, kv_heads, D, k_off,
+                    v_off);
+    if (rope && (half < 1 || 2 * half > D || rope_stride < 1 || cos_off < 0 || sin_off < 0 ||
+                 cos_off + half > rope_stride || sin_off + half > rope_stride))
+        return fail(ALV_ERR_ARG, "bad rope table layout stride=%d cos_off=%d sin_off=%d half=%d for D=%d", rope_stride,
+                    cos_off, sin_off, half, D);
+    if (reinterpret_cast<uintptr_t>(kcache) % 16 || reinterpret_cast<uintptr_t>(vcache) % 16 ||
+        reinterpret_cast<uintptr_t>(out) % 2)
+        return fail(ALV_ERR_ALIGN, "kcache and vcache need 16-byte alignment");
+    AttnArgs a{};
+    a.kcache = kcache;
+    a.vcache = vcache;
+    a.out = out;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.D = D;
+    a.max_seq = max_seq;
+    a.window = window;
+    a.scale = scale;
+    a.pos = pos_dev;
+    a.post = QkvPostArgs{qkv, k_off, v_off, heads, kv_heads, D, q_w, k_w, norm_q, norm_k, norm_v, eps,
+                         rope, rope_stride, cos_off, sin_off, half, pos_dev, max_seq, q_out, kcache, vcache};
+    return launch_attention(a, true, (hipStream_t)stream);
 }
 
 extern "C" int alv_add_norm(const uint16_t* resid, int ldr, const uint16_t* y, int ldy, const float* w_y, int norm_y,

@@ -184,6 +184,47 @@ __device__ __forceinline__ float rms_inv(const float* xs, int K, float eps, floa
     return __fdiv_rn(1.0f, sqrtf(add_rn(var, eps)));
 }
 
+// The same pairwise sum by one wave, for rows whose splits are halvings down
+// to at most 8 leaves (n <= 1024; every head width 64 ... 512): lane j of the
+// 8 lanes of leaf lf sums r[j] in order, three xor steps combine the 8 sums in
+// the leaf rule's order, the tail goes on every lane of the leaf, then xor
+// steps of 8, 16, 32 lanes pair the leaves in the recursion's tree (fadd is
+// commutative, so both lanes of a pair hold the same sum). No barrier; every
+// lane returns lane 0's sum (all lanes of the wave must be active).
+__device__ __forceinline__ float pw_wave_sq(const float* a, int n, int lane) {
+    int leaf = n, leaves = 1;
+    while (leaf > 128) {
+        leaf /= 2;
+        leaves *= 2;
+    }
+    const int j = lane & 7, lf = lane >> 3;
+    const int m8 = leaf - leaf % 8;
+    const float* p = a + (size_t)(lf < leaves ? lf : 0) * leaf;
+    float r = 0.0f;
+    if (leaf >= 8) {
+        r = sqv(p, j);
+        for (int i = 8 + j; i < m8; i += 8) r = add_rn(r, sqv(p, i));
+    }
+    r = add_rn(r, __shfl_xor(r, 1));
+    r = add_rn(r, __shfl_xor(r, 2));
+    r = add_rn(r, __shfl_xor(r, 4));
+    if (leaf < 8) {
+        r = 0.0f;
+        for (int i = 0; i < leaf; ++i) r = add_rn(r, sqv(p, i));
+    } else {
+        for (int i = m8; i < leaf; ++i) r = add_rn(r, sqv(p, i));
+    }
+    for (int s = 1; s < leaves; s *= 2) r = add_rn(r, __shfl_xor(r, 8 * s));
+    // Lanes past the last leaf summed leaf 0 again: every lane takes lane 0's.
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, r)));
+}
+
+// 1 / sqrt(mean(x^2) + eps) of a row of n <= 1024 halving width by one wave.
+__device__ __forceinline__ float rms_inv_wave(const float* xs, int n, float eps, int lane) {
+    const float var = __fdiv_rn(pw_wave_sq(xs, n, lane), (float)n);
+    return __fdiv_rn(1.0f, sqrtf(add_rn(var, eps)));
+}
+
 __device__ __forceinline__ void unpack8(uint4 v, float (&f)[8]) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll

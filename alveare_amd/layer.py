@@ -117,6 +117,48 @@ def qkv_post(qkv: torch.Tensor, pos_dev: torch.Tensor, kcache: torch.Tensor, vca
     return q_out
 
 
+def qkv_attention(qkv: torch.Tensor, pos_dev: torch.Tensor, kcache: torch.Tensor, vcache: torch.Tensor, *,
+                  heads: int, kv_heads: int, D: int, k_off: int, v_off: int, q_w=None, k_w=None, norm_q: bool = True,
+                  norm_k: bool = True, norm_v: bool = True, eps: float = _GEMMA_EPS, rope: torch.Tensor | None = None,
+                  rope_stride: int | None = None, cos_off: int = 0, sin_off: int | None = None,
+                  half: int | None = None, q_out: torch.Tensor | None = None, window: int = 0, scale: float = 1.0,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """qkv_post and attention in one: the attention kernel normalises and
+    rotates q, k and v itself (the same arithmetic, bit for bit), inserts k
+    and v into the caches and writes the rotated q to q_out when given."""
+    dev = _need_gpu(qkv)
+    n_v = 0 if v_off < 0 else v_off + kv_heads * D
+    _bf16(qkv, "qkv", max(k_off + kv_heads * D, n_v))
+    if kcache.shape != vcache.shape or kcache.dim() != 3 or kcache.shape[0] != kv_heads or kcache.shape[2] != D:
+        raise ValueError(f"caches must be ({kv_heads}, max_seq, {D}), got {tuple(kcache.shape)} / {tuple(vcache.shape)}")
+    _bf16(kcache, "kcache", kcache.numel())
+    _bf16(vcache, "vcache", vcache.numel())
+    if pos_dev.dtype != torch.int32 or pos_dev.device != dev:
+        raise ValueError("pos_dev must be an int32 tensor on the activations' device")
+    q_w = _f32(q_w, "q_w", D, dev)
+    k_w = _f32(k_w, "k_w", D, dev)
+    if rope is not None:
+        _bf16(rope, "rope", rope.numel())
+        rope_stride = D if rope_stride is None else rope_stride
+        half = D // 2 if half is None else half
+        sin_off = half if sin_off is None else sin_off
+        if rope.numel() < kcache.shape[1] * rope_stride:
+            raise ValueError(f"rope table of {rope.numel()} values has fewer than the cache's {kcache.shape[1]} rows "
+                             f"of {rope_stride}")
+    if q_out is not None:
+        _bf16(q_out, "q_out", heads * D)
+    if out is None:
+        out = torch.empty(heads * D, dtype=torch.bfloat16, device=dev)
+    _bf16(out, "out", heads * D)
+    with torch.cuda.device(dev):
+        check(lib().alv_qkv_attention(qkv.data_ptr(), k_off, v_off, heads, kv_heads, D, _ptr(q_w), _ptr(k_w),
+                                      int(norm_q), int(norm_k), int(norm_v), ctypes.c_float(eps), _ptr(rope),
+                                      rope_stride or 0, cos_off, sin_off or 0, half or 0, pos_dev.data_ptr(),
+                                      kcache.shape[1], _ptr(q_out), kcache.data_ptr(), vcache.data_ptr(), window,
+                                      ctypes.c_float(scale), out.data_ptr(), _stream(qkv)), "alv_qkv_attention")
+    return out
+
+
 def attention(q: torch.Tensor, kcache: torch.Tensor, vcache: torch.Tensor, pos_dev: torch.Tensor, *, heads: int,
               window: int = 0, scale: float = 1.0, out: torch.Tensor | None = None) -> torch.Tensor:
     """One token's attention over the cache positions up to `pos_dev`
@@ -322,8 +364,10 @@ class Gemma4DecodeLayer:
         ``defer`` result), run inside this layer's QKV launch, which computes
         the input norm itself (``x`` is that step's sum_out). ``defer``: leave
         this layer's last residual step to the next layer's QKV launch and
-        return (y, step) instead of y. With ``fuse`` the post-attention step
-        runs inside the FFN's gate/up launch (``x_norm2`` is then not written)."""
+        return (y, step) instead of y. With ``fuse`` the q/k/v norms, RoPE and
+        cache insert run inside the attention launch, and the post-attention
+        step inside the FFN's gate/up launch (``x_norm2`` is then not
+        written)."""
         H, n = self.H, self.norms
         if step_in is not None:
             gemv_bf16_addnorm(self.w_qkv, step_in["resid"], step_in["y"], sum_out=step_in["sum_out"],
@@ -333,11 +377,16 @@ class Gemma4DecodeLayer:
             if not normed:
                 rmsnorm(x, n["attn"], K=H, out=self.x_norm)
             gemv_bf16(self.w_qkv, self.x_norm, self.qkv_out)
-        qkv_post(self.qkv_out, self.pos_dev, self.kcache, self.vcache, heads=self.heads, kv_heads=self.kv_heads,
-                 D=self.D, k_off=self.q_size, v_off=self.q_size + self.k_size if self.sliding else -1,
-                 q_w=n["q"], k_w=n["k"], norm_v=True, rope=self.rope, q_out=self.q_rope)
-        attention(self.q_rope, self.kcache, self.vcache, self.pos_dev, heads=self.heads, window=self.window,
-                  out=self.attn_out)
+        post = dict(heads=self.heads, kv_heads=self.kv_heads, D=self.D, k_off=self.q_size,
+                    v_off=self.q_size + self.k_size if self.sliding else -1, q_w=n["q"], k_w=n["k"], norm_v=True,
+                    rope=self.rope, q_out=self.q_rope)
+        if self.fuse:
+            qkv_attention(self.qkv_out, self.pos_dev, self.kcache, self.vcache, window=self.window,
+                          out=self.attn_out, **post)
+        else:
+            qkv_post(self.qkv_out, self.pos_dev, self.kcache, self.vcache, **post)
+            attention(self.q_rope, self.kcache, self.vcache, self.pos_dev, heads=self.heads, window=self.window,
+                      out=self.attn_out)
         gemv_bf16(self.w_o, self.attn_out, self.attn_proj)
         if self.fuse:
             ffn_fused_bf16_addnorm(self.ffn, x, self.attn_proj, sum_out=self.x_post, w_y=n["post_attn"], w_x=n["ffn"],

@@ -290,6 +290,21 @@ int alv_attention(const uint16_t* q, const uint16_t* kcache, const uint16_t* vca
                   int kv_heads, int D, int max_seq, int window, float scale, const int* pos_dev, void* stream);
 
 /*
+ * alv_qkv_post followed by alv_attention in the attention's launches: the
+ * attention workgroups normalise and rotate q, k and v from the QKV output
+ * themselves (alv_qkv_post's arithmetic, bit for bit) while their K/V loads
+ * are in flight, insert k and v at pos into the caches and use them in place
+ * of the rows the caches held; q_out (optional) receives the rotated q.
+ * Arguments as the two calls'; the reference runs the same two steps one
+ * after the other (runtime/py/model.py:742-770 then :577-628).
+ */
+int alv_qkv_attention(const uint16_t* qkv, int k_off, int v_off, int heads, int kv_heads, int D, const float* q_w,
+                      const float* k_w, int norm_q, int norm_k, int norm_v, float eps, const uint16_t* rope,
+                      int rope_stride, int cos_off, int sin_off, int half, const int* pos_dev, int max_seq,
+                      uint16_t* q_out, uint16_t* kcache, uint16_t* vcache, int window, float scale, uint16_t* out,
+                      void* stream);
+
+/*
  * Residual step of a layer, per row: t = norm_y ? bf16(rmsnorm(y) * w_y) : y;
  * s = bf16(resid + t), then scale_mode 1: s = bf16(s * scale) (the Python
  * runtime's two roundings, model.py:783-788), 2: s = bf16((resid + t) * scale)

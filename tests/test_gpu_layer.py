@@ -157,6 +157,47 @@ def test_attention_head_groups(dev, D, kv, S, window, pos):
     assert mism <= 16 * D // 50
 
 
+@pytest.mark.parametrize("sliding,pos", [(True, 0), (True, 63), (True, 64), (True, 1500), (False, 0), (False, 1023),
+                                          (False, 2047)])
+def test_qkv_attention_fused_bit_identical(dev, sliding, pos):
+    """alv_qkv_attention gives what alv_qkv_post then alv_attention give,
+    bit for bit -- attention output, rotated q and both caches -- also when
+    the cache row at pos holds NaN beforehand (the fused kernel must use the
+    new k and v, not the row it loaded)."""
+    from alveare_amd import layer
+
+    _say(f"qkv_attention sliding={sliding} pos={pos}")
+    rng = np.random.default_rng(50 + pos + sliding)
+    D, kv, S = (256, 8, 2048) if sliding else (512, 1, 2048)
+    heads, q_size, k_size = 16, 16 * D, kv * D
+    n_qkv = q_size + (2 if sliding else 1) * k_size
+    qkv = bf_dev(rnd_bf16(rng, n_qkv, 1.0), dev)
+    kc0 = rnd_bf16(rng, (kv, S, D), 1.0)
+    vc0 = rnd_bf16(rng, (kv, S, D), 1.0)
+    qw = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    kw = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    table = torch.as_tensor(layer.cos_sin_table_gemma(1e4 if sliding else 1e6, D, S)).view(torch.bfloat16).to(dev)
+    pos_dev = torch.tensor([pos], dtype=torch.int32, device=dev)
+    post = dict(heads=heads, kv_heads=kv, D=D, k_off=q_size, v_off=q_size + k_size if sliding else -1, q_w=qw,
+                k_w=kw, norm_v=True, rope=table)
+    window = 1024 if sliding else 0
+    kc_a, vc_a = bf_dev(kc0, dev), bf_dev(vc0, dev)
+    q_a = torch.empty(heads * D, dtype=torch.bfloat16, device=dev)
+    layer.qkv_post(qkv, pos_dev, kc_a.view(kv, S, D), vc_a.view(kv, S, D), q_out=q_a, **post)
+    out_a = layer.attention(q_a, kc_a.view(kv, S, D), vc_a.view(kv, S, D), pos_dev, heads=heads, window=window)
+    kc_b, vc_b = bf_dev(kc0, dev), bf_dev(vc0, dev)
+    kc_b.view(kv, S, D)[:, pos].fill_(float("nan"))
+    vc_b.view(kv, S, D)[:, pos].fill_(float("nan"))
+    q_b = torch.empty(heads * D, dtype=torch.bfloat16, device=dev)
+    out_b = layer.qkv_attention(qkv, pos_dev, kc_b.view(kv, S, D), vc_b.view(kv, S, D), q_out=q_b, window=window,
+                                **post)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf_np(out_a), bf_np(out_b))
+    assert np.array_equal(bf_np(q_a), bf_np(q_b))
+    assert np.array_equal(bf_np(kc_a), bf_np(kc_b))
+    assert np.array_equal(bf_np(vc_a), bf_np(vc_b))
+
+
 # ---- residual steps (model.py:775-788; model.cpp:409-420) ---------------------------
 
 @pytest.mark.parametrize("mode,norm_y,norm_out,K,pad", [(0, True, True, 3840, 4096), (1, True, False, 3840, 4096),
