@@ -338,6 +338,56 @@ def graph_us(torch, fn, reps: int, per: int) -> float:
     return a.elapsed_time(b) * 1e3 / (reps * per)
 
 
+def eager_calls(torch, aa, dev, n: int = 200) -> dict:
+    """Wall time per eager call from Python, the host cost the reference's
+    per-call profile counts (tests/bench/gemma4_profile.txt: per-call host
+    overhead plus host<->device copies): device tensors in and out (Python ->
+    ctypes -> plan -> launch, n calls then one synchronize), and the drop-in
+    dispatch with host NumPy bf16 in and out (upload, launch, download: each
+    call synchronises), for the 8192x3840 QKV GEMV and the 3840<->15360 FFN."""
+    import numpy as np
+
+    from alveare_amd.runtime import Q4Dispatch, ResidentWeight
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0xEA6E)
+    wq_t = synth_q4_dev(torch, N_QKV, H, gen, dev)
+    wq = aa.Q4Weight(wq_t, N_QKV, H)
+    ffn = aa.pack_ffn_fused_weights(synth_q4_dev(torch, I_FF, H, gen, dev), synth_q4_dev(torch, I_FF, H, gen, dev),
+                                    synth_q4_dev(torch, H, I_FF, gen, dev), H, I_FF)
+    x = torch.randn(H, device=dev)
+    yq = torch.empty(N_QKV, device=dev)
+    yf = torch.empty(H, device=dev)
+
+    def per_call(fn, sync_each: bool) -> float:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+            if sync_each:
+                torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e6
+
+    out = {"gemv_8192x3840_device_tensors": round(per_call(lambda: wq(x, yq), False), 2),
+           "ffn_3840x15360_device_tensors": round(per_call(lambda: ffn(x, yf), False), 2)}
+    d = Q4Dispatch(H, I_FF, "gemma4", dev, host_io=True)
+    rw = ResidentWeight(wq_t.reshape(-1), (N_QKV, H // 32 * 20))
+    l = d.register_ffn(*(synth_q4_dev(torch, r, c, gen, dev).view(r, c // 32 * 20) for r, c in
+                         ((I_FF, H), (I_FF, H), (H, I_FF))))
+    xh = np.asarray(x.cpu().numpy(), np.float32)
+    out["gemv_8192x3840_host_numpy_bf16"] = round(per_call(lambda: d.run_gemv_npu(rw, xh), True), 2)
+    out["ffn_3840x15360_host_numpy_bf16"] = round(per_call(lambda: d.run_ffn_fused_npu(l, xh), True), 2)
+    out["note"] = ("per call, wall clock; device-tensor calls are launch-bound on the host when shorter than the "
+                   "kernel; the reference's decode profile spends about 106 us of host overhead and 417 us of "
+                   "host<->device copies per call")
+    wq.close()
+    ffn.close()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -541,6 +591,7 @@ def main() -> int:
         torch.cuda.empty_cache()
 
         extra["decode_step_gemma4_48l"] = decode_step(torch, aa, dev)
+        extra["eager_call_us"] = eager_calls(torch, aa, dev)
 
     from alveare_amd import profiling
 
