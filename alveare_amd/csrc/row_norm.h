@@ -110,6 +110,62 @@ __device__ float pw_serial_sq(const float* a, int n, PwFrame* st) {
     return ret;
 }
 
+// ---- lane moves ----------------------------------------------------------------------
+// DPP moves within rows of 16 lanes: quad_perm [1,0,3,2] (0xB1) and [2,3,0,1]
+// (0x4E) pair lanes 1 and 2 apart, row_half_mirror (0x141) lane i with 7 - i,
+// row_mirror (0x140) lane i with 15 - i. Every source lane must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// The sum of the squares of one leaf p[0, leaf), 8 <= leaf <= 128, by the
+// leaf's 8 lanes (an 8-aligned group, j = lane % 8, all active): lane j sums
+// r[j] = p[j]^2 + p[8 + j]^2 + ... in order (all loads issued at once), two
+// quad_perm moves and a half mirror combine ((r0 + r1) + (r2 + r3)) +
+// ((r4 + r5) + (r6 + r7)) on every lane (fadd is commutative, so both lanes of
+// a pair hold the same bits), then the leaf % 8 tail is added in order.
+__device__ __forceinline__ float leaf8_sq(const float* p, int leaf, int j) {
+    const int m8 = leaf - leaf % 8;
+    float sq[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) sq[q] = sqv(p, 8 * q + j < m8 ? 8 * q + j : j);
+    float r = sq[0];
+#pragma unroll
+    for (int q = 1; q < 16; ++q) {
+        const float t = add_rn(r, sq[q]);
+        r = 8 * q + j < m8 ? t : r;
+    }
+    r = add_rn(r, dpp_f<0xB1>(r));
+    r = add_rn(r, dpp_f<0x4E>(r));
+    r = add_rn(r, dpp_f<0x141>(r));
+    for (int i = m8; i < leaf; ++i) r = add_rn(r, sqv(p, i));
+    return r;
+}
+
+// The recursion's tree over `count` (a power of two <= 64) values held by
+// the wave's lanes 0, g, 2g, ... (g = 1: one per lane; g = 8: one per 8-lane
+// group, each group's lanes holding the same bits), returned to every lane:
+// DPP moves pair neighbours within rows of 16 lanes, readlane the rows.
+// Every lane of the wave must be active.
+__device__ __forceinline__ float fold_tree(float v, int count, int g) {
+    int c = count;
+    if (g == 1) {
+        if (c > 1) v = add_rn(v, dpp_f<0xB1>(v));
+        if (c > 2) v = add_rn(v, dpp_f<0x4E>(v));
+        if (c > 4) v = add_rn(v, dpp_f<0x141>(v));
+        c = c > 8 ? c / 8 : 1;  // groups of 8 lanes left to pair
+    }
+    if (c > 1) v = add_rn(v, dpp_f<0x140>(v));
+    if (c > 4) return add_rn(add_rn(lane_f(v, 0), lane_f(v, 16)), add_rn(lane_f(v, 32), lane_f(v, 48)));
+    if (c > 2) return add_rn(lane_f(v, 0), lane_f(v, 16));
+    return lane_f(v, 0);
+}
+
 // Pairwise sum of the squares of a[0, n), n <= 8192, by the workgroup
 // (NT threads; a and red in LDS, red >= 65 floats, 16-byte aligned: the
 // one-lane recursion keeps its frames in red[0, 64)). Returned to all.
@@ -125,46 +181,24 @@ __device__ __forceinline__ float pw_chunk_sq(const float* a, int n, float* red, 
         leaf /= 2;
         leaves *= 2;
     }
-    if (!halving || leaves > 64) {
+    if (!halving || leaf < 8 || leaves > 64) {
         if (tid == 0) red[64] = pw_serial_sq(a, n, reinterpret_cast<PwFrame*>(red));
-    } else {
-        // 8 lanes per leaf: lane j sums r[j] = a[j] + a[8 + j] + ... in order.
-        const int j = tid & 7;
-        const int m8 = leaf - leaf % 8;
-        for (int base = 0; base < leaves; base += NT / 8) {
-            const int lf = base + (tid >> 3);
-            const bool act = lf < leaves;
-            const float* p = a + (size_t)(act ? lf : 0) * leaf;
-            float r = 0.0f;
-            if (act && leaf >= 8) {
-                r = sqv(p, j);
-                for (int i = 8 + j; i < m8; i += 8) r = add_rn(r, sqv(p, i));
-            }
-            r = add_rn(r, __shfl_xor(r, 1));
-            r = add_rn(r, __shfl_xor(r, 2));
-            r = add_rn(r, __shfl_xor(r, 4));
-            if (act && j == 0) {
-                if (leaf < 8) {
-                    r = 0.0f;
-                    for (int i = 0; i < leaf; ++i) r = add_rn(r, sqv(p, i));
-                } else {
-                    for (int i = m8; i < leaf; ++i) r = add_rn(r, sqv(p, i));
-                }
-                red[lf] = r;
-            }
-        }
         __syncthreads();
-        if (tid < 64) {
-            float v = tid < leaves ? red[tid] : 0.0f;
-            for (int s = 1; s < leaves; s *= 2) {
-                const float o = __shfl_down(v, s);
-                if ((tid & (2 * s - 1)) == 0) v = add_rn(v, o);
-            }
-            if (tid == 0) red[64] = v;
+        const float r = red[64];
+        __syncthreads();  // red is reused by the next call
+        return r;
+    }
+    // 8 lanes per leaf, leaf sums to red[lf]; every wave then folds them.
+    for (int base = 0; base < leaves; base += NT / 8) {
+        const int lf = base + (tid >> 3);
+        if (lf < leaves) {
+            const float r = leaf8_sq(a + (size_t)lf * leaf, leaf, tid & 7);
+            if ((tid & 7) == 0) red[lf] = r;
         }
     }
     __syncthreads();
-    const float r = red[64];
+    const int lane = tid & 63;
+    const float r = fold_tree(red[lane < leaves ? lane : 0], leaves, 1);
     __syncthreads();  // red is reused by the next call
     return r;
 }
@@ -185,38 +219,26 @@ __device__ __forceinline__ float rms_inv(const float* xs, int K, float eps, floa
 }
 
 // The same pairwise sum by one wave, for rows whose splits are halvings down
-// to at most 8 leaves (n <= 1024; every head width 64 ... 512): lane j of the
-// 8 lanes of leaf lf sums r[j] in order, three xor steps combine the 8 sums in
-// the leaf rule's order, the tail goes on every lane of the leaf, then xor
-// steps of 8, 16, 32 lanes pair the leaves in the recursion's tree (fadd is
-// commutative, so both lanes of a pair hold the same sum). No barrier; every
-// lane returns lane 0's sum (all lanes of the wave must be active).
+// to at most 8 leaves (n <= 1024; every head width 64 ... 512): 8 lanes per
+// leaf (leaf8_sq), then the leaves paired in the recursion's tree
+// (fold_tree). No barrier; every lane returns the sum (all lanes of the wave
+// must be active).
 __device__ __forceinline__ float pw_wave_sq(const float* a, int n, int lane) {
     int leaf = n, leaves = 1;
     while (leaf > 128) {
         leaf /= 2;
         leaves *= 2;
     }
-    const int j = lane & 7, lf = lane >> 3;
-    const int m8 = leaf - leaf % 8;
-    const float* p = a + (size_t)(lf < leaves ? lf : 0) * leaf;
-    float r = 0.0f;
-    if (leaf >= 8) {
-        r = sqv(p, j);
-        for (int i = 8 + j; i < m8; i += 8) r = add_rn(r, sqv(p, i));
-    }
-    r = add_rn(r, __shfl_xor(r, 1));
-    r = add_rn(r, __shfl_xor(r, 2));
-    r = add_rn(r, __shfl_xor(r, 4));
     if (leaf < 8) {
-        r = 0.0f;
-        for (int i = 0; i < leaf; ++i) r = add_rn(r, sqv(p, i));
-    } else {
-        for (int i = m8; i < leaf; ++i) r = add_rn(r, sqv(p, i));
+        float r = 0.0f;
+        for (int i = 0; i < leaf; ++i) r = add_rn(r, sqv(a, i));
+        return lane_f(r, 0);
     }
-    for (int s = 1; s < leaves; s *= 2) r = add_rn(r, __shfl_xor(r, 8 * s));
-    // Lanes past the last leaf summed leaf 0 again: every lane takes lane 0's.
-    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, r)));
+    // Lanes past the last leaf sum leaf 0 again; the tree reads only lanes
+    // of real leaves.
+    const int lf = lane >> 3;
+    const float r = leaf8_sq(a + (size_t)(lf < leaves ? lf : 0) * leaf, leaf, lane & 7);
+    return fold_tree(r, leaves, 8);
 }
 
 // 1 / sqrt(mean(x^2) + eps) of a row of n <= 1024 halving width by one wave.
