@@ -279,10 +279,16 @@ def decode_step(torch, aa, dev, nl: int = 48, pos: int = 1500, reps: int = 10) -
                     "one HIP graph per token, device-resident token and position"}
 
 
+READ_SHAPES = [(wg, depth) for wg in (2, 4, 8) for depth in (4, 8, 16)]
+
+
 def read_floor(torch, aa, dev) -> dict:
-    """The practical ceiling per launch: a plain streaming read
-    (alv_stream_read) of each op's weight bytes, from distinct regions of a
-    2 GiB buffer (far beyond the Infinity Cache), timed like the ops."""
+    """The practical ceiling per launch: a plain streaming read of each op's
+    weight bytes, from distinct regions of a 2 GiB buffer (far beyond the
+    Infinity Cache), timed like the ops: the default shape (alv_stream_read,
+    4 workgroups per CU, 4 loads in flight per thread) and the fastest of a
+    sweep over queue depth (alv_stream_read_shape: 2-8 workgroups per CU,
+    4-16 loads per thread, up to 512 KiB in flight per CU)."""
     L = aa.lib()
     big = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
     sink = torch.zeros(2048, dtype=torch.int32, device=dev)
@@ -293,17 +299,25 @@ def read_floor(torch, aa, dev) -> dict:
         nb = nbytes // 256 * 256
         n = min(48, big.numel() // nb)
 
-        def fn(nb=nb, n=n):
-            st = torch.cuda.current_stream().cuda_stream
-            for i in range(n):
-                rc = L.alv_stream_read(big.data_ptr() + i * nb, nb, sink.data_ptr(), st)
-                if rc:
-                    raise RuntimeError(f"alv_stream_read failed ({rc})")
+        def timed(wg, depth, nb=nb, n=n):
+            def fn():
+                st = torch.cuda.current_stream().cuda_stream
+                for i in range(n):
+                    rc = L.alv_stream_read_shape(big.data_ptr() + i * nb, nb, sink.data_ptr(), wg, depth, st)
+                    if rc:
+                        raise RuntimeError(f"alv_stream_read_shape failed ({rc})")
+            return graph_us(torch, fn, 3, n)
 
-        us = graph_us(torch, fn, 3, n)
-        out[k] = {"us": round(us, 3), "GBps": round(nb / us / 1e3, 1)}
+        us = timed(4, 4)
+        sweep = {f"{wg}x{depth}": timed(wg, depth) for wg, depth in READ_SHAPES}
+        best = min(sweep, key=sweep.get)
+        out[k] = {"us": round(us, 3), "GBps": round(nb / us / 1e3, 1),
+                  "best_shape": best, "best_us": round(sweep[best], 3),
+                  "best_GBps": round(nb / sweep[best] / 1e3, 1),
+                  "sweep_us": {s: round(v, 3) for s, v in sweep.items()}}
     layer = out["qkv"]["us"] + out["o"]["us"] + out["ffn_gate_up"]["us"] + out["ffn_down"]["us"]
     out["layer_us"] = round(layer, 3)
+    out["layer_best_us"] = round(sum(out[k]["best_us"] for k in sizes), 3)
     del big
     torch.cuda.empty_cache()
     return out

@@ -398,6 +398,15 @@ int alv_glu(const float* g, const float* u, float* out, int64_t n, int act, void
  */
 int alv_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream);
 
+/*
+ * alv_stream_read with its launch shape chosen: wg_per_cu 256-thread
+ * workgroups per CU (1-8) and `depth` 16-byte loads in flight per thread and
+ * pass (2, 4, 8 or 16); alv_stream_read is wg_per_cu 4, depth 4. The
+ * benchmark sweeps these to find the deepest-queue read ceiling per launch.
+ * Measurement aid with no counterpart in the reference.
+ */
+int alv_stream_read_shape(const void* buf, size_t bytes, uint32_t* sink, int wg_per_cu, int depth, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -645,6 +645,14 @@ def test_stream_read_probe(dev):
         assert rc == 0
         want = np.bitwise_xor.reduce(buf.cpu().numpy().view(np.uint32))
         assert np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32)[::32]) == want
+        for wg, depth in ((1, 2), (2, 16), (8, 8), (3, 4)):
+            sink.zero_()
+            rc = aa.lib().alv_stream_read_shape(buf.data_ptr(), n * 4, sink.data_ptr(), wg, depth,
+                                                torch.cuda.current_stream().cuda_stream)
+            assert rc == 0
+            assert np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32)[::32]) == want, (n, wg, depth)
+    assert aa.lib().alv_stream_read_shape(buf.data_ptr(), 16, sink.data_ptr(), 4, 3, 0) != 0
+    assert aa.lib().alv_stream_read_shape(buf.data_ptr(), 16, sink.data_ptr(), 9, 4, 0) != 0
 
 
 @pytest.mark.parametrize("act", [0, 1])
