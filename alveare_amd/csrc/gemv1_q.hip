@@ -480,7 +480,7 @@ __device__ __forceinline__ void finish_tile(const Gemv1Args& a, const WgWork& wk
 // Every tile of the workgroup (wave w: tiles w, w + NW, ...), then the split-K
 // fixup (section 5). Split-K launches finish here, after all their units.
 template <int NW, int R, bool GLU, int MT, bool TB>
-__device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk, const f32x4* part, int* flag,
+__device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk, f32x4* part, int part_n, int* flag,
                                             int tid) {
     using Ph = PhaseT<R, false, GLU, MT, TB>;
     constexpr int NT = Ph::NT;
@@ -500,6 +500,7 @@ __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk
     if (tid == 0) {
         const uint32_t old = __hip_atomic_fetch_add(&a.cnt[wk.tg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *flag = old == (uint32_t)(a.ks - 1) ? 1 : 0;
+        flag[1] = 0;
     }
     __syncthreads();
     if (!*flag) return;
@@ -525,9 +526,41 @@ __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk
             for (int e = 0; e < 4; e += NT) {
                 const int m = (4 * ch + e) / NT;
                 if (m >= a.M) continue;
-                float out = y[e];
-                if constexpr (GLU) out = glu_out<MT>(y[e], y[e + NT - 1], a.act);
-                ystore(a, m, row, out);
+                if constexpr (GLU) {
+                    // GELU values the float32 path cannot settle wait in a
+                    // queue in the (now unused) unit slots: about one in ten
+                    // here, so nearly every wave would otherwise run the float64
+                    // path for all its values.
+                    const float gb = bf16_round(y[e]), ub = bf16_round(y[e + NT - 1]);
+                    float v;
+                    if (a.act != ALV_ACT_GELU_TANH) {
+                        v = glu_exact(gb, ub, a.act);
+                    } else if (!glu_fast(gb, ub, a.act, &v)) {
+                        const int qi = __hip_atomic_fetch_add(&flag[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                        if (qi < part_n) {
+                            reinterpret_cast<u32x4*>(part)[qi] = u32x4{__builtin_bit_cast(uint32_t, gb),
+                                                                       __builtin_bit_cast(uint32_t, ub), (uint32_t)m,
+                                                                       (uint32_t)row};
+                            continue;
+                        }
+                        v = glu_exact(gb, ub, a.act);
+                    }
+                    ystore(a, m, row, bf16_round(v));
+                } else {
+                    ystore(a, m, row, y[e]);
+                }
+            }
+        }
+        if constexpr (GLU) {
+            __syncthreads();
+            const int nq = min(flag[1], part_n);
+            for (int i = tid; i < nq; i += 64 * NW) {
+                // Elements through scalars: this clang lowers a bit cast of a
+                // vector element to a read of element 0.
+                const u32x4 q = reinterpret_cast<const u32x4*>(part)[i];
+                const uint32_t gbits = q[0], ubits = q[1], m = q[2], row = q[3];
+                ystore(a, (int)m, (int)row,
+                       bf16_round(glu_exact(__builtin_bit_cast(float, gbits), __builtin_bit_cast(float, ubits), a.act)));
             }
         }
     } else {
@@ -617,7 +650,7 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
         }
     }
     lds_barrier();
-    finish_rows<NW, R, GLU, MT, TB>(a, wk, part, next, tid);
+    finish_rows<NW, R, GLU, MT, TB>(a, wk, part, U * US, next, tid);
 }
 
 struct DevInfo {
