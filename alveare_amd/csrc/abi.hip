@@ -152,11 +152,12 @@ int small_tile_max_m() {
     return v >= 0 && v <= (1 << 30) ? (int)v : kSmallTileMaxM;
 }
 
-int tiled_min_m() {
+int tiled_min_m(bool fp32_x) {
+    const int dflt = fp32_x ? kTiledMinMF32 : kTiledMinMBf16;
     const char* e = getenv("ALV_TILED_MIN_M");
-    if (!e || !*e) return kTiledMinM;
+    if (!e || !*e) return dflt;
     const long v = strtol(e, nullptr, 10);
-    return v >= 1 && v <= (1 << 30) ? (int)v : kTiledMinM;
+    return v >= 1 && v <= (1 << 30) ? (int)v : dflt;
 }
 
 }  // namespace alv

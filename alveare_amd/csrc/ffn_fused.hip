@@ -12,7 +12,8 @@
 //   2. down = Wd * a, with a single bf16 term per activation value (it is
 //      bf16 by construction), summed entirely on the device -- the reference
 //      sums per-core partials on the host (runtime/cpp/src/npu.cpp:360-377).
-// Prefill (M >= 32): the same two steps with the MFMA tiled kernel (gemm_q.hip);
+// Prefill (from 17 bf16 / 33 fp32 tokens): the same two steps with the MFMA
+// tiled kernel (gemm_q.hip);
 // the M x I activation lives in the stream's prefill scratch (q4_host.h).
 #include <string.h>
 
@@ -130,7 +131,7 @@ extern "C" int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int l
     if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
     if (dev != w->device) return fail(ALV_ERR_HANDLE, "FFN handle belongs to device %d, current device is %d", w->device, dev);
     hipStream_t s = (hipStream_t)stream;
-    if (M >= tiled_min_m()) {
+    if (M >= tiled_min_m(true)) {
         // Prefill: the activation goes to the stream's scratch; the handle's
         // decode buffer keeps its size and address (graphs may hold it).
         void* act = nullptr;
@@ -174,7 +175,7 @@ extern "C" int alv_ffn_fused_bf16(alv_ffn_t w, const uint16_t* X, uint16_t* Y, i
         op[1].Y = nullptr;
         op[1].Yb = y;
     };
-    if (M >= tiled_min_m()) {
+    if (M >= tiled_min_m(false)) {
         void* act = nullptr;
         if (int rc = get_scratch(s, kScratchAct, (size_t)M * w->I * sizeof(uint16_t), &act)) return rc;
         GemvLaunch op[2];

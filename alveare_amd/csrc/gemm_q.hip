@@ -1,6 +1,6 @@
-// MFMA Q4 GEMM for prefill-sized batches (gfx950): the M >= 32 path of
-// alv_gemm_q, alv_gemv and alv_ffn_fused (gate/up with the GLU epilogue, then
-// down).
+// MFMA Q4 GEMM for prefill-sized batches (gfx950): the path of alv_gemm_q,
+// alv_gemv, alv_gemv_bf16, alv_ffn_fused and alv_ffn_fused_bf16 from 17 (bf16
+// activations) or 33 (fp32) tokens (gate/up with the GLU epilogue, then down).
 //
 // C[M, N] = X[M, K] * dequant(W)[N, K]^T. A workgroup of 8 waves owns a
 // TM-token x 128-weight-row tile -- TM = 256, or 64 up to 128 tokens (a

@@ -87,7 +87,7 @@ extern "C" int alv_gemm_q(const uint8_t* W, const float* X, float* Y, int M, int
     L.N = N;
     L.K = K;
     L.parts = 3;
-    if (M >= tiled_min_m()) {
+    if (M >= tiled_min_m(true)) {
         L.X = X;
         L.Y = Y;
         L.M = M;

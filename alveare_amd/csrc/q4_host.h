@@ -124,16 +124,20 @@ constexpr int kGemvMaxM = 16;
 int launch_gemm_tiled(const GemvLaunch& L, hipStream_t s);
 
 // M at and above which the tiled kernel runs a product (below it the
-// streaming kernel, 16 tokens per launch): kTiledMinM, or the positive value
-// of the environment variable ALV_TILED_MIN_M, read at each call (a tuning
-// knob; the benchmark times both kernels at small M with it). Measured on the
-// 12B-class FFN (3840 <-> 15360): the streaming kernel takes about 54 us per
-// 16 tokens; the tiled kernel with 64-token tiles 78-85 us for any M up to 64
-// with bf16-valued activations (one term) and 134-140 us with fp32 ones (three
-// terms). From 32 tokens the tiled kernel is faster for bf16-valued inputs
-// (81 against 107 us) and within a fifth for fp32 ones (136 against 112 us).
-constexpr int kTiledMinM = 32;
-int tiled_min_m();
+// streaming kernel, 16 tokens per launch), by activation type: bf16
+// activations (one term on both kernels) kTiledMinMBf16, fp32 ones (three
+// terms on both unless bf16-valued) kTiledMinMF32; the positive value of the
+// environment variable ALV_TILED_MIN_M, read at each call, overrides both (a
+// tuning knob; the benchmark times both kernels at small M with it).
+// Measured on the 12B-class FFN (3840 <-> 15360), 16 distinct layers, µs
+// per call: streaming 53-56 at 16 tokens and 82-84 at 17 (two launches);
+// tiled with 64-token tiles 78-80 for any M up to 64 with bf16-valued
+// activations and 133-138 with fp32 ones; so from 17 tokens the tiled kernel
+// wins for bf16 (78 against 82), and from 33 for fp32 (streaming 106 at 32,
+// 148 at 40, against 135-138).
+constexpr int kTiledMinMBf16 = 17;
+constexpr int kTiledMinMF32 = 33;
+int tiled_min_m(bool fp32_x);
 // Largest M the prefill GEMM runs with 64-token tiles (256-token tiles above);
 // ALV_GEMM_SMALL_TILE_MAX_M overrides.
 constexpr int kSmallTileMaxM = 128;

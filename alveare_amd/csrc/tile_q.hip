@@ -141,7 +141,7 @@ extern "C" int alv_gemv(alv_weight_t w, const float* X, float* Y, int M, int ldx
     L.parts = 3;
     L.tiled = true;
     hipStream_t s = (hipStream_t)stream;
-    if (M >= tiled_min_m()) {
+    if (M >= tiled_min_m(true)) {
         L.X = X;
         L.Y = Y;
         L.M = M;
@@ -175,7 +175,7 @@ extern "C" int alv_gemv_bf16(alv_weight_t w, const uint16_t* X, uint16_t* Y, int
     L.parts = 1;
     L.tiled = true;
     hipStream_t s = (hipStream_t)stream;
-    if (M >= tiled_min_m()) {
+    if (M >= tiled_min_m(false)) {
         L.Xb = X;
         L.Yb = Y;
         L.M = M;

@@ -512,7 +512,8 @@ def main() -> int:
                                      "mfma_frac_bf16_dense": round(flops / us / 1e6 / 2500.0, 4)}
 
         # Where the streaming kernel should hand over to the MFMA tiled kernel
-        # (small-M decode against the 12B-class FFN): both kernels at M = 8 ... 128,
+        # (small-M decode against the 12B-class FFN): both kernels at M = 8 ... 128
+        # (finely between 16 and 48, where the crossovers lie),
         # selected with the library's ALV_TILED_MIN_M knob, for fp32 activations
         # (three bf16 terms on the tiled kernel) and bf16-valued ones (one term).
         cross = {}
@@ -526,7 +527,7 @@ def main() -> int:
                 for kind, knob in (("streaming", "1000000"), ("tiled", "1")):
                     os.environ["ALV_TILED_MIN_M"] = knob
                     row = cross.setdefault(f"{kind}_{xname}", {})
-                    for M in (8, 16, 32, 48, 64, 96, 128):
+                    for M in (8, 16, 17, 20, 24, 28, 32, 40, 48, 64, 96, 128):
                         us = graph_us(torch, lambda: [ffn(xm, ym, M=M) for _, _, ffn in layers[:ncross]], 2, ncross)
                         row[str(M)] = round(us, 2)
         finally:

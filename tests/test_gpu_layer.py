@@ -237,7 +237,7 @@ def test_add_norm_bit_exact(dev, mode, norm_y, norm_out, K, pad):
 # ---- bf16 GEMV and FFN (the reference's run_gemv / run_ffn_fused contract) ----------
 
 @pytest.mark.parametrize("M,N,K", [(1, 8192, 3840), (1, 3840, 4096), (4, 2048, 2048), (16, 1024, 3840),
-                                   (64, 1024, 3840)])
+                                   (17, 1024, 3840), (24, 2048, 2048), (64, 1024, 3840)])
 def test_gemv_bf16(orc, dev, M, N, K):
     import alveare_amd as aa
     from alveare_amd import layer
@@ -254,14 +254,21 @@ def test_gemv_bf16(orc, dev, M, N, K):
     w.close()
 
 
-@pytest.mark.parametrize("H,I,M", [(1152, 6912, 1), (3840, 15360, 1), (1152, 6912, 4), (1024, 2048, 64)])
-def test_ffn_fused_bf16(orc, dev, H, I, M):
+@pytest.mark.parametrize("H,I,M", [(1152, 6912, 1), (3840, 15360, 1), (1152, 6912, 4), (1152, 6912, 20),
+                                   (1024, 2048, 64)])
+def test_ffn_fused_bf16(orc, dev, H, I, M, monkeypatch):
     """bf16 ends on the same device FFN: gate/up reads the bf16 activation as
     its one term and gives the activation alv_ffn_fused gives for the same
     (bf16-valued) input, bit for bit; the bf16 output is the rounding of
-    alv_ffn_fused's float32 output (which meets the FFN bar against the oracle)."""
+    alv_ffn_fused's float32 output (which meets the FFN bar against the oracle).
+    From 17 to 32 tokens the bf16 call takes the tiled kernel and the fp32 one
+    the streaming kernel: both are held to the tiled kernel there, so that the
+    two runs share one summation order."""
     import alveare_amd as aa
     from alveare_amd import layer
+
+    if 17 <= M < 33:
+        monkeypatch.setenv("ALV_TILED_MIN_M", "17")
 
     _say(f"ffn_fused_bf16 H={H} I={I} M={M}")
     Wg, Wu, Wd = orc.synth_q4(I, H, 200), orc.synth_q4(I, H, 201), orc.synth_q4(H, I, 202)

@@ -370,7 +370,7 @@ def test_chain_long_and_repeated_ffn(orc, dev):
     p.close()
 
 
-# ---- GEMM (small M: streaming kernel; M >= 32: MFMA tiled kernel) -------------------
+# ---- GEMM (small M: streaming kernel; from 17 bf16 / 33 fp32 tokens: MFMA tiled kernel) ---
 
 @pytest.mark.parametrize("M,N,K,bf16x", [(2, 3840, 3840, False), (4, 15360, 3840, False),
                                           (8, 3840, 15360, False), (16, 3840, 3840, False),
