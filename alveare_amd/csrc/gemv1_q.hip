@@ -437,8 +437,9 @@ __device__ __forceinline__ void finish_tile(const Gemv1Args& a, const WgWork& wk
     for (int m = 0; m < MT; ++m)
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
-            y[m][n] += __shfl_xor(y[m][n], 1);
-            y[m][n] += __shfl_xor(y[m][n], 2);
+            // lanes c ^ 1, then c ^ 2, of the row's four (DPP quad_perm moves)
+            y[m][n] += dpp_f<0xB1>(y[m][n]);
+            y[m][n] += dpp_f<0x4E>(y[m][n]);
         }
     const int row = tile_row(wk, tl) * 16 + jj;
     if (row >= a.N) return;
