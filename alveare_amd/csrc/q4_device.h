@@ -257,14 +257,15 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
 //
 // GELU fast path, for results that reach the same bf16 value: with
 // z = sqrt(2/pi) * inner rounded to fp32, 1 + tanh(z) = 2 / (1 + e^(-2z)) has
-// no cancellation, and for z >= -7 (|2z| <= 14 where it matters) the fp32 value
-// v = (0.5 g) * that * u is within 2^-19 |V| of the reference's V (z's rounding
-// 14 * 2^-24 through the exponential, expf 1 ulp, the add, the divide and two
-// products 2^-24 each); the reference's own float64 1 + t loses at most
-// 2^-53 / (1 + tanh(-7)) < 2^-33 there. 2^-19 relative is at most 32 fp32 ulps
-// of v, so when v's bits are more than 64 ulps from the bf16 rounding midpoint
-// of its binade (low half 0x8000) and v is normal, bf16(f32(V)) = bf16(v).
-// Anything else -- z < -7, NaN, zero, tiny or huge v, near a midpoint (about
+// no cancellation, and for z >= -11 (|2z| <= 22 where it matters) the fp32
+// value v = (0.5 g) * that * u is within 34 * 2^-24 |V| of the reference's V:
+// z's rounding 22 * 2^-24 through the exponential, expf 2 ulps (4 * 2^-24),
+// the add, the divide and two products 2^-24 each, and the reference's own
+// float64 1 + t, which loses at most 2^-53 / (1 + tanh(-11)) < 4 * 2^-24
+// there (t within an ulp of tanh). That is at most 34 fp32 ulps of v, so when
+// v's bits are more than 64 ulps from the bf16 rounding midpoint of its
+// binade (low half 0x8000) and v is normal, bf16(f32(V)) = bf16(v).
+// Anything else -- z < -11, NaN, zero, tiny or huge v, near a midpoint (about
 // 0.2 % of values) -- takes the float64 path, which is the reference's.
 // The reference's arithmetic, float64 tanh and all.
 __device__ __forceinline__ float glu_exact(float g, float u, int act) {
@@ -292,7 +293,7 @@ __device__ __forceinline__ bool glu_fast(float g, float u, int act, float* out) 
     const float g3 = (g * g) * g;
     const float inner = g + 0.044715f * g3;
     const double zd = 0.7978845608028654 * (double)inner;
-    if (!(zd >= -7.0)) return false;
+    if (!(zd >= -11.0)) return false;
     const float z = (float)zd;
     const float v = ((0.5f * g) * (2.0f / (1.0f + expf(-2.0f * z)))) * u;
     const uint32_t b = __builtin_bit_cast(uint32_t, v);
