@@ -79,7 +79,7 @@ int alv_gemv_q(const uint8_t* W, const float* x, float* y, int N, int K, void* s
  * (kernels/gemm_q/gemm_q.py:28-39) and NpuRegistry::run_gemm
  * (runtime/cpp/include/alveare/npu.h:82-87, runtime/cpp/src/npu.cpp:290-310).
  * M is any positive token count (the reference's B=16 chunking is not needed).
- * M < 32 runs the streaming GEMV kernel (16 tokens per launch), M >= 32 the
+ * M <= 32 runs the streaming GEMV kernel (16 tokens per launch), M >= 33 the
  * MFMA tiled kernel, both reading the combined layout directly.
  */
 int alv_gemm_q(const uint8_t* W, const float* X, float* Y, int M, int N, int K,
@@ -101,7 +101,7 @@ int alv_weight_shape(alv_weight_t w, int* N, int* K);
 /*
  * Y[M,N] = X[M,K] @ dequant(W)^T with W registered; rows of X/Y at leading
  * dimensions ldx/ldy. M = 1 is the decode GEMV, small M the streaming kernel,
- * M >= 32 the MFMA tiled kernel (ALV_TILED_MIN_M overrides the threshold).
+ * M >= 33 the MFMA tiled kernel (ALV_TILED_MIN_M overrides the threshold).
  * Replaces NpuRegistry::run_gemv / run_gemm (runtime/cpp/include/alveare/npu.h:78-87,
  * runtime/cpp/src/npu.cpp:269-310).
  */
@@ -112,6 +112,9 @@ int alv_gemv(alv_weight_t w, const float* X, float* Y, int M, int ldx, int ldy, 
  * the reference's run_gemv(N, K, w, x_bf16, y_bf16) contract
  * (runtime/cpp/include/alveare/npu.h:78-87; runtime/py/model.py:283-362
  * run_gemv_npu returns bf16). X rows 16-byte aligned (ldx a multiple of 8).
+ * bf16 activations take the MFMA tiled kernel from M = 17 (one term per
+ * activation on both kernels moves the crossover down; ALV_TILED_MIN_M
+ * overrides it).
  */
 int alv_gemv_bf16(alv_weight_t w, const uint16_t* X, uint16_t* Y, int M, int ldx, int ldy, void* stream);
 
@@ -198,6 +201,7 @@ int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int ldx, int ldy
  * (runtime/cpp/include/alveare/npu.h:90-97, runtime/cpp/src/npu.cpp:340-378:
  * partials summed in float32, then bf16). Same rounding points as
  * alv_ffn_fused; Y = bf16(down). X rows 16-byte aligned (ldx a multiple of 8).
+ * Tiled (MFMA) kernels from M = 17, as for alv_gemv_bf16.
  */
 int alv_ffn_fused_bf16(alv_ffn_t w, const uint16_t* X, uint16_t* Y, int M, int ldx, int ldy, void* stream);
 
@@ -220,8 +224,9 @@ int alv_ffn_fused_noalloc(alv_ffn_t w, const float* X, float* Y, int M, int ldx,
 /*
  * out[M, I] = the activation a = bf16(act(g) * u) of the handle's last
  * alv_ffn_fused call (fp32 holding bf16 values), for M up to that call's
- * token count (all tokens when it had M <= 16 or M >= 32; otherwise the last
- * 16-token chunk). Test / parity entry point: lets a checker separate the
+ * token count (all tokens when it had M <= 16 or ran the tiled kernel, M >= 33
+ * for fp32 activations and M >= 17 for bf16; otherwise the last 16-token
+ * chunk). Test / parity entry point: lets a checker separate the
  * bf16 rounding points from the down projection.
  */
 int alv_ffn_activation(alv_ffn_t w, float* out, int M, void* stream);
