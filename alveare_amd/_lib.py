@@ -36,10 +36,12 @@ SIGNATURES: dict[str, tuple] = {
     "alv_ffn_activation": (_i, [_vp, _vp, _i, _vp]),
     "alv_ffn_gate_up": (_i, [_vp, _vp, _i, _i, _vp]),
     "alv_ffn_shape": (_i, [_vp, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i)]),
+    "alv_ffn_exec_shape": (_i, [_vp, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "alv_ffn_release": (None, [_vp]),
     "alv_dequant_q4": (_i, [_vp, _vp, _i, _i, _vp]),
     "alv_weight_register": (_i, [_vp, _i, _i, ctypes.POINTER(_vp), _vp]),
     "alv_weight_shape": (_i, [_vp, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
+    "alv_weight_exec_shape": (_i, [_vp, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "alv_gemv": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "alv_weight_release": (None, [_vp]),
     "alv_lm_head": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _vp, _vp]),

@@ -39,16 +39,13 @@ extern "C" int alv_chain_run(const alv_chain_op* ops, int n, int M, void* stream
         const alv_chain_op& c = ops[i];
         if (c.weight) {
             GemvLaunch L;
-            L.W0 = c.weight->w;
+            weight_launch(c.weight, L);
             L.X = c.x;
             L.ldx = c.weight->K;
             L.Y = c.y;
             L.ldy = c.weight->N;
             L.M = M;
-            L.N = c.weight->N;
-            L.K = c.weight->K;
             L.parts = 3;
-            L.tiled = true;
             if (int rc = launch_gemv(L, s)) return rc;
         } else {
             GemvLaunch two[2];

@@ -49,8 +49,9 @@ void ffn_ops(alv_ffn_t w, uint16_t* act, const float* X, int ldx, float* Y, int 
     up.Yb = act;
     up.ldy = w->I;
     up.M = M;
-    up.N = w->I;
-    up.K = w->H;
+    up.N = w->Ie;
+    up.K = w->He;
+    up.Nz = w->I;  // the activation of trimmed (all-zero) rows is zero
     up.parts = 3;
     up.glu = true;
     up.tiled = true;
@@ -63,8 +64,9 @@ void ffn_ops(alv_ffn_t w, uint16_t* act, const float* X, int ldx, float* Y, int 
     down.Y = Y;
     down.ldy = ldy;
     down.M = M;
-    down.N = w->H;
-    down.K = w->I;
+    down.N = w->He;
+    down.K = w->Ie;
+    down.Nz = w->H;
     down.parts = 1;
     down.tiled = true;
 }
@@ -91,15 +93,28 @@ extern "C" int alv_ffn_register(const uint8_t* Wg, const uint8_t* Wu, const uint
     h->H = H;
     h->I = I;
     h->act = act;
-    h->gate_bytes = gate_bytes;
-    h->down_bytes = down_bytes;
     int rc = hip_check(hipGetDevice(&h->device), "hipGetDevice");
-    if (!rc) rc = hip_check(hipMalloc(&h->w, 2 * gate_bytes + down_bytes), "hipMalloc(FFN weights)");
-    if (!rc) rc = launch_tile(Wg, h->w, I, H, s);
-    if (!rc) rc = launch_tile(Wu, h->w + gate_bytes, I, H, s);
-    if (!rc) rc = launch_tile(Wd, h->w + 2 * gate_bytes, H, I, s);
+    // Trailing all-zero rows and columns (the reference's padded FFN, 15360 x
+    // 3840 stored as 16384 x 4096) are trimmed: gate/up rows past Ie and
+    // columns past He, down rows past He and columns past Ie hold only zero
+    // weights, so the activation there is GLU(0, 0) = 0 and the output 0.
+    int eg[2] = {0, 0}, eu[2] = {0, 0}, ed[2] = {0, 0};
+    const uint32_t rs_h = (uint32_t)(H / kBlockK) * kBlockBytes, rs_i = (uint32_t)(I / kBlockK) * kBlockBytes;
+    if (!rc) rc = weight_extent(Wg, I, H, rs_h, s, eg);
+    if (!rc) rc = weight_extent(Wu, I, H, rs_h, s, eu);
+    if (!rc) rc = weight_extent(Wd, H, I, rs_i, s, ed);
+    auto up32 = [](int v) { return std::max(kBlockK, (v + kBlockK - 1) / kBlockK * kBlockK); };
+    h->He = std::min(H, up32(std::max({kBlockK * eg[1], kBlockK * eu[1], ed[0]})));
+    h->Ie = std::min(I, up32(std::max({eg[0], eu[0], kBlockK * ed[1]})));
+    h->gate_bytes = tile_bytes(h->Ie, h->He);
+    h->down_bytes = tile_bytes(h->He, h->Ie);
+    if (!rc) rc = hip_check(hipMalloc(&h->w, 2 * h->gate_bytes + h->down_bytes), "hipMalloc(FFN weights)");
+    if (!rc) rc = launch_tile(Wg, h->w, h->Ie, h->He, s, rs_h);
+    if (!rc) rc = launch_tile(Wu, h->w + h->gate_bytes, h->Ie, h->He, s, rs_h);
+    if (!rc) rc = launch_tile(Wd, h->w + 2 * h->gate_bytes, h->He, h->Ie, s, rs_i);
     h->a_cap = (size_t)I * kGemvMaxM;
     if (!rc) rc = hip_check(hipMalloc(&h->a, h->a_cap * sizeof(uint16_t)), "hipMalloc(FFN activation)");
+    if (!rc) rc = hip_check(hipMemsetAsync(h->a, 0, h->a_cap * sizeof(uint16_t), s), "hipMemsetAsync(FFN activation)");
     h->last_a = h->a;
     if (!rc) rc = hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
     if (rc) {
@@ -110,6 +125,13 @@ extern "C" int alv_ffn_register(const uint8_t* Wg, const uint8_t* Wu, const uint
         return rc;
     }
     *out = h;
+    return ALV_OK;
+}
+
+extern "C" int alv_ffn_exec_shape(alv_ffn_t w, int* H, int* I) {
+    if (int rc = check_handle(w)) return rc;
+    if (H) *H = w->He;
+    if (I) *I = w->Ie;
     return ALV_OK;
 }
 
@@ -249,6 +271,9 @@ extern "C" int alv_ffn_fused_bf16_addnorm(alv_ffn_t w, const uint16_t* resid, co
     int dev = -1;
     if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
     if (dev != w->device) return fail(ALV_ERR_HANDLE, "FFN handle belongs to device %d, current device is %d", w->device, dev);
+    if (w->He != w->H)
+        return fail(ALV_ERR_ARG, "a fused residual step needs the whole row: this FFN registered with its trailing "
+                    "all-zero hidden columns trimmed (H=%d executed as %d)", w->H, w->He);
     ResidStep st;
     st.resid = resid;
     st.y = y;

@@ -417,6 +417,19 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q4_kernel(GemmArgs a) {
             }
 }
 
+// Output rows [N, Nz) of every token as zeros (the all-zero trailing rows a
+// registration trimmed off).
+__global__ void __launch_bounds__(256) zero_rows_kernel(float* Y, uint16_t* Yb, int ldy, int M, int N, int Nz) {
+    const int nz = Nz - N;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < (int64_t)nz * M; i += (int64_t)gridDim.x * 256) {
+        const int m = (int)(i / nz), r = N + (int)(i % nz);
+        if (Yb)
+            Yb[(size_t)m * ldy + r] = 0;
+        else
+            Y[(size_t)m * ldy + r] = 0.0f;
+    }
+}
+
 // fp32 activations -> three bf16 term arrays (exact split, q4_device.h::split3)
 // once per call, so the GEMM reads half the bytes per activation and its
 // token tiles hold them in L2; flags[m] != 0 when token m has a nonzero second
@@ -561,7 +574,14 @@ int launch_gemm_tiled(const GemvLaunch& L, hipStream_t s) {
         e = L.tiled ? launch_gemm_x<2, true>(a, xf32, TM, grid, s) : launch_gemm_x<2, false>(a, xf32, TM, grid, s);
     else
         e = L.tiled ? launch_gemm_x<1, true>(a, xf32, TM, grid, s) : launch_gemm_x<1, false>(a, xf32, TM, grid, s);
-    return hip_check(e, "gemm_q4_kernel launch");
+    if (int rc = hip_check(e, "gemm_q4_kernel launch")) return rc;
+    if (L.Nz > L.N) {
+        const int64_t n = (int64_t)(L.Nz - L.N) * L.M;
+        const int zg = (int)std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, 1024));
+        hipLaunchKernelGGL(zero_rows_kernel, dim3(zg), dim3(256), 0, s, L.Y, L.Yb, L.ldy, L.M, L.N, L.Nz);
+        return hip_check(hipGetLastError(), "zero_rows_kernel launch");
+    }
+    return ALV_OK;
 }
 
 }  // namespace alv

@@ -66,6 +66,7 @@ struct Gemv1Args {
     int rt_q, rt_r;  // so group t owns rt_q + (t < rt_r) row tiles
     int ks;          // K splits: workgroup b is tile group b / ks, super-step range b % ks
     int act;
+    int Nz;          // output rows [N, Nz) of every token are written as zeros
     // Fused residual step (bf16 one-token launches; pr_r null: none).
     const uint16_t* pr_r;
     const uint16_t* pr_y;
@@ -597,6 +598,12 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const WgWork wk = wg_work(a, blockIdx.x);
     const int U = wk.nt * wk.nsw * NT;
+    if (a.Nz > a.N) {
+        // Trimmed all-zero rows: their outputs are zeros, spread over the grid.
+        const int nz = a.Nz - a.N;
+        for (int i = blockIdx.x * 64 * NW + tid; i < nz * a.M; i += gridDim.x * 64 * NW)
+            ystore(a, i / nz, a.N + i % nz, 0.0f);
+    }
     __bf16* xs = reinterpret_cast<__bf16*>(smem);
     f32x4* part = reinterpret_cast<f32x4*>(smem + (size_t)wk.nsw * 1024 * SR);
     // Unit counter of the workgroup, after the unit slots: the first P * NW
@@ -890,6 +897,7 @@ int fill_args(const GemvLaunch& L, const Gemv1Plan& p, int m0, int m, hipStream_
     a.rt_r = p.rt_r;
     a.ks = p.ks;
     a.act = L.act;
+    a.Nz = L.Nz;
     if (const ResidStep* st = L.step) {
         a.pr_r = st->resid;
         a.pr_y = st->y;

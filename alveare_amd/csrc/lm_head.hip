@@ -129,16 +129,15 @@ extern "C" int alv_lm_head(alv_weight_t w, const float* x, float* logits, int vo
     int* pi = reinterpret_cast<int*>(pv + kHeadGroups);
     // The GEMV over the first `vocab` rows (rows are independent).
     GemvLaunch L;
-    L.W0 = w->w;
+    weight_launch(w, L);
     L.X = x;
     L.ldx = w->K;
     L.Y = logits;
     L.ldy = vocab;
     L.M = 1;
-    L.N = vocab;
-    L.K = w->K;
+    L.N = std::min(vocab, w->Ne);  // rows past the registered extent are zero logits
+    L.Nz = vocab;
     L.parts = 3;
-    L.tiled = true;
     if (int rc = launch_gemv(L, s)) return rc;
     const int groups = std::min(kHeadGroups, (vocab + 63) / 64);
     hipLaunchKernelGGL(head_kernel, dim3(groups), dim3(kHeadThreads), 0, s, logits, vocab, softcap, pv, pi);

@@ -102,6 +102,9 @@ struct GemvLaunch {
     int act = ALV_ACT_GELU_TANH;
     const SplitBuf* split = nullptr;  // caller's split-K temporaries (nullptr: the stream's)
     const ResidStep* step = nullptr;  // fused residual step (M = 1, bf16 activation; nullptr: X / Xb as given)
+    // Output rows [N, Nz) of every token are written as zeros (the all-zero
+    // trailing rows a registration trimmed off, see weight_extent); Nz <= N: none.
+    int Nz = 0;
 };
 int launch_gemv(const GemvLaunch& L, hipStream_t s);
 // The split-K partial-sum bytes launch_gemv(L) needs (0: no launch splits K),
@@ -111,10 +114,18 @@ int64_t gemv_split_bytes(const GemvLaunch& L);
 // Arrival counters per stream: one per tile group of a split-K launch.
 constexpr int kSplitCounters = 1024;
 
-// Repack W (combined layout, N x K) into the tiled layout at `out`
-// (tile_bytes(N, K) bytes), on `s` (tile_q.hip).
-int launch_tile(const uint8_t* W, uint8_t* out, int N, int K, hipStream_t s);
+// Repack W (combined layout, N x K, rows `rs` bytes apart; 0: K / 32 * 20)
+// into the tiled layout at `out` (tile_bytes(N, K) bytes), on `s` (tile_q.hip).
+int launch_tile(const uint8_t* W, uint8_t* out, int N, int K, hipStream_t s, uint32_t rs = 0);
 uint64_t tile_bytes(int N, int K);
+
+// The part of a combined-layout matrix (N x K, rows `rs` bytes apart) that
+// holds nonzero weights: ext[0] = 1 + its last row with a nonzero weight,
+// ext[1] = 1 + its last 32-column block with one (0 and 0 when every weight
+// is zero). A block's 32 weights bf16(q * s) are all zero exactly when its
+// scale is +-0, or its codes are all zero and its scale is finite. Enqueued
+// on `s`, then synchronised (tile_q.hip).
+int weight_extent(const uint8_t* W, int N, int K, uint32_t rs, hipStream_t s, int ext[2]);
 
 // Largest M the streaming kernel takes in one launch (3 * 16 = 48 A rows).
 constexpr int kGemvMaxM = 16;
@@ -152,6 +163,10 @@ int device_cus();
 // the GLU epilogue into the bf16 activation `act`, then down from it.
 void ffn_ops(alv_ffn_t w, uint16_t* act, const float* X, int ldx, float* Y, int ldy, int M, GemvLaunch (&op)[2]);
 
+// The launch of registered matrix w (tile_q.hip): weights, executed shape and
+// the zero rows up to its logical N; the caller adds activations and M.
+void weight_launch(const struct alv_weight* w, GemvLaunch& L);
+
 }  // namespace alv
 
 namespace alv {
@@ -160,11 +175,19 @@ constexpr uint32_t kFfnMagic = 0xA1FEED42u;     // live alv_ffn
 }  // namespace alv
 
 // Registered projection (tile_q.hip).
+// Registration keeps the nonzero part of a matrix only: a padded matrix (the
+// reference quantizer zero-pads Gemma-4's K to 4096 and its FFN to 16384 x
+// 4096, tools/quantize_gemma4.py:145-187; its runtime pads the sliding O
+// projection to 8192 rows, runtime/cpp/src/weights.cpp:318-327) is streamed
+// at the executed shape Ne x Ke, and the trimmed rows [Ne, N) are written as
+// exact zeros -- the value the reference computes there up to the sign of
+// zero. N and K stay the caller's (logical) shape for every argument check.
 struct alv_weight {
     uint32_t magic;
     int device;
     int N, K;
-    uint8_t* w;  // tiled copy, tile_bytes(N, K)
+    int Ne, Ke;  // executed shape: the leading Ne rows and Ke columns
+    uint8_t* w;  // tiled copy, tile_bytes(Ne, Ke)
 };
 
 // Registered FFN layer (ffn_fused.hip).
@@ -172,6 +195,7 @@ struct alv_ffn {
     uint32_t magic;
     int device;
     int H, I, act;
+    int He, Ie;  // executed shape (trailing all-zero rows and columns trimmed, as for alv_weight)
     uint8_t* w;  // one allocation: gate | up | down, tiled layout (q4_device.h)
     size_t gate_bytes, down_bytes;
     uint16_t* a;  // decode activation (bf16 bit patterns), kGemvMaxM x I, fixed for the handle's life

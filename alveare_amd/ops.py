@@ -234,6 +234,14 @@ class Q4Weight:
             raise ValueError("weights were released")
         return self._h.value
 
+    @property
+    def exec_shape(self) -> tuple[int, int]:
+        """(N, K) the kernels stream: registration drops trailing rows and
+        32-column blocks whose weights are all zero (padded shapes)."""
+        n, k = ctypes.c_int(), ctypes.c_int()
+        check(lib().alv_weight_exec_shape(self.handle, ctypes.byref(n), ctypes.byref(k)), "alv_weight_exec_shape")
+        return n.value, k.value
+
     def close(self) -> None:
         if self._h:
             with torch.cuda.device(self.device):
@@ -292,6 +300,14 @@ class FfnWeights:
         if not self._h:
             raise ValueError("FFN weights were released")
         return self._h.value
+
+    @property
+    def exec_shape(self) -> tuple[int, int]:
+        """(H, I) the kernels run at after registration dropped trailing
+        all-zero hidden / intermediate rows and columns (padded shapes)."""
+        h, i = ctypes.c_int(), ctypes.c_int()
+        check(lib().alv_ffn_exec_shape(self.handle, ctypes.byref(h), ctypes.byref(i)), "alv_ffn_exec_shape")
+        return h.value, i.value
 
     def close(self) -> None:
         if self._h:

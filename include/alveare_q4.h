@@ -92,11 +92,22 @@ int alv_gemm_q(const uint8_t* W, const float* X, float* Y, int M, int N, int K,
  * Replaces NpuRegistry::create_gemv_weight (runtime/cpp/include/alveare/npu.h:68-69,
  * runtime/cpp/src/npu.cpp:241-253); the reference also registers weights once
  * and keeps them device-resident (runtime/py/model.py:31-35 ResidentWeight).
+ * Trailing rows and 32-column blocks whose weights are all zero (the zero
+ * padding of the reference's Gemma-4 shapes: K 3840 stored as 4096,
+ * tools/quantize_gemma4.py:145-187; the sliding O projection padded to 8192
+ * rows, runtime/cpp/src/weights.cpp:318-327) are not copied: calls stream the
+ * nonzero part and write exact zeros to the trimmed output rows, the
+ * reference's values there up to the sign of zero.
  */
 int alv_weight_register(const uint8_t* W, int N, int K, alv_weight_t* out, void* stream);
 
-/* Shape of a registered projection (either output pointer may be NULL). */
+/* Shape of a registered projection as registered (either pointer may be NULL). */
 int alv_weight_shape(alv_weight_t w, int* N, int* K);
+
+/* Shape a registered projection executes at: its rows and columns up to the
+ * last nonzero weight (rounded up to a 32-column block). No reference
+ * counterpart: it reports what alv_weight_register trimmed. */
+int alv_weight_exec_shape(alv_weight_t w, int* N, int* K);
 
 /*
  * Y[M,N] = X[M,K] @ dequant(W)^T with W registered; rows of X/Y at leading
@@ -178,10 +189,17 @@ int alv_q4_tile(const uint8_t* W, uint8_t* out, int N, int K, void* stream);
  * Replaces NpuRegistry::create_ffn_fused_weight (npu.h:70-71, npu.cpp:255-267)
  * together with the registration-time repack pack_ffn_fused_weights
  * (runtime/cpp/src/weights.cpp:94-190; kernels/ffn_fused/ffn_fused.py:330-395).
- * Synchronises `stream` before returning.
+ * Trailing all-zero hidden / intermediate rows and columns (the reference's
+ * 15360 x 3840 FFN stored as 16384 x 4096, tools/quantize_gemma4.py:177-187)
+ * are trimmed as in alv_weight_register: their activations and outputs are
+ * exact zeros. Synchronises `stream` before returning.
  */
 int alv_ffn_register(const uint8_t* Wg, const uint8_t* Wu, const uint8_t* Wd, int H, int I,
                      int act, alv_ffn_t* out, void* stream);
+
+/* The (H, I) a registered FFN executes at after trimming (either pointer may
+ * be NULL). No reference counterpart. */
+int alv_ffn_exec_shape(alv_ffn_t w, int* H, int* I);
 
 /*
  * Y[M,H] = down(GLU(gate X, up X)) with the reference CPU path's bf16 rounding

@@ -184,7 +184,8 @@ def test_tile_layout_matches_definition(orc, dev, N, K):
 
 
 REG_SHAPES = [(2048, 2048), (8192, 3840), (3840, 4096), (3840, 15360), (333, 1152), (17, 96), (1, 32),
-              (100, 480)]
+              (100, 480),
+              (8704, 3840), (3840, 8192)]  # Gemma-4 global layers: fused q (16 x 512) + k (512), and O
 
 
 @pytest.mark.parametrize("N,K", REG_SHAPES)

@@ -77,10 +77,11 @@ def test_ffn_noalloc_matches_allocating_entry_point(orc, dev):
 
     # H = 4096, I = 65536 at 16 tokens: the gate/up launch needs 32 MiB of
     # split-K partial sums, beyond the fixed 16 MiB, so the call is refused and
-    # writes nothing. The weights' values do not matter.
+    # writes nothing. The weights' values do not matter as long as they are
+    # nonzero (registration trims all-zero trailing rows and columns).
     H2, I2 = 4096, 65536
-    Wz = torch.zeros((I2, H2 // 32 * 20), dtype=torch.uint8, device=dev)
-    Wdz = torch.zeros((H2, I2 // 32 * 20), dtype=torch.uint8, device=dev)
+    Wz = torch.full((I2, H2 // 32 * 20), 0x11, dtype=torch.uint8, device=dev)
+    Wdz = torch.full((H2, I2 // 32 * 20), 0x11, dtype=torch.uint8, device=dev)
     f2 = aa.FfnWeights(Wz, Wz, Wdz, H2, I2, "gelu")
     del Wz, Wdz
     X2 = torch.zeros((16, H2), device=dev)
