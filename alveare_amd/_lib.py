@@ -64,8 +64,6 @@ SIGNATURES: dict[str, tuple] = {
     "alv_q4_tiled_bytes": (ctypes.c_uint64, [_i, _i]),
     "alv_q4_tile": (_i, [_vp, _vp, _i, _i, _vp]),
     "alv_chain_run": (_i, [_vp, _i, _i, _vp]),
-    "alv_stream_read": (_i, [_vp, ctypes.c_size_t, _vp, _vp]),
-    "alv_stream_read_shape": (_i, [_vp, ctypes.c_size_t, _vp, _i, _i, _vp]),
     "alv_glu": (_i, [_vp, _vp, _vp, ctypes.c_int64, _i, _vp]),
 }
 

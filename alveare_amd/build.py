@@ -75,7 +75,26 @@ def build(verbose: bool = True) -> str:
     if verbose:
         print(f"built {LIB}")
     build_adapter(verbose)
+    build_probe(verbose)
     return LIB
+
+
+PROBE_SRC = os.path.join(ROOT, "measure", "read_probe.hip")
+PROBE_LIB = os.path.join(ROOT, "measure", "libalveare_probe.so")
+
+
+def build_probe(verbose: bool = True) -> str:
+    """The benchmark's streaming-read probe, a library of its own
+    (measure/libalveare_probe.so), not part of libalveare_q4.so."""
+    tmp = PROBE_LIB + ".tmp"
+    cmd = [_hipcc(), *HIPCC_FLAGS, "-shared", PROBE_SRC, "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {PROBE_SRC}:\n{r.stderr}")
+    os.replace(tmp, PROBE_LIB)
+    if verbose:
+        print(f"built {PROBE_LIB}")
+    return PROBE_LIB
 
 
 def _run(cmd: list[str], what: str) -> None:

@@ -13,14 +13,18 @@
 //   * errors are std::runtime_error (invalid handle, shape mismatch, a
 //     failing device call).
 // Differences that follow from the hardware:
-//   * there is no AOT kernel manifest: every shape with K (and H, I) a
-//     multiple of 32 has a kernel, so has_* answer by shape, kernels() is
-//     empty and the context budget / pinning calls do nothing. The manifest
-//     path is read only for "model_type" when the file exists;
+//   * no per-shape kernels are compiled: every shape with K (and H, I) a
+//     multiple of 32 has a kernel, so has_* answer by shape and the context
+//     budget / pinning calls do nothing. The manifest, when the file exists,
+//     is read for "model_type" and its "kernels" list, which kernels()
+//     returns (so drivers that walk it, runtime/cpp/test/parity_test.cpp,
+//     exercise its shapes);
 //   * create_ffn_fused_weight takes the reference's packed blob
-//     (pack_ffn_fused_weights, runtime/cpp/src/weights.cpp:94-190, with
-//     m_I = 32 and k_tile = 128 for H = 1152, else 256 -- set_ffn_packing
-//     changes them) and unpacks it to gate / up / down before registering.
+//     (pack_ffn_fused_weights, runtime/cpp/src/weights.cpp:94-190) and
+//     unpacks it to gate / up / down before registering. Its m_I and k_tile
+//     come from set_ffn_packing, else the manifest's ffn_fused kernel of the
+//     same (H, I, activation), else the reference loader's rule (m_I = 32,
+//     k_tile = 128 for H = 1152, else 256).
 #pragma once
 
 #include <cstddef>
@@ -31,8 +35,8 @@
 
 namespace alveare {
 
-// One kernel of the reference's AOT manifest (kernels/build/manifest.json).
-// The GPU registry compiles no per-shape kernels, so its list is empty.
+// One kernel of the reference's AOT manifest (kernels/build/manifest.json),
+// as kernels() lists it from the manifest file.
 struct KernelSpec {
     std::string kind;
     int N = 0;

@@ -6,6 +6,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cstdio>
 #include <cstring>
@@ -74,6 +75,127 @@ struct DevBuf {
         if (p) (void)hipFree(p);
     }
 };
+
+// ---- the kernel manifest (kernels/build/manifest.json) -----------------------
+// A small JSON reader for the manifest the reference registry loads
+// (runtime/cpp/src/npu.cpp:186-216): "model_type" and the "kernels" array of
+// objects with string and integer fields. Anything else is skipped.
+struct Json {
+    const std::string& s;
+    size_t i = 0;
+    explicit Json(const std::string& t) : s(t) {}
+    void ws() {
+        while (i < s.size() && (s[i] == ' ' || s[i] == '\t' || s[i] == '\n' || s[i] == '\r')) ++i;
+    }
+    bool eat(char c) {
+        ws();
+        if (i < s.size() && s[i] == c) {
+            ++i;
+            return true;
+        }
+        return false;
+    }
+    void need(char c) {
+        if (!eat(c)) throw std::runtime_error(std::string("npu: manifest: expected '") + c + "'");
+    }
+    std::string str() {
+        need('"');
+        std::string out;
+        while (i < s.size() && s[i] != '"') {
+            char c = s[i++];
+            if (c == '\\' && i < s.size()) {
+                const char e = s[i++];
+                c = e == 'n' ? '\n' : e == 't' ? '\t' : e == 'r' ? '\r' : e == 'b' ? '\b' : e == 'f' ? '\f' : e;
+                if (e == 'u') {  // \uXXXX: kept as '?' (no manifest field needs it)
+                    i = std::min(s.size(), i + 4);
+                    c = '?';
+                }
+            }
+            out += c;
+        }
+        need('"');
+        return out;
+    }
+    // Skip one value of any kind; returns it as text for scalars.
+    std::string value() {
+        ws();
+        if (i >= s.size()) throw std::runtime_error("npu: manifest: unexpected end");
+        if (s[i] == '"') return str();
+        if (s[i] == '{' || s[i] == '[') {
+            const char open = s[i], close = open == '{' ? '}' : ']';
+            ++i;
+            if (eat(close)) return "";
+            do {
+                if (open == '{') {
+                    str();
+                    need(':');
+                }
+                value();
+            } while (eat(','));
+            need(close);
+            return "";
+        }
+        const size_t b = i;
+        while (i < s.size() && s[i] != ',' && s[i] != '}' && s[i] != ']' && s[i] != ' ' && s[i] != '\n' &&
+               s[i] != '\r' && s[i] != '\t')
+            ++i;
+        return s.substr(b, i - b);
+    }
+};
+
+int json_int(const std::string& v) {
+    try {
+        return v.empty() ? 0 : (int)std::stod(v);
+    } catch (const std::exception&) {
+        return 0;
+    }
+}
+
+// model_type and the kernel list of a manifest's text.
+void parse_manifest(const std::string& text, std::string* model_type, std::vector<alveare::KernelSpec>* specs) {
+    Json j(text);
+    j.need('{');
+    if (j.eat('}')) return;
+    do {
+        const std::string key = j.str();
+        j.need(':');
+        if (key == "model_type") {
+            *model_type = j.value();
+        } else if (key == "kernels") {
+            j.need('[');
+            if (j.eat(']')) continue;
+            do {
+                alveare::KernelSpec k;
+                j.need('{');
+                if (!j.eat('}')) {
+                    do {
+                        const std::string f = j.str();
+                        j.need(':');
+                        const std::string v = j.value();
+                        if (f == "kind") k.kind = v;
+                        else if (f == "N") k.N = json_int(v);
+                        else if (f == "K") k.K = json_int(v);
+                        else if (f == "B") k.B = json_int(v);
+                        else if (f == "H") k.H = json_int(v);
+                        else if (f == "I") k.I = json_int(v);
+                        else if (f == "activation") k.activation = v;
+                        else if (f == "m") k.m = json_int(v);
+                        else if (f == "k_tile") k.k_tile = json_int(v);
+                        else if (f == "n_cores") k.n_cores = json_int(v);
+                        else if (f == "xclbin") k.xclbin = v;
+                        else if (f == "insts") k.insts = v;
+                    } while (j.eat(','));
+                    j.need('}');
+                }
+                specs->push_back(std::move(k));
+            } while (j.eat(','));
+            j.need(']');
+        } else {
+            j.value();
+        }
+    } while (j.eat(','));
+    j.need('}');
+}
 
 }  // namespace
 
@@ -203,13 +325,7 @@ NpuRegistry::NpuRegistry(const std::string& manifest_path, unsigned device_index
     if (f) {
         std::stringstream ss;
         ss << f.rdbuf();
-        const std::string s = ss.str();
-        const size_t k = s.find("\"model_type\"");
-        if (k != std::string::npos) {
-            const size_t q0 = s.find('"', s.find(':', k) + 1);
-            const size_t q1 = q0 == std::string::npos ? q0 : s.find('"', q0 + 1);
-            if (q1 != std::string::npos) impl_->model_type = s.substr(q0 + 1, q1 - q0 - 1);
-        }
+        parse_manifest(ss.str(), &impl_->model_type, &impl_->kernels);
     }
 }
 
@@ -254,8 +370,18 @@ WeightHandle NpuRegistry::create_ffn_fused_weight(int H, int I, const std::strin
     std::lock_guard<std::mutex> lk(impl_->mu);
     impl_->enter();
     const int act = act_id(activation);
-    const int m_I = impl_->m_I ? impl_->m_I : 32;
-    const int k_tile = impl_->k_tile ? impl_->k_tile : (H == 1152 ? 128 : 256);
+    // The blob's packing: set_ffn_packing's, else the manifest's ffn_fused
+    // kernel of this shape (its m and k_tile, npu.cpp:211-213), else the
+    // reference loader's rule (weights.cpp:364-365).
+    int m_I = 32, k_tile = H == 1152 ? 128 : 256;
+    for (const KernelSpec& k : impl_->kernels)
+        if (k.kind == "ffn_fused" && k.H == H && k.I == I && act_id(k.activation.empty() ? "gelu" : k.activation) == act) {
+            if (k.m > 0) m_I = k.m;
+            if (k.k_tile > 0) k_tile = k.k_tile;
+            break;
+        }
+    if (impl_->m_I) m_I = impl_->m_I;
+    if (impl_->k_tile) k_tile = impl_->k_tile;
     const size_t gb = (size_t)I * (H / 32) * 20, db = (size_t)H * (I / 32) * 20;
     std::vector<uint8_t> host(2 * gb + db);
     if (alvnpu_unpack_ffn(static_cast<const uint8_t*>(packed), nbytes, H, I, m_I, k_tile, host.data(),

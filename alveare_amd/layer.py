@@ -308,6 +308,11 @@ def cos_sin_table_gemma(base: float, dim: int, max_seq_len: int, gemma4: bool = 
     return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
 
 
+# Longest attention span (the sliding window, or a global layer's cache) the
+# chunked attention takes: its merge holds 1024 chunk partials of 64 positions.
+ATTN_MAX_SPAN = 1024 * 64
+
+
 class Gemma4DecodeLayer:
     """One Gemma-4 decoder layer with every step on the device
     (runtime/py/model.py:705-790 with the NPU matmuls). Weights are combined
@@ -327,6 +332,10 @@ class Gemma4DecodeLayer:
         self.k_size = self.kv_heads * self.D
         self.n_qkv = self.q_size + (2 if sliding else 1) * self.k_size
         self.window = 1024 if sliding else 0
+        span = min(self.window, max_seq) if sliding else max_seq
+        if max_seq < 1 or span > ATTN_MAX_SPAN:
+            raise ValueError(f"max_seq={max_seq}: attention takes up to {ATTN_MAX_SPAN} positions per "
+                             f"{'window' if sliding else 'global'} span (its chunk merge holds 1024 chunks of 64)")
         self.scale = float(np.float32(scale))
 
         def dev_u8(a):
@@ -440,6 +449,13 @@ class Gemma4Decoder:
         self.final_norm = _f32(final_norm, "final_norm", self.H, self.device)
         self.head, self.vocab, self.softcap = head, vocab, softcap
         self.scale = math.sqrt(self.H)
+        # Positions the KV caches hold: a step at pos >= max_pos would write
+        # past them (the reference raises IndexError there). The host tracks
+        # the position through step() and replay(); on the device a step at
+        # such a position writes token -1 (never a vocabulary token), so raw
+        # graph replays past the end cannot yield a plausible token.
+        self.max_pos = min(L.max_seq for L in layers) if layers else 1 << 30
+        self.pos_host = 0  # the position of the next step, as last seen by the host
         self.token_dev = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.x = torch.empty(self.H, dtype=torch.bfloat16, device=self.device)
         self.x_norm = torch.empty(head.K, dtype=torch.bfloat16, device=self.device)
@@ -471,21 +487,49 @@ class Gemma4Decoder:
             rmsnorm(h, self.final_norm, K=self.H, pad=self.head.K, out=self.x_norm)
         self.x_f32.copy_(self.x_norm)
         lm_head(self.head, self.x_f32, self.vocab, self.softcap, self.logits, token=self.token_dev)
+        self.token_dev.masked_fill_(self.pos_dev >= self.max_pos, -1)
         self.pos_dev.add_(1)
+
+    def _check_pos(self, pos: int) -> None:
+        if not 0 <= pos < self.max_pos:
+            raise IndexError(f"decode position {pos} outside the KV caches' {self.max_pos} positions")
+
+    def _current_pos(self) -> int:
+        # The device position is authoritative (callers may set pos_dev
+        # themselves); reading it synchronises, as an eager step does anyway.
+        self.pos_host = int(self.pos_dev.item())
+        return self.pos_host
 
     def step(self, token: int | None = None, pos: int | None = None) -> int:
         """One eager step (from `token` at `pos` when given, else from the
-        device state); returns the greedy next token."""
+        device state); returns the greedy next token. Raises IndexError when
+        the position is past the KV caches."""
+        p = int(pos) if pos is not None else self._current_pos()
+        self._check_pos(p)
         self.stream.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(self.stream):
             if token is not None:
                 self.token_dev.fill_(int(token))
             if pos is not None:
-                self.pos_dev.fill_(int(pos))
+                self.pos_dev.fill_(p)
             self.enqueue()
             tok = int(self.token_dev.item())
         torch.cuda.current_stream(self.device).wait_stream(self.stream)
+        self.pos_host = p + 1
         return tok
+
+    def replay(self, graph: torch.cuda.CUDAGraph, steps: int = 1) -> None:
+        """Replay a captured step `steps` times on the decoder's stream,
+        refusing (IndexError, before anything runs) when the last of them
+        would be past the KV caches."""
+        p = self._current_pos()
+        self._check_pos(p + steps - 1)
+        self.stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(self.stream):
+            for _ in range(steps):
+                graph.replay()
+        torch.cuda.current_stream(self.device).wait_stream(self.stream)
+        self.pos_host = p + steps
 
     def capture(self) -> torch.cuda.CUDAGraph:
         """A HIP graph of one step on the decoder's stream (run one eager
@@ -498,3 +542,10 @@ class Gemma4Decoder:
         with torch.cuda.graph(g, stream=self.stream):
             self.enqueue()
         return g
+
+    def set_position(self, pos: int) -> None:
+        """Point the next step at `pos` (the device position and the host's
+        record of it)."""
+        self._check_pos(int(pos))
+        self.pos_dev.fill_(int(pos))
+        self.pos_host = int(pos)

@@ -388,14 +388,35 @@ def padded_shapes(torch, aa, dev) -> dict:
     return out
 
 
+_PROBE = None
+
+
+def probe_lib():
+    """measure/libalveare_probe.so (the streaming-read probe), built by
+    __graft_entry__.build() beside the product library."""
+    global _PROBE
+    if _PROBE is None:
+        import ctypes
+        path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "measure", "libalveare_probe.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built (run __graft_entry__.build())")
+        lib = ctypes.CDLL(path)
+        lib.alvprobe_stream_read.restype = ctypes.c_int
+        lib.alvprobe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
+                                             ctypes.c_int, ctypes.c_void_p]
+        lib.alvprobe_last_error.restype = ctypes.c_char_p
+        _PROBE = lib
+    return _PROBE
+
+
 def read_floor(torch, aa, dev) -> dict:
     """The practical ceiling per launch: a plain streaming read of each op's
     weight bytes, from distinct regions of a 2 GiB buffer (far beyond the
-    Infinity Cache), timed like the ops: the default shape (alv_stream_read,
-    4 workgroups per CU, 4 loads in flight per thread) and the fastest of a
-    sweep over queue depth (alv_stream_read_shape: 2-8 workgroups per CU,
+    Infinity Cache), timed like the ops: the default shape (4 workgroups per
+    CU, 4 loads in flight per thread) and the fastest of a sweep over queue
+    depth (measure/libalveare_probe.so: 2-8 workgroups per CU,
     4-16 loads per thread, up to 512 KiB in flight per CU)."""
-    L = aa.lib()
+    L = probe_lib()
     big = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
     sink = torch.zeros(2048, dtype=torch.int32, device=dev)
     sizes = {"qkv": q4_bytes(N_QKV, H), "o": q4_bytes(H, K_O), "ffn_gate_up": 2 * q4_bytes(I_FF, H),
@@ -409,9 +430,9 @@ def read_floor(torch, aa, dev) -> dict:
             def fn():
                 st = torch.cuda.current_stream().cuda_stream
                 for i in range(n):
-                    rc = L.alv_stream_read_shape(big.data_ptr() + i * nb, nb, sink.data_ptr(), wg, depth, st)
+                    rc = L.alvprobe_stream_read(big.data_ptr() + i * nb, nb, sink.data_ptr(), wg, depth, st)
                     if rc:
-                        raise RuntimeError(f"alv_stream_read_shape failed ({rc})")
+                        raise RuntimeError(f"alvprobe_stream_read failed: {L.alvprobe_last_error().decode()}")
             return graph_us(torch, fn, 3, n)
 
         us = timed(4, 4)
@@ -715,7 +736,7 @@ def main() -> int:
         extra["decode_step_gemma4_48l"] = decode_step(torch, aa, dev)
         extra["eager_call_us"] = eager_calls(torch, aa, dev)
 
-    from alveare_amd import profiling
+    from measure import profiling
 
     out = {
         "metric": "Q4 GEMV/fused-FFN achieved HBM GB/s (% of peak) + µs/layer at 3840×15360",

@@ -411,24 +411,6 @@ int alv_dequant_q4(const uint8_t* W, uint16_t* out, int N, int K, void* stream);
  */
 int alv_glu(const float* g, const float* u, float* out, int64_t n, int act, void* stream);
 
-/*
- * Read `bytes` at `buf` once with a plain streaming kernel and XOR-fold them
- * into sink[0], sink[32], ..., sink[32 * 63] (sink: 2048 words of device
- * memory; the XOR of those 64 words changes by the XOR of every word read).
- * Measurement aid with no counterpart in the reference: the practical HBM
- * read ceiling for a launch of that size, which the benchmark reports beside
- * the Q4 kernels. buf and bytes need 16-byte alignment.
- */
-int alv_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream);
-
-/*
- * alv_stream_read with its launch shape chosen: wg_per_cu 256-thread
- * workgroups per CU (1-8) and `depth` 16-byte loads in flight per thread and
- * pass (2, 4, 8 or 16); alv_stream_read is wg_per_cu 4, depth 4. The
- * benchmark sweeps these to find the deepest-queue read ceiling per launch.
- * Measurement aid with no counterpart in the reference.
- */
-int alv_stream_read_shape(const void* buf, size_t bytes, uint32_t* sink, int wg_per_cu, int depth, void* stream);
 
 #ifdef __cplusplus
 }

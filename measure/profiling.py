@@ -1,13 +1,13 @@
 """Summaries of rocprofv3 output for the Q4 decode kernels.
 
-    python -m alveare_amd.profiling stats <dir>
+    python -m measure.profiling stats <dir>
         per-kernel calls / average / min / max duration from a
         ``rocprofv3 --kernel-trace --stats`` output directory.
-    python -m alveare_amd.profiling launches <dir>
+    python -m measure.profiling launches <dir>
         the same run's Q4 dispatches grouped by launch shape (grid, LDS).
-    python -m alveare_amd.profiling counters <dir>
+    python -m measure.profiling counters <dir>
         mean per dispatch of every counter of a ``--pmc`` run, per Q4 kernel.
-    python -m alveare_amd.profiling traffic <fetch_dir> <write_dir> <copy_bytes>
+    python -m measure.profiling traffic <fetch_dir> <write_dir> <copy_bytes>
         HBM bytes per dispatch of every q4 kernel from one ``--pmc FETCH_SIZE``
         and one ``--pmc WRITE_SIZE`` run of ``bench.py --profile-pass``, each
         scaled by what the counter reads for the pass's calibration copy (an

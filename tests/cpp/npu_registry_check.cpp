@@ -7,6 +7,8 @@
 //   npu_registry_check gemm_streamed B N K W x y
 //   npu_registry_check ffn H I act packed x y [m_I k_tile]
 //   npu_registry_check errors N K W
+//   npu_registry_check manifest out.txt      (kernels() of $NPU_MANIFEST as text)
+// NPU_MANIFEST, when set, is the manifest the registry reads.
 // Prints "ok" and exits 0, or prints the exception and exits 1.
 #include <cstdio>
 #include <cstdlib>
@@ -33,7 +35,21 @@ int main(int argc, char** argv) {
     try {
         if (argc < 2) throw std::runtime_error("usage: npu_registry_check <mode> ...");
         const std::string mode = argv[1];
-        alveare::NpuRegistry reg("/nonexistent/manifest.json");
+        // NPU_MANIFEST names a manifest for the registry to read (none by default).
+        const char* mf = getenv("NPU_MANIFEST");
+        alveare::NpuRegistry reg(mf ? mf : "/nonexistent/manifest.json");
+        if (mode == "manifest" && argc == 3) {
+            // kernels() as text, one kernel a line, into argv[2]
+            std::string out = "model_type " + reg.model_type() + "\n";
+            for (const alveare::KernelSpec& k : reg.kernels())
+                out += k.kind + " " + std::to_string(k.N) + " " + std::to_string(k.K) + " " + std::to_string(k.B) +
+                       " " + std::to_string(k.H) + " " + std::to_string(k.I) + " " + k.activation + " " +
+                       std::to_string(k.m) + " " + std::to_string(k.k_tile) + " " + std::to_string(k.n_cores) + " " +
+                       k.xclbin + "\n";
+            spit(argv[2], out.data(), out.size());
+            printf("ok\n");
+            return 0;
+        }
         if (mode == "gemv" && argc == 7) {
             const int N = atoi(argv[2]), K = atoi(argv[3]);
             auto W = slurp(argv[4]);

@@ -127,6 +127,64 @@ def ffn_check(orc, Wg, Wu, Wd, x, H, I, act, y_test, a_test=None, tol=TOL, cache
     return {"max_rel": max_rel(y_test, y_ref), "flips": int(len(flips)), "down_max_rel": e1}
 
 
+def ffn_check_batch(orc, Wg, Wu, Wd, X, H, I, act, Y_test, A_test, tol=TOL):
+    """ffn_check for every token of a batch at once, against the exact
+    (float64) arithmetic on the oracle's dequantized matrices instead of the
+    float32 oracle (whose per-token cost is a full dequantization): for each
+    token, (1) the down projection of the tested activation within tol of
+    max|y|, (2) activation flips against a64 = GLU(bf16(g64), bf16(u64)) rare
+    and each on a bf16 rounding midpoint within the fp32 error bound of g, u
+    or the GLU product, (3) y within tol * max|y| plus the flips' exact
+    contribution. Returns per-batch figures: the worst end-to-end max-rel, the
+    worst down-projection max-rel, flip counts, and how many tokens exceed tol
+    end to end before the flip budget."""
+    X = np.asarray(X, np.float32).reshape(-1, H)
+    M = X.shape[0]
+    X64 = X.astype(np.float64)
+    G = deq_f64(orc, Wg, I, H).reshape(I, H)
+    U = deq_f64(orc, Wu, I, H).reshape(I, H)
+    D = deq_f64(orc, Wd, H, I).reshape(H, I)
+    g64 = X64 @ G.T
+    u64 = X64 @ U.T
+    gb = orc.bf16_round(g64.astype(np.float32)).reshape(M, I)
+    ub = orc.bf16_round(u64.astype(np.float32)).reshape(M, I)
+    a64 = orc.glu(gb, ub, act).reshape(M, I)
+    A_test = np.asarray(A_test, np.float32).reshape(M, I)
+    Y_test = np.asarray(Y_test, np.float64).reshape(M, H)
+    y_ref = a64.astype(np.float64) @ D.T
+    y_at = A_test.astype(np.float64) @ D.T
+    scale = np.max(np.abs(y_ref), axis=1)
+    e_down = np.max(np.abs(Y_test - y_at), axis=1) / np.maximum(np.max(np.abs(y_at), axis=1), 1e-30)
+    assert np.all(e_down <= tol), f"down projection max-rel {e_down.max():.3e} > {tol} (token {int(np.argmax(e_down))})"
+    flip_m, flip_i = np.nonzero(A_test != a64)
+    per_tok = np.bincount(flip_m, minlength=M)
+    assert np.all(per_tok <= max(2, FLIP_RATE * I)), f"{per_tok.max()} activation flips in one token of {I}"
+    if len(flip_m):
+        xa = np.abs(X64[flip_m])
+        bg = np.sum(np.abs(G[flip_i]) * xa, axis=1) * 2 * H * U32
+        bu = np.sum(np.abs(U[flip_i]) * xa, axis=1) * 2 * H * U32
+        near_g = _midpoint_dist(g64[flip_m, flip_i]) <= bg
+        near_u = _midpoint_dist(u64[flip_m, flip_i]) <= bu
+        gf = gb[flip_m, flip_i].astype(np.float64)
+        uf = ub[flip_m, flip_i].astype(np.float64)
+        if act == 0:
+            raw = 0.5 * gf * (1 + np.tanh(np.sqrt(2 / np.pi) * (gf + 0.044715 * gf ** 3))) * uf
+        else:
+            raw = gf / (1 + np.exp(-gf)) * uf
+        near_a = _midpoint_dist(raw) <= 1e-6 * np.abs(raw) + 1e-30
+        tiny = np.abs(A_test[flip_m, flip_i].astype(np.float64) - a64[flip_m, flip_i]) <= 1e-9 * (np.abs(uf) + 1)
+        legit = near_g | near_u | near_a | tiny
+        assert legit.all(), f"unexplained activation flips at (token, row) {list(zip(flip_m[~legit][:8], flip_i[~legit][:8]))}"
+    da = np.abs(A_test.astype(np.float64) - a64)
+    budget = da @ np.abs(D).T
+    err = np.abs(Y_test - y_ref)
+    bad = err > tol * scale[:, None] + budget
+    assert not bad.any(), f"{bad.sum()} outputs outside tolerance + flip budget (token {int(np.argmax(bad.any(1)))})"
+    rel = np.max(err, axis=1) / np.maximum(scale, 1e-30)
+    return {"tokens": M, "max_rel": float(rel.max()), "down_max_rel": float(e_down.max()), "flips": int(len(flip_m)),
+            "tokens_with_flips": int(np.count_nonzero(per_tok)), "tokens_over_tol": int(np.count_nonzero(rel > tol))}
+
+
 def tile_layout_np(W: np.ndarray, N: int, K: int) -> np.ndarray:
     """The kernels' tiled layout, restated from its definition: per 16-row tile
     and 512-column super-step, lane (g, j) owns the 80-byte run of row j over

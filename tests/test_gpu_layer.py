@@ -450,3 +450,55 @@ def test_gemma4_decoder_step_and_graph(orc, dev):
     for L in layers:
         L.close()
     head.close()
+
+
+def test_gemma4_decoder_position_bounds(orc, dev):
+    """Steps past the KV caches: an eager step or a checked replay at
+    position >= max_seq raises IndexError before anything runs (the
+    reference raises IndexError writing the cache past max_seq_len); a raw
+    graph replay there writes token -1 rather than a token from stale
+    attention."""
+    import alveare_amd as aa
+    from alveare_amd import layer
+
+    H, I, S, V = 256, 512, 3, 300
+    rng = np.random.default_rng(500)
+    pos_dev = torch.zeros(1, dtype=torch.int32, device=dev)
+    D, kv = 256, 8
+    n_qkv = 16 * D + 2 * kv * D
+    norms = {k: rng.uniform(0.5, 1.5, D if k in ("q", "k") else H).astype(np.float32)
+             for k in ("attn", "q", "k", "post_attn", "ffn", "post_ffw")}
+    L = layer.Gemma4DecodeLayer(qkv=orc.synth_q4(n_qkv, H, 501), o=orc.synth_q4(H, 16 * D, 502),
+                                gate=orc.synth_q4(I, H, 503), up=orc.synth_q4(I, H, 504),
+                                down=orc.synth_q4(H, I, 505), norms=norms, scale=0.7, sliding=True, H=H, I=I,
+                                max_seq=S, device=dev, pos_dev=pos_dev)
+    table = torch.from_numpy(rng.normal(0, 0.05, (V, H)).astype(np.float16)).to(dev)
+    head = aa.Q4Weight(torch.from_numpy(orc.synth_q4(V, H, 506)).to(dev), V, H)
+    dec = layer.Gemma4Decoder([L], table, rng.uniform(0.5, 1.5, H).astype(np.float32), head, V, softcap=30.0)
+    assert dec.max_pos == S
+    toks = [dec.step(token=5, pos=0)] + [dec.step() for _ in range(S - 1)]
+    assert all(0 <= t < V for t in toks)
+    assert int(pos_dev.item()) == S
+    with pytest.raises(IndexError):
+        dec.step()
+    with pytest.raises(IndexError):
+        dec.step(token=1, pos=S)
+    assert int(pos_dev.item()) == S  # nothing ran
+    dec.set_position(S - 1)
+    g = dec.capture()  # the captured step itself advances nothing until replayed
+    dec.set_position(S - 1)
+    dec.replay(g)  # the last position the caches hold
+    torch.cuda.synchronize()
+    assert 0 <= int(dec.token_dev.item()) < V
+    with pytest.raises(IndexError):
+        dec.replay(g)
+    g.replay()  # unchecked: the device guard marks the token
+    torch.cuda.synchronize()
+    assert int(dec.token_dev.item()) == -1
+    with pytest.raises(ValueError, match="positions"):
+        layer.Gemma4DecodeLayer(qkv=orc.synth_q4(8704, H, 1), o=orc.synth_q4(H, 16 * 512, 2), gate=orc.synth_q4(I, H, 3),
+                                up=orc.synth_q4(I, H, 4), down=orc.synth_q4(H, I, 5), norms=norms, scale=0.7,
+                                sliding=False, H=H, I=I, max_seq=layer.ATTN_MAX_SPAN + 64, device=dev)
+    del g
+    L.close()
+    head.close()

@@ -87,3 +87,58 @@ def test_registry_errors(orc, dev, tmp_path):
     raise std::runtime_error (runtime/cpp/src/npu.cpp:272-276, :295-299)."""
     orc.synth_q4(256, 512, 520).tofile(tmp_path / "W")
     _run(["errors", 256, 512, tmp_path / "W"], tmp_path)
+
+
+MANIFEST = """{
+  "model_type": "gemma4",
+  "kernel_name": "MLIR_AIE",
+  "kernels": [
+    {"kind": "gemv", "N": 8192, "K": 4096, "m": 32, "k_tile": 256, "n_cores": 32,
+     "xclbin": "gemv_8192x4096.xclbin", "insts": "gemv_8192x4096.bin"},
+    {"kind": "gemm", "B": 16, "N": 16384, "K": 4096, "m": 32, "k_tile": 256, "n_cores": 32,
+     "xclbin": "gemm.xclbin", "insts": "gemm.bin", "extra": {"nested": [1, 2, "x\\"y"]}},
+    {"kind": "ffn_fused", "H": 1024, "I": 2048, "activation": "gelu", "m": 32, "k_tile": 128,
+     "n_cores": 32, "xclbin": "ffn.xclbin", "insts": "ffn.bin"}
+  ]
+}
+"""
+
+
+def test_registry_reads_manifest(dev, tmp_path):
+    """kernels() lists the manifest's kernels (the reference's parity driver,
+    runtime/cpp/test/parity_test.cpp:30, walks it), model_type comes from it,
+    and unknown fields are skipped."""
+    (tmp_path / "manifest.json").write_text(MANIFEST)
+    env = dict(os.environ, NPU_MANIFEST=str(tmp_path / "manifest.json"))
+    r = subprocess.run([CHECK, "manifest", str(tmp_path / "k.txt")], capture_output=True, text=True, timeout=120, env=env)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", r.stdout + r.stderr
+    lines = (tmp_path / "k.txt").read_text().splitlines()
+    assert lines[0] == "model_type gemma4"
+    assert lines[1:] == ["gemv 8192 4096 0 0 0  32 256 32 gemv_8192x4096.xclbin",
+                         "gemm 16384 4096 16 0 0  32 256 32 gemm.xclbin",
+                         "ffn_fused 0 0 0 1024 2048 gelu 32 128 32 ffn.xclbin"]
+
+
+def test_registry_ffn_packing_from_manifest(orc, dev, tmp_path):
+    """A blob packed with k_tile = 128 at H = 1024 (the loader's rule would
+    say 256): the manifest's ffn_fused entry for the shape gives the packing,
+    so the blob unpacks to the right weights."""
+    import alveare_amd as aa
+    from alveare_amd import layer
+
+    H, I = 1024, 2048
+    Wg, Wu, Wd = orc.synth_q4(I, H, 530), orc.synth_q4(I, H, 531), orc.synth_q4(H, I, 532)
+    x = qn.bf16_rne(orc.synth_normal(H, 533))
+    qn.pack_ffn_fused_weights_ref(Wg, Wu, Wd, H, I, 32, 128).tofile(tmp_path / "P")
+    _bf16_file(tmp_path / "x", x)
+    (tmp_path / "manifest.json").write_text(MANIFEST)
+    env = dict(os.environ, NPU_MANIFEST=str(tmp_path / "manifest.json"))
+    args = [CHECK, "ffn", H, I, "gelu", tmp_path / "P", tmp_path / "x", tmp_path / "y"]
+    r = subprocess.run([str(a) for a in args], capture_output=True, text=True, timeout=120, env=env)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", r.stdout + r.stderr
+    y = np.fromfile(tmp_path / "y", np.uint16)
+    F = aa.FfnWeights(*(torch.from_numpy(w).to(dev) for w in (Wg, Wu, Wd)), H, I, "gelu")
+    xd = torch.from_numpy(parity.f32_bits_bf16(x).view(np.int16)).view(torch.bfloat16).to(dev)
+    direct = parity.bf16_bits(layer.ffn_fused_bf16(F, xd))
+    F.close()
+    assert np.array_equal(y, direct)

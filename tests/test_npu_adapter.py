@@ -82,3 +82,31 @@ def test_unpack_rejects_lossy_packing_and_bad_sizes(npu):
     blob = q4_numpy.pack_ffn_fused_weights_ref(_rand(rng, I, H), _rand(rng, I, H), _rand(rng, H, I), H, I, 32, 128)
     rc, *_ = _unpack(npu, blob[:-20], H, I, 32, 128)
     assert rc == -1 and b"expected" in npu.alvnpu_last_error()
+
+
+REF = "/root/reference"
+REF_SRC = os.path.join(REF, "runtime", "cpp", "src")
+
+
+@pytest.mark.skipif(not os.path.isdir(REF_SRC), reason="the reference tree is not mounted here")
+@pytest.mark.parametrize("unit", ["weights", "model", "generator", "main"])
+def test_reference_runtime_compiles_against_adapter(tmp_path, unit):
+    """The reference's C++ runtime sources compile unchanged against this
+    build's alveare/npu.h (syntax only: the XRT-free translation units the
+    registry is used from). The adapter's include directory comes first, and
+    the header list shows that its npu.h, not the reference's, was used."""
+    import subprocess
+
+    inc = [os.path.join(ROOT, "alveare_amd", "cpp"), os.path.join(REF, "runtime", "cpp", "include")]
+    tp = os.path.join(REF, "third_party")
+    if os.path.isdir(tp):
+        inc.append(tp)
+    cmd = ["g++", "-std=c++17", "-fsyntax-only", "-H", *[f"-I{d}" for d in inc], os.path.join(REF_SRC, unit + ".cpp")]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-4000:]
+    headers = [l.lstrip(". ").strip() for l in r.stderr.splitlines() if l.startswith(".")]
+    ours = os.path.join(ROOT, "alveare_amd", "cpp", "alveare", "npu.h")
+    theirs = os.path.join(REF, "runtime", "cpp", "include", "alveare", "npu.h")
+    if any(os.path.basename(h) == "npu.h" for h in headers):
+        assert any(os.path.realpath(h) == os.path.realpath(ours) for h in headers), "adapter npu.h not used"
+        assert not any(os.path.realpath(h) == os.path.realpath(theirs) for h in headers), "reference npu.h used"

@@ -483,3 +483,21 @@ def test_gemma4_layer_restatement_closed_form():
     v_n = np.concatenate([q4_numpy.rmsnorm_cpu(qkv_val[6144 + 256 * h:6144 + 256 * (h + 1)], None) for h in range(8)])
     assert np.array_equal(vc[:, 3].reshape(-1), v_n)
     assert np.any(kc[:, 3] != 0) and not np.any(kc[:, 4])
+
+
+def test_ffn_check_batch_pins(orc):
+    """The batched flip-aware FFN check (tests/parity.py::ffn_check_batch)
+    accepts the float32 oracle's own outputs and rejects a planted mistake:
+    the GLU applied to g before its bf16 rounding."""
+    import parity
+
+    H, I, M = 256, 512, 7
+    Wg, Wu, Wd = orc.synth_q4(I, H, 1), orc.synth_q4(I, H, 2), orc.synth_q4(H, I, 3)
+    X = orc.synth_normal(M * H, 4).reshape(M, H)
+    G, U = orc.gemm_q(Wg, X, M, I, H), orc.gemm_q(Wu, X, M, I, H)
+    A = orc.glu(orc.bf16_round(G), orc.bf16_round(U), 0).reshape(M, I)
+    st = parity.ffn_check_batch(orc, Wg, Wu, Wd, X, H, I, 0, orc.gemm_q(Wd, A, M, H, I), A)
+    assert st["tokens"] == M and st["max_rel"] <= parity.TOL
+    A2 = orc.glu(G.reshape(-1), orc.bf16_round(U), 0).reshape(M, I)
+    with pytest.raises(AssertionError):
+        parity.ffn_check_batch(orc, Wg, Wu, Wd, X, H, I, 0, orc.gemm_q(Wd, A2, M, H, I), A2)
