@@ -267,16 +267,15 @@ __device__ void fused_resid_step(const Gemv1Args& a, const WgWork& wk, __bf16* x
         __syncthreads();
         inv = rms_inv<NT>(row, K, a.pr_eps, red, tid);
     }
-    unpack8(rv, rf);
-    uint16_t b[8];
+    if (in) {  // waves wholly past K skip the step
+        unpack8(rv, rf);
+        uint16_t b[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        f[e] = resid_step(f[e], rf[e], wy[e], inv, a.pr_norm_y, a.pr_wy != nullptr, a.pr_mode, a.pr_scale);
-        b[e] = bf16_rne_bits(f[e]);
-    }
-    if (in) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) row[8 * v + e] = f[e];
+        for (int e = 0; e < 8; ++e) {
+            f[e] = resid_step(f[e], rf[e], wy[e], inv, a.pr_norm_y, a.pr_wy != nullptr, a.pr_mode, a.pr_scale);
+            b[e] = bf16_rne_bits(f[e]);
+            row[8 * v + e] = f[e];
+        }
         if (blockIdx.x == 0) reinterpret_cast<uint4*>(a.pr_s)[v] = pack8(b);
     }
     __syncthreads();

@@ -39,10 +39,12 @@ __device__ __forceinline__ float mul_rn(float a, float b) {
     return a * b;
 }
 
+// Round to nearest even: v_cvt_pk_bf16_f32 (the round-to-nearest-even
+// conversion, float32 denormals kept), NaN as 0x7FC0 -- two instructions
+// where the integer form (u + 0x7FFF + lsb) >> 16 takes six.
 __device__ __forceinline__ uint16_t bf16_rne_bits(float v) {
-    if (v != v) return 0x7FC0u;
-    const uint32_t u = __builtin_bit_cast(uint32_t, v);
-    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+    const uint16_t h = __builtin_bit_cast(uint16_t, (__bf16)v);
+    return v != v ? (uint16_t)0x7FC0u : h;
 }
 
 __device__ __forceinline__ float bf16r(float v) { return bf16_bits_to_f32(bf16_rne_bits(v)); }
@@ -147,6 +149,37 @@ __device__ __forceinline__ float leaf8_sq(const float* p, int leaf, int j) {
     return r;
 }
 
+// leaf8_sq for leaf = 8 N8 (every leaf of a halving row wider than 128): the
+// loads at constant offsets from the lane's first value, no per-lane bounds.
+template <int N8>
+__device__ __forceinline__ float leaf8_sq_n(const float* p, int j) {
+    const float* pj = p + j;
+    float sq[N8];
+#pragma unroll
+    for (int q = 0; q < N8; ++q) sq[q] = mul_rn(pj[8 * q], pj[8 * q]);
+    float r = sq[0];
+#pragma unroll
+    for (int q = 1; q < N8; ++q) r = add_rn(r, sq[q]);
+    r = add_rn(r, dpp_f<0xB1>(r));
+    r = add_rn(r, dpp_f<0x4E>(r));
+    return add_rn(r, dpp_f<0x141>(r));
+}
+
+// A leaf's sum by its 8 lanes (leaf uniform across the wave).
+__device__ __forceinline__ float leaf_sq(const float* p, int leaf, int j) {
+    switch (leaf) {
+        case 72: return leaf8_sq_n<9>(p, j);
+        case 80: return leaf8_sq_n<10>(p, j);
+        case 88: return leaf8_sq_n<11>(p, j);
+        case 96: return leaf8_sq_n<12>(p, j);
+        case 104: return leaf8_sq_n<13>(p, j);
+        case 112: return leaf8_sq_n<14>(p, j);
+        case 120: return leaf8_sq_n<15>(p, j);
+        case 128: return leaf8_sq_n<16>(p, j);
+        default: return leaf8_sq(p, leaf, j);
+    }
+}
+
 // The recursion's tree over `count` (a power of two <= 64) values held by
 // the wave's lanes 0, g, 2g, ... (g = 1: one per lane; g = 8: one per 8-lane
 // group, each group's lanes holding the same bits), returned to every lane:
@@ -192,7 +225,7 @@ __device__ __forceinline__ float pw_chunk_sq(const float* a, int n, float* red, 
     for (int base = 0; base < leaves; base += NT / 8) {
         const int lf = base + (tid >> 3);
         if (lf < leaves) {
-            const float r = leaf8_sq(a + (size_t)lf * leaf, leaf, tid & 7);
+            const float r = leaf_sq(a + (size_t)lf * leaf, leaf, tid & 7);
             if ((tid & 7) == 0) red[lf] = r;
         }
     }
@@ -237,7 +270,7 @@ __device__ __forceinline__ float pw_wave_sq(const float* a, int n, int lane) {
     // Lanes past the last leaf sum leaf 0 again; the tree reads only lanes
     // of real leaves.
     const int lf = lane >> 3;
-    const float r = leaf8_sq(a + (size_t)(lf < leaves ? lf : 0) * leaf, leaf, lane & 7);
+    const float r = leaf_sq(a + (size_t)(lf < leaves ? lf : 0) * leaf, leaf, lane & 7);
     return fold_tree(r, leaves, 8);
 }
 

@@ -58,6 +58,46 @@ def test_rmsnorm_bit_exact(dev, rows, K, weighted):
     assert not got[:, K:].any()
 
 
+def test_rmsnorm_rounding_edges(dev):
+    """bf16 rounding at its edges, through RMSNorm's final products x * inv * w:
+    weights that drive them into float32 subnormals (including values that
+    round up into the normal range), past the largest bf16 to inf, to NaN
+    (canonical 0x7FC0), signed zeros, and exact rounding ties (w chosen so
+    that x * inv * w lands halfway between two bf16 values)."""
+    from alveare_amd import layer
+
+    rng = np.random.default_rng(1234)
+    rows, K = 8, 4096
+    x = rnd_bf16(rng, (rows, K), 1.0)
+    w = rng.uniform(0.3, 2.0, K).astype(np.float32)
+    w[0:512] = rng.uniform(1e-45, 1e-37, 512).astype(np.float32)       # subnormal and just-normal products
+    w[512:576] = np.float32(3.0e38)                                     # overflow to +-inf
+    w[576:580] = np.float32("nan")
+    w[580:584] = [0.0, -0.0, np.float32(1e-45), np.float32(-1e-45)]
+    w[584:600] = -w[600:616]                                            # sign flips
+    # ties: pick w so that the float32 product is exactly halfway (odd and even
+    # bf16 neighbours) for row 0.
+    x0 = x[0].astype(np.float32)
+    n0 = x0 * (1.0 / np.sqrt(np.mean(x0 ** 2) + 1e-6))
+    ties = 0
+    for k in range(600, 1100):
+        if n0[k] == 0:
+            continue
+        # (2n + 1) 2^(s - 1), n in [128, 256): halfway between two bf16 values
+        target = np.float32((2 * int(rng.integers(128, 256)) + 1) * 2.0 ** int(rng.integers(-30, 10)))
+        wk = np.float32(target / n0[k])
+        if n0[k] * wk == target:
+            w[k] = wk
+            ties += 1
+    assert ties > 100
+    out = layer.rmsnorm(bf_dev(x, dev), w, K=K, rows=rows, pad=K)
+    got = parity.bf16_bits(out).reshape(rows, K)
+    for r in range(rows):
+        want = parity.f32_bits_bf16(qn.rmsnorm_cpu(x[r], w))
+        assert np.array_equal(got[r], want), f"row {r}: {np.flatnonzero(got[r] != want)[:8]}"
+    assert (got[:, 576:580] == 0x7FC0).all()
+
+
 # ---- q/k/v post-processing (model.py:742-770) ---------------------------------------
 
 @pytest.mark.parametrize("sliding,pos", [(True, 0), (True, 7), (True, 1500), (False, 0), (False, 2047)])
