@@ -247,6 +247,34 @@ __device__ __forceinline__ void stage_acts(const Gemv1Args& a, const WgWork& wk,
 // floats) for the pairwise sums. Workgroup 0 writes s to pr_s. Octet t of x
 // goes to operand slot (t / 64) * 64 + (t % 16) * 4 + (t / 16) % 4 (the
 // inverse of stage_acts' slot order); octets past K are zeros.
+// The residual step of one octet with its flags as constants: resid_step's
+// branches on runtime flags cost a scalar branch per value and flag.
+template <bool NY, bool HW, int MODE>
+__device__ __forceinline__ void resid_octet(float (&f)[8], const float (&rf)[8], const float (&wy)[8], float inv,
+                                            float scale) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = resid_step(f[e], rf[e], wy[e], inv, NY, HW, MODE, scale);
+}
+
+__device__ __forceinline__ void resid_octet_any(const Gemv1Args& a, float (&f)[8], const float (&rf)[8],
+                                                const float (&wy)[8], float inv) {
+    const float sc = a.pr_scale;
+    switch ((a.pr_norm_y ? 1 : 0) | (a.pr_wy ? 2 : 0) | (a.pr_mode << 2)) {
+        case 0: resid_octet<false, false, 0>(f, rf, wy, inv, sc); break;
+        case 1: resid_octet<true, false, 0>(f, rf, wy, inv, sc); break;
+        case 2: resid_octet<false, true, 0>(f, rf, wy, inv, sc); break;
+        case 3: resid_octet<true, true, 0>(f, rf, wy, inv, sc); break;
+        case 4: resid_octet<false, false, 1>(f, rf, wy, inv, sc); break;
+        case 5: resid_octet<true, false, 1>(f, rf, wy, inv, sc); break;
+        case 6: resid_octet<false, true, 1>(f, rf, wy, inv, sc); break;
+        case 7: resid_octet<true, true, 1>(f, rf, wy, inv, sc); break;
+        case 8: resid_octet<false, false, 2>(f, rf, wy, inv, sc); break;
+        case 9: resid_octet<true, false, 2>(f, rf, wy, inv, sc); break;
+        case 10: resid_octet<false, true, 2>(f, rf, wy, inv, sc); break;
+        default: resid_octet<true, true, 2>(f, rf, wy, inv, sc); break;
+    }
+}
+
 template <int NW>
 __device__ void fused_resid_step(const Gemv1Args& a, const WgWork& wk, __bf16* xs, float* red, float* row, int tid) {
     constexpr int NT = 64 * NW;
@@ -258,36 +286,38 @@ __device__ void fused_resid_step(const Gemv1Args& a, const WgWork& wk, __bf16* x
     float wy[8], wx[8], f[8], rf[8];
     load_w8(in && a.pr_norm_y ? a.pr_wy : nullptr, v, wy);
     load_w8(in ? a.pr_wx : nullptr, v, wx);
+    if (!a.pr_wx)  // t * 1 is t, bit for bit (NaN, signed zeros and subnormals included)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wx[e] = 1.0f;
     unpack8(yv, f);
     float inv = 1.0f;
+    // Neither sum waits at its end: red is next written after the barrier
+    // that follows the step, and nothing reads it after the second sum.
     if (a.pr_norm_y) {
         if (in)
 #pragma unroll
             for (int e = 0; e < 8; ++e) row[8 * v + e] = f[e];
         __syncthreads();
-        inv = rms_inv<NT>(row, K, a.pr_eps, red, tid);
+        inv = rms_inv<NT, false>(row, K, a.pr_eps, red, tid);
     }
     if (in) {  // waves wholly past K skip the step
         unpack8(rv, rf);
+        resid_octet_any(a, f, rf, wy, inv);
         uint16_t b[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            f[e] = resid_step(f[e], rf[e], wy[e], inv, a.pr_norm_y, a.pr_wy != nullptr, a.pr_mode, a.pr_scale);
-            b[e] = bf16_rne_bits(f[e]);
+            b[e] = (uint16_t)(__builtin_bit_cast(uint32_t, f[e]) >> 16);  // f[e] holds a bf16 value
             row[8 * v + e] = f[e];
         }
         if (blockIdx.x == 0) reinterpret_cast<uint4*>(a.pr_s)[v] = pack8(b);
     }
     __syncthreads();
-    const float inv2 = rms_inv<NT>(row, K, a.pr_eps, red, tid);
+    const float inv2 = rms_inv<NT, false>(row, K, a.pr_eps, red, tid);
     if (v < wk.nsw * 64) {
         uint16_t xb[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         if (in)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float t = mul_rn(f[e], inv2);
-                xb[e] = bf16_rne_bits(a.pr_wx ? mul_rn(t, wx[e]) : t);
-            }
+            for (int e = 0; e < 8; ++e) xb[e] = bf16_rne_bits(mul_rn(mul_rn(f[e], inv2), wx[e]));
         const int sl = (v >> 6) * 64 + ((v & 15) << 2) + ((v >> 4) & 3);
         *reinterpret_cast<uint4*>(xs + (size_t)sl * 8) = pack8(xb);
     }

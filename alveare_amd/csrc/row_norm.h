@@ -201,8 +201,10 @@ __device__ __forceinline__ float fold_tree(float v, int count, int g) {
 
 // Pairwise sum of the squares of a[0, n), n <= 8192, by the workgroup
 // (NT threads; a and red in LDS, red >= 65 floats, 16-byte aligned: the
-// one-lane recursion keeps its frames in red[0, 64)). Returned to all.
-template <int NT>
+// one-lane recursion keeps its frames in red[0, 64)). Returned to all. SYNC:
+// a closing barrier, so that the caller may write red (and a) at once; without
+// it, red must not be written again before the caller's next barrier.
+template <int NT, bool SYNC = true>
 __device__ __forceinline__ float pw_chunk_sq(const float* a, int n, float* red, int tid) {
     int leaf = n, leaves = 1;
     bool halving = true;
@@ -218,7 +220,7 @@ __device__ __forceinline__ float pw_chunk_sq(const float* a, int n, float* red, 
         if (tid == 0) red[64] = pw_serial_sq(a, n, reinterpret_cast<PwFrame*>(red));
         __syncthreads();
         const float r = red[64];
-        __syncthreads();  // red is reused by the next call
+        if (SYNC) __syncthreads();  // red is reused by the next call
         return r;
     }
     // 8 lanes per leaf, leaf sums to red[lf]; every wave then folds them.
@@ -232,19 +234,20 @@ __device__ __forceinline__ float pw_chunk_sq(const float* a, int n, float* red, 
     __syncthreads();
     const int lane = tid & 63;
     const float r = fold_tree(red[lane < leaves ? lane : 0], leaves, 1);
-    __syncthreads();  // red is reused by the next call
+    if (SYNC) __syncthreads();  // red is reused by the next call
     return r;
 }
 
 // 1 / sqrt(mean(x^2) + eps) of the K values xs (LDS) in numpy's float32
 // arithmetic: np.add.reduce takes the array in buffers of 8192 elements
 // (np.getbufsize()), sums each pairwise and adds the buffer sums in order.
-template <int NT>
+template <int NT, bool SYNC = true>
 __device__ __forceinline__ float rms_inv(const float* xs, int K, float eps, float* red, int tid) {
     constexpr int kBuf = 8192;
-    float s = pw_chunk_sq<NT>(xs, min(K, kBuf), red, tid);
+    if (!SYNC && K > kBuf) return rms_inv<NT, true>(xs, K, eps, red, tid);  // buffers reuse red in turn
+    float s = pw_chunk_sq<NT, SYNC>(xs, min(K, kBuf), red, tid);
     for (int off = kBuf; off < K; off += kBuf)
-        s = add_rn(s, pw_chunk_sq<NT>(xs + off, min(K - off, kBuf), red, tid));
+        s = add_rn(s, pw_chunk_sq<NT, SYNC>(xs + off, min(K - off, kBuf), red, tid));
     const float var = __fdiv_rn(s, (float)K);
     // sqrtf is the correctly rounded square root here (v_sqrt_f32 plus a
     // neighbour test); __fsqrt_rn compiles to the bare 1-ulp v_sqrt_f32.
