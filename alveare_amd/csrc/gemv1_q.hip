@@ -14,8 +14,9 @@
 // (2 to 8 tokens) or term-major (9 to 16; see ARows), staged once per workgroup in LDS in operand
 // order; the tokens of a launch share every dequantized weight. When a
 // workgroup's activations outgrow the LDS, K is split over several workgroups
-// per row-tile group (partial sums in a per-stream scratch; the last
-// workgroup of the group adds them in split order).
+// per row-tile group (partial sums in a per-stream scratch, added in split
+// order by the last workgroup of the group or, from 4 splits, by a second
+// launch, split_fix_kernel).
 //
 // Work split. A unit is one (row tile, super-step[, matrix]) tile of the
 // registered layout: 16 rows x 512 columns, 5 KiB, read by one wave as five
@@ -38,6 +39,7 @@
 // computed which unit.
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 
 #include "q4_device.h"
 #include "q4_host.h"
@@ -66,6 +68,7 @@ struct Gemv1Args {
     int rt_q, rt_r;  // so group t owns rt_q + (t < rt_r) row tiles
     int ks;          // K splits: workgroup b is tile group b / ks, super-step range b % ks
     int act;
+    int fix;         // split K: shares stored plainly, summed by a separate launch (split_fix_kernel)
     int Nz;          // output rows [N, Nz) of every token are written as zeros
     // Fused residual step (bf16 one-token launches; pr_r null: none).
     const uint16_t* pr_r;
@@ -489,13 +492,20 @@ __device__ __forceinline__ void finish_tile(const Gemv1Args& a, const WgWork& wk
                 u32x4 v;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[e] = __builtin_bit_cast(uint32_t, y[(4 * ch + e) / NT][(4 * ch + e) % NT]);
-                __builtin_amdgcn_raw_buffer_store_b128(v, rp, base + 16u * ch, 0, 16);
+                if (a.fix)
+                    __builtin_amdgcn_raw_buffer_store_b128(v, rp, base + 16u * ch, 0, 0);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b128(v, rp, base + 16u * ch, 0, 16);
             }
         } else if (c == 0) {
 #pragma unroll
-            for (int f = 0; f < F; ++f)
-                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y[f / NT][f % NT]), rp, base + 4u * f,
-                                                      0, 16);
+            for (int f = 0; f < F; ++f) {
+                const uint32_t v = __builtin_bit_cast(uint32_t, y[f / NT][f % NT]);
+                if (a.fix)
+                    __builtin_amdgcn_raw_buffer_store_b32(v, rp, base + 4u * f, 0, 0);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b32(v, rp, base + 4u * f, 0, 16);
+            }
         }
         return;
     }
@@ -508,48 +518,33 @@ __device__ __forceinline__ void finish_tile(const Gemv1Args& a, const WgWork& wk
     }
 }
 
-// Every tile of the workgroup (wave w: tiles w, w + NW, ...), then the split-K
-// fixup (section 5). Split-K launches finish here, after all their units.
-template <int NW, int R, bool GLU, int MT, bool TB>
-__device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk, f32x4* part, int part_n, int* flag,
-                                            int tid) {
-    using Ph = PhaseT<R, false, GLU, MT, TB>;
-    constexpr int NT = Ph::NT;
-    const int lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const bool split = a.ks > 1;
-    for (int tl = w; tl < wk.nt; tl += NW) finish_tile<R, GLU, MT, TB>(a, wk, part, tl, lane);
-    if (!split) return;
-
-    // ---- 5. split K: the last workgroup of the tile group adds the shares ---------
-    // The shares land before the workgroup counts itself in; the workgroup
-    // that brings the count to ks reads all of them (sc1, past this XCD's L2)
-    // and sums them in split order, so the result does not depend on which
-    // workgroup came last; it then clears the count for the next launch.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(&a.cnt[wk.tg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *flag = old == (uint32_t)(a.ks - 1) ? 1 : 0;
-        flag[1] = 0;
-    }
-    __syncthreads();
-    if (!*flag) return;
+// ---- 5'. the split-K sum of rows row_of(0 .. nrow - 1) ---------------------------
+// Each row's ks shares in split order (so the result does not depend on
+// which workgroup wrote which share), then the epilogue: GLU or the plain
+// output. SC1: the shares were written through by workgroups of this launch
+// (the last arriver reads them past its XCD's L2); otherwise a launch before
+// this one wrote them. flag[1] counts the GELU values the float32 path cannot
+// settle, queued in `part` (part_n 16-byte entries) for a float64 pass.
+template <int NW, bool GLU, int MT, bool SC1, class RowOf>
+__device__ __forceinline__ void split_sum(const Gemv1Args& a, int nrow, RowOf row_of, f32x4* part, int part_n,
+                                          int* flag, int tid) {
+    constexpr int NT = GLU ? 2 : 1;
     const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.part, a.pbytes);
     constexpr int F = MT * NT;
     if constexpr (F % 4 == 0) {
         // One (row, 16-byte piece) per thread: the piece of every split, in
         // split order, then the piece's tokens (two (gate, up) pairs, or four
         // outputs).
-        for (int i = tid; i < wk.nt * 16 * (F / 4); i += 64 * NW) {
+        for (int i = tid; i < nrow * (F / 4); i += 64 * NW) {
             const int r = i / (F / 4), ch = i - r * (F / 4);
-            const int row = tile_row(wk, r >> 4) * 16 + (r & 15);
+            const int row = row_of(r);
             if (row >= a.N) continue;
             const uint32_t base = (uint32_t)(((size_t)row * a.ks * F + 4 * ch) * sizeof(float));
             float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 4
             for (int kq = 0; kq < a.ks; ++kq) {
-                const u32x4 v = buf_load16_sc1(rp, base + (uint32_t)((size_t)kq * F * sizeof(float)));
+                const u32x4 v = (SC1 ? buf_load16_sc1(rp, base + (uint32_t)((size_t)kq * F * sizeof(float)))
+                                    : buf_load16(rp, base + (uint32_t)((size_t)kq * F * sizeof(float))));
 #pragma unroll
                 for (int e = 0; e < 4; ++e) y[e] += __builtin_bit_cast(float, (uint32_t)v[e]);
             }
@@ -595,9 +590,9 @@ __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk
             }
         }
     } else {
-        for (int i = tid; i < wk.nt * 16 * MT; i += 64 * NW) {  // one (row, token) per thread
+        for (int i = tid; i < nrow * MT; i += 64 * NW) {  // one (row, token) per thread
             const int r = i / MT, m = i - r * MT;
-            const int row = tile_row(wk, r >> 4) * 16 + (r & 15);
+            const int row = row_of(r);
             if (row >= a.N || m >= a.M) continue;
             const uint32_t base = (uint32_t)((((size_t)row * a.ks) * MT + m) * NT * sizeof(float));
             float y[NT];
@@ -607,12 +602,42 @@ __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk
             for (int kq = 0; kq < a.ks; ++kq)
 #pragma unroll
                 for (int n = 0; n < NT; ++n)
-                    y[n] += __builtin_bit_cast(float, buf_load4_sc1(rp, base + (uint32_t)(((size_t)kq * MT * NT + n) * 4)));
+                    y[n] += __builtin_bit_cast(float, SC1 ? buf_load4_sc1(rp, base + (uint32_t)(((size_t)kq * MT * NT + n) * 4))
+                                                          : buf_load4(rp, base + (uint32_t)(((size_t)kq * MT * NT + n) * 4)));
             float out = y[0];
             if constexpr (GLU) out = glu_out<MT>(y[0], y[NT - 1], a.act);
             ystore(a, m, row, out);
         }
     }
+}
+
+// Every tile of the workgroup (wave w: tiles w, w + NW, ...), then the split-K
+// fixup (section 5). Split-K launches finish here, after all their units.
+template <int NW, int R, bool GLU, int MT, bool TB>
+__device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk, f32x4* part, int part_n, int* flag,
+                                            int tid) {
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool split = a.ks > 1;
+    for (int tl = w; tl < wk.nt; tl += NW) finish_tile<R, GLU, MT, TB>(a, wk, part, tl, lane);
+    if (!split || a.fix) return;
+
+    // ---- 5. split K: the last workgroup of the tile group adds the shares ---------
+    // The shares land before the workgroup counts itself in; the workgroup
+    // that brings the count to ks reads all of them (sc1, past this XCD's L2)
+    // and sums them in split order, so the result does not depend on which
+    // workgroup came last; it then clears the count for the next launch.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(&a.cnt[wk.tg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = old == (uint32_t)(a.ks - 1) ? 1 : 0;
+        flag[1] = 0;
+    }
+    __syncthreads();
+    if (!*flag) return;
+    const int nrow = wk.nt * 16;
+    split_sum<NW, GLU, MT, true>(a, nrow, [&](int r) { return tile_row(wk, r >> 4) * 16 + (r & 15); }, part, part_n, flag, tid);
     if (tid == 0) __hip_atomic_store(&a.cnt[wk.tg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -688,6 +713,62 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     }
     lds_barrier();
     finish_rows<NW, R, GLU, MT, TB>(a, wk, part, U * US, next, tid);
+}
+
+// The split-K sums of a launch made with a.fix, after it: workgroup b adds
+// the shares of rows [b rpw, b rpw + rpw), one (row, 16-byte piece) or one
+// (row, token) per thread, in split order -- the arithmetic of the last
+// arriver's sum, so both give the same bits.
+constexpr int kFixThreads = 256;
+
+template <bool GLU, int MT>
+__global__ void __launch_bounds__(kFixThreads) split_fix_kernel(Gemv1Args a, int rpw) {
+    __shared__ f32x4 queue[2 * kFixThreads];  // GELU values for the float64 pass
+    __shared__ int flag[2];
+    const int tid = threadIdx.x;
+    if (tid == 0) flag[1] = 0;
+    __syncthreads();
+    const int r0 = blockIdx.x * rpw;
+    split_sum<kFixThreads / 64, GLU, MT, false>(a, min(rpw, a.N - r0), [&](int r) { return r0 + r; }, queue,
+                                                2 * kFixThreads, flag, tid);
+}
+
+// Rows per fixup workgroup: one 16-byte piece (or one token) per thread.
+constexpr int fix_rows(bool glu, int mt) {
+    return (mt * (glu ? 2 : 1)) % 4 == 0 ? kFixThreads / (mt * (glu ? 2 : 1) / 4) : kFixThreads / mt;
+}
+
+template <bool GLU>
+hipError_t launch_fix_g(const Gemv1Args& a, int mt, hipStream_t s) {
+    const int rpw = fix_rows(GLU, mt);
+    const dim3 grid((a.N + rpw - 1) / rpw);
+    switch (mt) {
+        case 1: hipLaunchKernelGGL((split_fix_kernel<GLU, 1>), grid, dim3(kFixThreads), 0, s, a, rpw); break;
+        case 2: hipLaunchKernelGGL((split_fix_kernel<GLU, 2>), grid, dim3(kFixThreads), 0, s, a, rpw); break;
+        case 4: hipLaunchKernelGGL((split_fix_kernel<GLU, 4>), grid, dim3(kFixThreads), 0, s, a, rpw); break;
+        case 5: hipLaunchKernelGGL((split_fix_kernel<GLU, 5>), grid, dim3(kFixThreads), 0, s, a, rpw); break;
+        case 8: hipLaunchKernelGGL((split_fix_kernel<GLU, 8>), grid, dim3(kFixThreads), 0, s, a, rpw); break;
+        default: hipLaunchKernelGGL((split_fix_kernel<GLU, 16>), grid, dim3(kFixThreads), 0, s, a, rpw); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_fix(const Gemv1Args& a, bool glu, int mt, hipStream_t s) {
+    return glu ? launch_fix_g<true>(a, mt, s) : launch_fix_g<false>(a, mt, s);
+}
+
+// Whether a launch of ks K splits sums its shares in a launch of its own
+// (split_fix_kernel) rather than in its last-arriving workgroups: from 4
+// splits. Measured on the 12B-class FFN (3840 <-> 15360, 16 distinct layers,
+// same box, bit-identical outputs), µs per call: 16 tokens (gate/up and down
+// at 4 splits) 50.7 against 58.9 with the last arrivers; 8 tokens (2 splits)
+// 43.9 against 43.0 -- there the second launch costs more than the shorter
+// tail saves. The environment variable ALV_SPLIT_FIX (0: never, 1: every
+// split launch), read at each call, overrides.
+bool split_fix(int ks) {
+    const char* e = getenv("ALV_SPLIT_FIX");
+    if (e && *e) return ks > 1 && atoi(e) != 0;
+    return ks >= 4;
 }
 
 struct DevInfo {
@@ -926,6 +1007,7 @@ int fill_args(const GemvLaunch& L, const Gemv1Plan& p, int m0, int m, hipStream_
     a.rt_r = p.rt_r;
     a.ks = p.ks;
     a.act = L.act;
+    a.fix = split_fix(p.ks) ? 1 : 0;
     a.Nz = L.Nz;
     if (const ResidStep* st = L.step) {
         a.pr_r = st->resid;
@@ -1002,6 +1084,8 @@ int launch_gemv(const GemvLaunch& L, hipStream_t s) {
         if (int rc = fill_args(L, p, m0, m, s, &a)) return rc;
         const hipError_t e = launch_shape(a, L, p.sh, p.tg * p.ks, p.lds, s);
         if (int rc = hip_check(e, "q4_gemv1_kernel launch")) return rc;
+        if (a.fix)
+            if (int rc = hip_check(launch_fix(a, L.glu, p.sh.mt, s), "split_fix_kernel launch")) return rc;
     }
     return ALV_OK;
 }

@@ -225,8 +225,9 @@ int alv_ffn_fused_bf16(alv_ffn_t w, const uint16_t* X, uint16_t* Y, int M, int l
 
 /*
  * alv_ffn_fused for M <= 16 tokens (decode and small-M verification) that
- * allocates nothing: the split-K partial sums and arrival counters of its two
- * launches live in a fixed 16 MiB + 4 KiB array in device memory, one per GPU
+ * allocates nothing: the split-K partial sums and arrival counters of its
+ * launches (gate/up and down, each followed by a summing launch when it splits
+ * K four ways or more) live in a fixed 16 MiB + 4 KiB array in device memory, one per GPU
  * the library runs on, held until the process ends; X, Y and the handle are
  * the caller's as in alv_ffn_fused. Calls no hipMalloc / hipFree, so it may run
  * under HIP graph capture, inside tight serving loops and in harnesses that
