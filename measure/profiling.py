@@ -26,7 +26,7 @@ from collections import defaultdict
 
 Q4_KERNELS = ("q4_gemv1_kernel", "gemm_q4_kernel", "tile_kernel", "rmsnorm_kernel", "qkv_post_kernel",
               "attn_partial_kernel", "attn_merge_kernel", "add_norm_kernel", "embed_kernel", "head_kernel",
-              "head_fold_kernel", "quant_kernel", "split_x_kernel")
+              "head_fold_kernel", "quant_kernel", "split_x_kernel", "split_fix_kernel")
 CALIBRATION = "MulFunctor"  # the profile pass's copy: torch.mul(src, 1.0, out=dst)
 
 
