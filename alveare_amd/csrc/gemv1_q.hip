@@ -820,8 +820,13 @@ hipError_t launch_k(const Gemv1Args& a, int groups, size_t lds, hipStream_t s) {
 }
 
 // Ring depth: one unit in flight per wave (16 per CU) measures faster than two
-// on every decode shape -- a deeper ring only lengthens the memory queues.
+// on every one-token shape -- a deeper ring only lengthens the memory queues.
+// From 8 tokens a unit's compute (two or three MFMAs per weight octet) holds
+// a wave long enough that a second unit in flight pays: 12B-class FFN at 8
+// tokens 42.8 against 43.5 µs, at 16 tokens 50.2 against 50.8 (same box,
+// bit-identical; no more VGPRs at 16 tokens).
 constexpr int kP = 1;
+constexpr int kPWide = 2;  // 8 and 16 tokens
 
 // Token capacity of a launch, activation terms per token and row layout:
 // fp32 activations take the exact three-term split: token quads for 2, 3-4
@@ -853,8 +858,8 @@ hipError_t launch_shape(const Gemv1Args& a, const GemvLaunch& L, Shape sh, int g
             case 1: return launch_k<kP, 1, true, true, 1>(a, groups, lds, s);
             case 2: return launch_k<kP, 1, true, true, 2>(a, groups, lds, s);
             case 4: return launch_k<kP, 1, true, true, 4>(a, groups, lds, s);
-            case 8: return launch_k<kP, 1, true, true, 8>(a, groups, lds, s);
-            default: return launch_k<kP, 1, true, true, 16>(a, groups, lds, s);
+            case 8: return launch_k<kPWide, 1, true, true, 8>(a, groups, lds, s);
+            default: return launch_k<kPWide, 1, true, true, 16>(a, groups, lds, s);
         }
     }
     if (L.Xb) {
@@ -862,8 +867,8 @@ hipError_t launch_shape(const Gemv1Args& a, const GemvLaunch& L, Shape sh, int g
             case 1: return launch_k<kP, 1, true, false, 1>(a, groups, lds, s);
             case 2: return launch_k<kP, 1, true, false, 2>(a, groups, lds, s);
             case 4: return launch_k<kP, 1, true, false, 4>(a, groups, lds, s);
-            case 8: return launch_k<kP, 1, true, false, 8>(a, groups, lds, s);
-            default: return launch_k<kP, 1, true, false, 16>(a, groups, lds, s);
+            case 8: return launch_k<kPWide, 1, true, false, 8>(a, groups, lds, s);
+            default: return launch_k<kPWide, 1, true, false, 16>(a, groups, lds, s);
         }
     }
     if (L.glu) {
@@ -872,8 +877,8 @@ hipError_t launch_shape(const Gemv1Args& a, const GemvLaunch& L, Shape sh, int g
             case 2: return launch_k<kP, 3, false, true, 2>(a, groups, lds, s);
             case 4: return launch_k<kP, 3, false, true, 4>(a, groups, lds, s);
             case 5: return launch_k<kP, 3, false, true, 5>(a, groups, lds, s);
-            case 8: return launch_k<kP, 3, false, true, 8>(a, groups, lds, s);
-            default: return launch_k<kP, 3, false, true, 16, true>(a, groups, lds, s);
+            case 8: return launch_k<kPWide, 3, false, true, 8>(a, groups, lds, s);
+            default: return launch_k<kPWide, 3, false, true, 16, true>(a, groups, lds, s);
         }
     }
     if (!L.tiled) {
