@@ -15,7 +15,10 @@
 // head_kernel, which rewrites each logit in place and folds each workgroup's
 // slice to one (value, index) pair in the stream's scratch; head_fold_kernel,
 // one workgroup folding the pairs into the token. The order is total, so the
-// token does not depend on the fold's shape.
+// token does not depend on the fold's shape. alv_lm_head_bf16 takes the
+// activation as bf16 (one MFMA term; the fp32 entry splits its activation
+// into three, and a bf16-valued fp32 activation gives the same bits) and can
+// advance a device-resident decode position in its last launch.
 #include <algorithm>
 
 #include "q4_device.h"
@@ -93,14 +96,23 @@ __global__ void __launch_bounds__(kHeadThreads) head_kernel(float* logits, int v
     }
 }
 
-// The pairs of head_kernel's `groups` workgroups folded into the token.
+// The pairs of head_kernel's `groups` workgroups folded into the token. With
+// a position (pos non-null) the token is -1 when *pos >= max_pos, and *pos
+// then advances by one.
 __global__ void __launch_bounds__(kHeadThreads) head_fold_kernel(const float* pv, const int* pi, int groups,
-                                                                int32_t* argmax) {
+                                                                int32_t* argmax, int32_t* pos, int max_pos) {
     float v = -__builtin_inff();
     int i = 0x7FFFFFFF;
     for (int b = threadIdx.x; b < groups; b += kHeadThreads) head_fold(v, i, pv[b], pi[b]);
     head_fold_block(v, i);
-    if (threadIdx.x == 0) *argmax = i;
+    if (threadIdx.x == 0) {
+        if (pos) {
+            const int p = *pos;
+            if (p >= max_pos) i = -1;
+            *pos = p + 1;
+        }
+        *argmax = i;
+    }
 }
 
 }  // namespace
@@ -109,16 +121,20 @@ __global__ void __launch_bounds__(kHeadThreads) head_fold_kernel(const float* pv
 
 using namespace alv;
 
-extern "C" int alv_lm_head(alv_weight_t w, const float* x, float* logits, int vocab, float softcap,
-                           int32_t* argmax, void* stream) {
+namespace {
+
+int lm_head(alv_weight_t w, const float* x, const uint16_t* xb, float* logits, int vocab, float softcap,
+            int32_t* argmax, int32_t* pos, int max_pos, void* stream) {
     if (!w || w->magic != kWeightMagic) return fail(ALV_ERR_HANDLE, "invalid weight handle");
-    if (!x || !logits || !argmax) return fail(ALV_ERR_ARG, "null pointer");
+    if ((!x && !xb) || !logits || !argmax) return fail(ALV_ERR_ARG, "null pointer");
     if (vocab < 1 || vocab > w->N) return fail(ALV_ERR_ARG, "vocab=%d outside the head's %d rows", vocab, w->N);
     if (!(softcap >= 0.0f) || softcap == __builtin_inff())
         return fail(ALV_ERR_ARG, "softcap must be 0 (none) or a positive finite cap");
-    if (reinterpret_cast<uintptr_t>(x) % 4 || reinterpret_cast<uintptr_t>(logits) % 4 ||
-        reinterpret_cast<uintptr_t>(argmax) % 4)
-        return fail(ALV_ERR_ALIGN, "x, logits and argmax need 4-byte alignment");
+    if (reinterpret_cast<uintptr_t>(logits) % 4 || reinterpret_cast<uintptr_t>(argmax) % 4 ||
+        reinterpret_cast<uintptr_t>(pos) % 4)
+        return fail(ALV_ERR_ALIGN, "logits, argmax and pos need 4-byte alignment");
+    if (x ? reinterpret_cast<uintptr_t>(x) % 4 : reinterpret_cast<uintptr_t>(xb) % 16)
+        return fail(ALV_ERR_ALIGN, "x needs 4-byte (fp32) or 16-byte (bf16) alignment");
     int dev = -1;
     if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
     if (dev != w->device) return fail(ALV_ERR_HANDLE, "weight handle belongs to device %d, current device is %d", w->device, dev);
@@ -131,17 +147,32 @@ extern "C" int alv_lm_head(alv_weight_t w, const float* x, float* logits, int vo
     GemvLaunch L;
     weight_launch(w, L);
     L.X = x;
+    L.Xb = xb;
     L.ldx = w->K;
     L.Y = logits;
     L.ldy = vocab;
     L.M = 1;
     L.N = std::min(vocab, w->Ne);  // rows past the registered extent are zero logits
     L.Nz = vocab;
-    L.parts = 3;
+    L.parts = xb ? 1 : 3;
     if (int rc = launch_gemv(L, s)) return rc;
     const int groups = std::min(kHeadGroups, (vocab + 63) / 64);
     hipLaunchKernelGGL(head_kernel, dim3(groups), dim3(kHeadThreads), 0, s, logits, vocab, softcap, pv, pi);
     if (int rc = hip_check(hipGetLastError(), "head_kernel launch")) return rc;
-    hipLaunchKernelGGL(head_fold_kernel, dim3(1), dim3(kHeadThreads), 0, s, pv, pi, groups, argmax);
+    hipLaunchKernelGGL(head_fold_kernel, dim3(1), dim3(kHeadThreads), 0, s, pv, pi, groups, argmax, pos, max_pos);
     return hip_check(hipGetLastError(), "head_fold_kernel launch");
+}
+
+}  // namespace
+
+extern "C" int alv_lm_head(alv_weight_t w, const float* x, float* logits, int vocab, float softcap,
+                           int32_t* argmax, void* stream) {
+    if (!x) return fail(ALV_ERR_ARG, "null pointer");
+    return lm_head(w, x, nullptr, logits, vocab, softcap, argmax, nullptr, 0, stream);
+}
+
+extern "C" int alv_lm_head_bf16(alv_weight_t w, const uint16_t* x, float* logits, int vocab, float softcap,
+                                int32_t* argmax, int32_t* pos_dev, int max_pos, void* stream) {
+    if (!x) return fail(ALV_ERR_ARG, "null pointer");
+    return lm_head(w, nullptr, x, logits, vocab, softcap, argmax, pos_dev, max_pos, stream);
 }

@@ -459,7 +459,6 @@ class Gemma4Decoder:
         self.token_dev = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.x = torch.empty(self.H, dtype=torch.bfloat16, device=self.device)
         self.x_norm = torch.empty(head.K, dtype=torch.bfloat16, device=self.device)
-        self.x_f32 = torch.empty(head.K, dtype=torch.float32, device=self.device)
         self.logits = torch.empty(vocab, dtype=torch.float32, device=self.device)
         # Steps run on the decoder's own stream: the per-stream scratch that
         # eager steps size is then the scratch a captured step uses.
@@ -485,10 +484,10 @@ class Gemma4Decoder:
             step = None
         if n == 0:
             rmsnorm(h, self.final_norm, K=self.H, pad=self.head.K, out=self.x_norm)
-        self.x_f32.copy_(self.x_norm)
-        lm_head(self.head, self.x_f32, self.vocab, self.softcap, self.logits, token=self.token_dev)
-        self.token_dev.masked_fill_(self.pos_dev >= self.max_pos, -1)
-        self.pos_dev.add_(1)
+        # The head on the bf16 final norm; its last launch also writes token -1
+        # past the caches and advances pos_dev.
+        lm_head(self.head, self.x_norm, self.vocab, self.softcap, self.logits, token=self.token_dev,
+                pos=self.pos_dev, max_pos=self.max_pos)
 
     def _check_pos(self, pos: int) -> None:
         if not 0 <= pos < self.max_pos:

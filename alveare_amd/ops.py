@@ -414,16 +414,30 @@ def chain_run(ops, M: int = 1) -> None:
 
 
 def lm_head(W: "Q4Weight", x: torch.Tensor, vocab: int | None = None, softcap: float = 30.0,
-            logits: torch.Tensor | None = None, token: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+            logits: torch.Tensor | None = None, token: torch.Tensor | None = None,
+            pos: torch.Tensor | None = None, max_pos: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
     """LM head of a decode step (alv_lm_head): logits[:vocab] =
     softcap * tanh(bf16(W x) / softcap) in float32 (softcap 0: the bf16
     logits) and the greedy token, np.argmax of the logits, as a 1-element
     int32 tensor on the device (runtime/py/model.py:904-916,
-    runtime/py/sampler.py:9; runtime/cpp/src/generator.cpp:15-52)."""
+    runtime/py/sampler.py:9; runtime/cpp/src/generator.cpp:15-52).
+    A bfloat16 x runs alv_lm_head_bf16 (one activation term, the same bits
+    as its float32 widening). ``pos`` (bfloat16 x only): a 1-element int32
+    device tensor holding the decode position, advanced by one in the head's
+    last launch; the token is then -1 when pos >= max_pos."""
     if not isinstance(W, Q4Weight):
         raise TypeError("W must be a registered Q4Weight")
     vocab = W.N if vocab is None else int(vocab)
-    xv = _act_in(x, W.K, "x")
+    bf = x.dtype == torch.bfloat16
+    if pos is not None and not bf:
+        raise ValueError("pos takes a bfloat16 x (alv_lm_head_bf16)")
+    if bf:
+        _too_small("x", x.numel(), W.K)
+        xv = x.reshape(-1)[:W.K].contiguous()
+        if xv.data_ptr() % 16:
+            xv = xv.clone()
+    else:
+        xv = _act_in(x, W.K, "x")
     if xv.device != W.device:
         raise ValueError(f"x on {xv.device}, weights on {W.device}")
     if logits is None:
@@ -436,9 +450,16 @@ def lm_head(W: "Q4Weight", x: torch.Tensor, vocab: int | None = None, softcap: f
         token = torch.empty(1, dtype=torch.int32, device=W.device)
     if token.dtype != torch.int32 or token.device != W.device:
         raise TypeError("token must be an int32 tensor on the weights' device")
+    if pos is not None and (pos.dtype != torch.int32 or pos.device != W.device or pos.numel() < 1):
+        raise TypeError("pos must be an int32 tensor on the weights' device")
     with torch.cuda.device(W.device):
-        check(lib().alv_lm_head(W.handle, xv.data_ptr(), logits.data_ptr(), vocab, float(softcap),
-                                token.data_ptr(), _stream(xv)), "alv_lm_head")
+        if bf:
+            check(lib().alv_lm_head_bf16(W.handle, xv.data_ptr(), logits.data_ptr(), vocab, float(softcap),
+                                         token.data_ptr(), pos.data_ptr() if pos is not None else None,
+                                         int(max_pos), _stream(xv)), "alv_lm_head_bf16")
+        else:
+            check(lib().alv_lm_head(W.handle, xv.data_ptr(), logits.data_ptr(), vocab, float(softcap),
+                                    token.data_ptr(), _stream(xv)), "alv_lm_head")
     return logits, token
 
 

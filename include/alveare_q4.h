@@ -149,6 +149,20 @@ int alv_lm_head(alv_weight_t w, const float* x, float* logits, int vocab, float 
                 void* stream);
 
 /*
+ * alv_lm_head with x as K bf16 values (bit patterns, 16-byte aligned), the
+ * head's input as the reference produces it (the final norm's bf16 output,
+ * runtime/py/model.py:907-912): one MFMA term per value where alv_lm_head
+ * splits its fp32 x into three; the same logits and token as alv_lm_head on
+ * the bf16 values widened to fp32, bit for bit. pos_dev (optional, device
+ * int32; NULL: none) is a decode position the call also advances: the token
+ * is written as -1 when *pos_dev >= max_pos, then *pos_dev += 1 -- the
+ * bookkeeping of a device-resident decode step (alveare_amd.layer.Gemma4Decoder)
+ * inside the head's last launch. No counterpart in the reference for pos_dev.
+ */
+int alv_lm_head_bf16(alv_weight_t w, const uint16_t* x, float* logits, int vocab, float softcap, int32_t* argmax,
+                     int32_t* pos_dev, int max_pos, void* stream);
+
+/*
  * Quantize float32 weights to the Q4 combined layout on the GPU:
  * quantize_to_q4_0 + pack_to_combined (tools/convert/gemv_q_convert.py:5-85)
  * with the zero padding of quantize_and_pack_tensor

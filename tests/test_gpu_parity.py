@@ -751,6 +751,44 @@ def test_lm_head_reduced_vocab(orc, dev, softcap):
     w3.close()
 
 
+def test_lm_head_bf16_and_position(orc, dev):
+    """alv_lm_head_bf16: the head on bf16 activations (one MFMA term) gives
+    the logits and token of alv_lm_head on the same values widened to fp32,
+    bit for bit, also with a NaN row; with a decode position it advances the
+    position by one per call and writes token -1 once the position reaches
+    max_pos (the decoder's bookkeeping, folded into the head's last launch)."""
+    import torch
+
+    import alveare_amd as aa
+
+    N, K, vocab = 20000, 4096, 19990
+    seed = orc.seed_for(6, 2)
+    W = orc.synth_q4(N, K, seed)
+    W = W.reshape(N, K // 32 * 20)
+    W[vocab - 11, 16:18] = [0xC0, 0x7F]  # a NaN logit
+    x = np.zeros(K, np.float32)
+    x[:3840] = orc.bf16_round(orc.synth_normal(3840, seed + 1))
+    w = aa.Q4Weight(to_dev(W, dev), N, K)
+    xd = to_dev(x, dev)
+    for softcap in (30.0, 0.0):
+        l32, t32 = aa.lm_head(w, xd, vocab, softcap)
+        l16, t16 = aa.lm_head(w, xd.bfloat16(), vocab, softcap)
+        assert int(t16.item()) == int(t32.item()) == vocab - 11
+        assert np.array_equal(l16.cpu().numpy().view(np.uint32), l32.cpu().numpy().view(np.uint32))
+    W[vocab - 11, 16:18] = 0x00
+    w.close()
+    w = aa.Q4Weight(to_dev(W, dev), N, K)
+    lref, tref = aa.lm_head(w, xd, vocab, 30.0)
+    exact, tok_ref = _head_check(orc, W.reshape(-1), x, N, K, vocab, 30.0, lref.cpu().numpy(), int(tref.item()))
+    pos = torch.tensor([5], dtype=torch.int32, device=dev)
+    for p_before, want in ((5, int(tref.item())), (6, int(tref.item())), (7, -1), (8, -1)):
+        _, tok = aa.lm_head(w, xd.bfloat16(), vocab, 30.0, pos=pos, max_pos=7)
+        assert int(tok.item()) == want, (p_before, int(tok.item()), want)
+        assert int(pos.item()) == p_before + 1
+    _say(f"  bf16 head: token {int(tref.item())} (reference {tok_ref}), {exact:.4%} logits bit-equal; position advanced")
+    w.close()
+
+
 def test_lm_head_full_vocab(orc, dev):
     """The reference's head shape: 262144 x 4096 (671 MB of Q4 weights, the
     largest GEMV of a decode step), softcap 30, whole vocabulary; then through
