@@ -427,6 +427,167 @@ class Gemma4DecodeLayer:
         self.ffn.close()
 
 
+def cos_sin_table_llama(max_seq_len: int) -> np.ndarray:
+    """The Llama-3.2 RoPE table (precompute_cos_sin_table,
+    runtime/py/model.py:230-261): head dim 64, base 500000, the Llama-3
+    frequency scaling (factor 32, low/high frequency factors 1 and 4, original
+    context 8192), float32 rows [cos | cos | sin | sin] of the 32 angles (128
+    values), then bf16 (returned as uint16 bit patterns)."""
+    dim, base, factor, lo, hi, old_ctx = 64, 500000.0, 32.0, 1.0, 4.0, 8192
+    inv_freq = 1.0 / (base ** (np.arange(0, dim, 2, dtype=np.float32) / dim))
+    wavelen = 2 * np.pi / inv_freq
+    scaled = np.where(wavelen > old_ctx / lo, inv_freq / factor, inv_freq)
+    smooth = np.clip((old_ctx / wavelen - lo) / (hi - lo), 0.0, 1.0)
+    smoothed = (1 - smooth) * (inv_freq / factor) + smooth * inv_freq
+    inv = np.where((wavelen >= old_ctx / hi) & (wavelen <= old_ctx / lo), smoothed, scaled)
+    table = np.zeros((max_seq_len, 128), dtype=np.float32)
+    for pos in range(max_seq_len):
+        freqs = pos * inv
+        c, sn = np.cos(freqs), np.sin(freqs)
+        table[pos] = np.concatenate([c, c, sn, sn])
+    u = table.view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+class _DecodeLayer:
+    """A Gemma-3 or Llama-3.2 decoder layer with every step on the device,
+    composed of the same launches as Gemma4DecodeLayer: the input norm, one
+    QKV GEMV over the rows [q | k | v], the q/k norms (Gemma-3), RoPE and the
+    cache insert inside the attention launch (``fuse``) or before it, the O
+    GEMV, the post-attention residual step (inside the FFN's gate/up launch
+    with ``fuse``) and the last residual step. ``forward(x, pos)`` takes and
+    returns bf16 [H] device tensors and updates the KV caches. Subclasses set
+    the model's constants (norm eps, which norms exist, activation, RoPE
+    table, attention window)."""
+
+    eps: float
+    post_norms: bool          # residual steps normalise the branch output (Gemma) or add it as is (Llama)
+    qk_norms: bool
+    act: str
+
+    def __init__(self, *, qkv, o, gate, up, down, norms: dict, H: int, I: int, heads: int, kv_heads: int, D: int,
+                 max_seq: int, window: int, rope_table: np.ndarray, rope_stride: int, sin_off: int, half: int,
+                 device, pos_dev: torch.Tensor | None = None, fuse: bool = True):
+        dev = torch.device(device)
+        self.H, self.I, self.heads, self.kv_heads, self.D = H, I, heads, kv_heads, D
+        self.max_seq, self.window, self.device, self.fuse = max_seq, window, dev, fuse
+        self.q_size, self.k_size = heads * D, kv_heads * D
+        self.n_qkv = self.q_size + 2 * self.k_size
+        span = min(window, max_seq) if window > 0 else max_seq
+        if max_seq < 1 or span > ATTN_MAX_SPAN:
+            raise ValueError(f"max_seq={max_seq}: attention takes up to {ATTN_MAX_SPAN} positions per span")
+        if heads % kv_heads:
+            raise ValueError(f"heads={heads} is not a multiple of kv_heads={kv_heads}")
+
+        def dev_u8(a):
+            return torch.as_tensor(np.ascontiguousarray(a)).to(dev) if isinstance(a, np.ndarray) else a
+
+        self.w_qkv = Q4Weight(dev_u8(qkv), self.n_qkv, H)
+        self.w_o = Q4Weight(dev_u8(o), H, self.q_size)
+        self.ffn = FfnWeights(dev_u8(gate), dev_u8(up), dev_u8(down), H, I, self.act)
+        self.norms = {k: _f32(v, k, D if k in ("q", "k") else H, dev) for k, v in norms.items()}
+        self.rope = torch.as_tensor(np.ascontiguousarray(rope_table)).view(torch.bfloat16).to(dev)
+        self.rope_args = dict(rope=self.rope, rope_stride=rope_stride, cos_off=0, sin_off=sin_off, half=half)
+        if self.rope.numel() < max_seq * rope_stride:
+            raise ValueError(f"the RoPE table holds fewer than {max_seq} rows of {rope_stride}")
+        self.attn_scale = float(np.float32(1.0 / np.sqrt(D)))
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        self.kcache = torch.zeros((kv_heads, max_seq, D), **bf)
+        self.vcache = torch.zeros((kv_heads, max_seq, D), **bf)
+        self.pos_dev = torch.zeros(1, dtype=torch.int32, device=dev) if pos_dev is None else pos_dev
+        self.x_norm = torch.empty(H, **bf)
+        self.qkv_out = torch.empty(self.n_qkv, **bf)
+        self.q_rope = torch.empty(self.q_size, **bf)
+        self.attn_out = torch.empty(self.q_size, **bf)
+        self.attn_proj = torch.empty(H, **bf)
+        self.x_post = torch.empty(H, **bf)
+        self.x_norm2 = torch.empty(H, **bf)
+        self.down = torch.empty(H, **bf)
+        self.y = torch.empty(H, **bf)
+
+    def enqueue(self, x: torch.Tensor) -> torch.Tensor:
+        H, n, eps = self.H, self.norms, self.eps
+        rmsnorm(x, n["attn"], K=H, eps=eps, out=self.x_norm)
+        gemv_bf16(self.w_qkv, self.x_norm, self.qkv_out)
+        post = dict(heads=self.heads, kv_heads=self.kv_heads, D=self.D, k_off=self.q_size,
+                    v_off=self.q_size + self.k_size, q_w=n.get("q"), k_w=n.get("k"), norm_q=self.qk_norms,
+                    norm_k=self.qk_norms, norm_v=False, eps=eps, q_out=self.q_rope, **self.rope_args)
+        if self.fuse:
+            qkv_attention(self.qkv_out, self.pos_dev, self.kcache, self.vcache, window=self.window,
+                          scale=self.attn_scale, out=self.attn_out, **post)
+        else:
+            qkv_post(self.qkv_out, self.pos_dev, self.kcache, self.vcache, **post)
+            attention(self.q_rope, self.kcache, self.vcache, self.pos_dev, heads=self.heads, window=self.window,
+                      scale=self.attn_scale, out=self.attn_out)
+        gemv_bf16(self.w_o, self.attn_out, self.attn_proj)
+        w_post = n.get("post_attn") if self.post_norms else None
+        if self.fuse:
+            ffn_fused_bf16_addnorm(self.ffn, x, self.attn_proj, sum_out=self.x_post, w_y=w_post,
+                                   norm_y=self.post_norms, w_x=n["ffn"], eps=eps, Y=self.down)
+        else:
+            add_norm(x, self.attn_proj, K=H, w_y=w_post, norm_y=self.post_norms, w_out=n["ffn"], norm_out=True,
+                     eps=eps, sum_out=self.x_post, norm_buf=self.x_norm2)
+            ffn_fused_bf16(self.ffn, self.x_norm2, self.down)
+        add_norm(self.x_post, self.down, K=H, w_y=n.get("post_ffw") if self.post_norms else None,
+                 norm_y=self.post_norms, eps=eps, sum_out=self.y)
+        return self.y
+
+    def forward(self, x: torch.Tensor, pos: int) -> torch.Tensor:
+        if not 0 <= pos < self.max_seq:
+            raise IndexError(f"position {pos} outside the cache of {self.max_seq}")
+        self.pos_dev.fill_(pos)
+        return self.enqueue(x)
+
+    def close(self) -> None:
+        self.w_qkv.close()
+        self.w_o.close()
+        self.ffn.close()
+
+
+class Gemma3DecodeLayer(_DecodeLayer):
+    """One Gemma-3 decoder layer (runtime/py/model.py:632-700; Gemma-3 1B:
+    H 1152, 4 q heads and 1 kv head of 256, FFN 6912 GeGLU): RMSNorm eps 1e-6,
+    per-head q/k norms with weights, no v norm, RoPE over the whole 256-wide
+    head (base 10000 on sliding layers, 1e6 on global ones), attention scaled
+    by 1/sqrt(256) over a 512-position window on sliding layers, the
+    post-attention and post-FFN norms on the residual adds, no output scale.
+    ``qkv`` holds the rows [q | k | v]; norms: attn, q, k, post_attn, ffn,
+    post_ffw."""
+
+    eps, post_norms, qk_norms, act = _GEMMA_EPS, True, True, "gelu"
+
+    def __init__(self, *, qkv, o, gate, up, down, norms: dict, sliding: bool, H: int = 1152, I: int = 6912,
+                 heads: int = 4, kv_heads: int = 1, D: int = 256, max_seq: int, device, rope_table=None,
+                 pos_dev: torch.Tensor | None = None, fuse: bool = True):
+        self.sliding = sliding
+        if rope_table is None:
+            rope_table = cos_sin_table_gemma(10000.0 if sliding else 1000000.0, D, max_seq, gemma4=False)
+        super().__init__(qkv=qkv, o=o, gate=gate, up=up, down=down, norms=norms, H=H, I=I, heads=heads,
+                         kv_heads=kv_heads, D=D, max_seq=max_seq, window=512 if sliding else 0,
+                         rope_table=rope_table, rope_stride=D, sin_off=D // 2, half=D // 2, device=device,
+                         pos_dev=pos_dev, fuse=fuse)
+
+
+class LlamaDecodeLayer(_DecodeLayer):
+    """One Llama-3.2 decoder layer (runtime/py/model.py:820-860; Llama-3.2 1B:
+    H 2048, 32 q heads and 8 kv heads of 64, FFN 8192 SwiGLU): RMSNorm eps
+    1e-5, no q/k norms, RoPE on 64-wide heads from the scaled Llama-3 table
+    (cos_sin_table_llama; run_rope_cpu, model.py:533-547), full attention
+    scaled by 1/8, the branch outputs added to the residual as they are.
+    ``qkv`` holds the rows [q | k | v]; norms: attn, ffn."""
+
+    eps, post_norms, qk_norms, act = 1e-5, False, False, "silu"
+
+    def __init__(self, *, qkv, o, gate, up, down, norms: dict, H: int = 2048, I: int = 8192, heads: int = 32,
+                 kv_heads: int = 8, max_seq: int, device, rope_table=None, pos_dev: torch.Tensor | None = None,
+                 fuse: bool = True):
+        if rope_table is None:
+            rope_table = cos_sin_table_llama(max_seq)
+        super().__init__(qkv=qkv, o=o, gate=gate, up=up, down=down, norms=norms, H=H, I=I, heads=heads,
+                         kv_heads=kv_heads, D=64, max_seq=max_seq, window=0, rope_table=rope_table,
+                         rope_stride=128, sin_off=64, half=32, device=device, pos_dev=pos_dev, fuse=fuse)
+
+
 class Gemma4Decoder:
     """A whole Gemma-4 decode step on the device (runtime/py/model.py:889-915):
     embedding of the token in ``token_dev``, every layer, the final RMSNorm

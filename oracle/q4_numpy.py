@@ -21,6 +21,10 @@ numpy expressions, so numpy decides dtype promotion and the matmul order:
 * ``attention_host``        -- ``runtime/py/model.py:577-628``
 * ``gemma4_decode_layer``   -- ``runtime/py/model.py:705-790`` (the NPU path:
                               the projections and the FFN are callables)
+* ``gemma3_decode_layer``   -- ``runtime/py/model.py:632-700``
+* ``llama_decode_layer``    -- ``runtime/py/model.py:820-860``
+* ``cos_sin_table_llama``   -- ``runtime/py/model.py:230-261``
+* ``rope_cpu_llama``        -- ``runtime/py/model.py:533-547``
 
 bf16 arrays of the reference are float32 arrays of bf16-exact values here, so
 ``x.astype(np.float32)`` of a bf16 array is the identity and
@@ -235,6 +239,111 @@ def gemma4_decode_layer(x: np.ndarray, pos: int, sliding: bool, w: dict, qkv_pro
     down_normed = rmsnorm_cpu(down, w["post_ffw"])
     y = bf16_rne(x_post + down_normed)
     st["y"] = y = bf16_rne(y * np.float32(w["scale"]))
+    return y
+
+
+def cos_sin_table_llama(max_seq_len: int) -> np.ndarray:
+    """precompute_cos_sin_table (model.py:230-261): Llama-3.2's RoPE for
+    64-wide heads, base 500000, the Llama-3 frequency scaling (factor 32,
+    low / high frequency factors 1 / 4, original context 8192); rows
+    [cos | cos | sin | sin] of the 32 angles, float32, then bf16."""
+    dim = 64
+    base = 500000.0
+    factor = 32.0
+    low_freq_factor = 1.0
+    high_freq_factor = 4.0
+    old_context_len = 8192
+    inv_freq = 1.0 / (base ** (np.arange(0, dim, 2, dtype=np.float32) / dim))
+    low_freq_wavelen = old_context_len / low_freq_factor
+    high_freq_wavelen = old_context_len / high_freq_factor
+    wavelen = 2 * np.pi / inv_freq
+    inv_freq_llama = np.where(wavelen > low_freq_wavelen, inv_freq / factor, inv_freq)
+    smooth_factor = np.clip((old_context_len / wavelen - low_freq_factor) / (high_freq_factor - low_freq_factor),
+                            0.0, 1.0)
+    smoothed_inv_freq = (1 - smooth_factor) * (inv_freq / factor) + smooth_factor * inv_freq
+    is_medium_freq = (wavelen >= high_freq_wavelen) & (wavelen <= low_freq_wavelen)
+    inv_freq_llama = np.where(is_medium_freq, smoothed_inv_freq, inv_freq_llama)
+    table = np.zeros((max_seq_len, 128), dtype=np.float32)
+    for pos in range(max_seq_len):
+        freqs = pos * inv_freq_llama
+        cos_val, sin_val = np.cos(freqs), np.sin(freqs)
+        table[pos] = np.concatenate([cos_val, cos_val, sin_val, sin_val])
+    return bf16_rne(table)
+
+
+def rope_cpu_llama(x: np.ndarray, cos_sin_row: np.ndarray) -> np.ndarray:
+    """run_rope_cpu (model.py:533-547) on one table row: 64-wide heads, cos
+    from the row's first 32 values and sin from values 64..95, rotate-half
+    pairs (i, i + 32), float32, then bf16."""
+    x_flat = np.asarray(x, np.float32).reshape(-1)
+    cos = np.asarray(cos_sin_row[:32], np.float32)
+    sin = np.asarray(cos_sin_row[64:96], np.float32)
+    num_heads = x_flat.shape[0] // 64
+    x_fp32 = x_flat.reshape(num_heads, 64)
+    y_fp32 = np.zeros_like(x_fp32)
+    for h in range(num_heads):
+        x1 = x_fp32[h, :32]
+        x2 = x_fp32[h, 32:]
+        y_fp32[h, :32] = x1 * cos - x2 * sin
+        y_fp32[h, 32:] = x2 * cos + x1 * sin
+    return bf16_rne(y_fp32.reshape(-1))
+
+
+def gemma3_decode_layer(x: np.ndarray, pos: int, sliding: bool, w: dict, qkv_proj, o_proj, ffn,
+                        k_cache: np.ndarray, v_cache: np.ndarray, cos_sin_row: np.ndarray, n_heads: int = 4,
+                        n_kv: int = 1, h_dim: int = 256, stages: dict | None = None):
+    """run_layer for gemma3 (model.py:632-700), NPU path. qkv_proj(x_norm)
+    returns the bf16 rows [q | k | v] (the reference's three GEMVs over the
+    same input), o_proj and ffn the bf16 outputs (first H used); w holds the
+    float32 norm weights (attn, q, k, post_attn, ffn, post_ffw). q and k are
+    normalised per head, v is not; attention is scaled by 1/sqrt(h_dim) over
+    a 512-position window on sliding layers; no output scale."""
+    H = x.shape[0]
+    q_size, k_size = n_heads * h_dim, n_kv * h_dim
+    st = {} if stages is None else stages
+    st["x_norm"] = x_norm = rmsnorm_cpu(x, w["attn"])
+    qkv = qkv_proj(x_norm)
+    q, k, v = qkv[:q_size], qkv[q_size:q_size + k_size], qkv[q_size + k_size:q_size + 2 * k_size]
+    q_n = np.concatenate([rmsnorm_cpu(q[h * h_dim:(h + 1) * h_dim], w["q"]) for h in range(n_heads)])
+    k_n = np.concatenate([rmsnorm_cpu(k[h * h_dim:(h + 1) * h_dim], w["k"]) for h in range(n_kv)])
+    st["q_rope"] = q_rope = rope_cpu_gemma(q_n, cos_sin_row, h_dim)
+    k_rope = rope_cpu_gemma(k_n, cos_sin_row, h_dim)
+    k_cache[:, pos, :] = k_rope.reshape(n_kv, h_dim)
+    v_cache[:, pos, :] = np.asarray(v, np.float32).reshape(n_kv, h_dim)
+    st["attn_out"] = attn_out = attention_host(q_rope, k_cache, v_cache, pos, n_heads, n_kv, h_dim,
+                                               1.0 / np.sqrt(h_dim), 512 if sliding else 0)
+    st["attn_proj"] = attn_proj = o_proj(attn_out)[:H]
+    st["x_post"] = x_post = bf16_rne(x + rmsnorm_cpu(attn_proj, w["post_attn"]))
+    st["x_norm2"] = x_norm2 = rmsnorm_cpu(x_post, w["ffn"])
+    st["down"] = down = ffn(x_norm2)[:H]
+    st["y"] = y = bf16_rne(x_post + rmsnorm_cpu(down, w["post_ffw"]))
+    return y
+
+
+def llama_decode_layer(x: np.ndarray, pos: int, w: dict, qkv_proj, o_proj, ffn, k_cache: np.ndarray,
+                       v_cache: np.ndarray, cos_sin_row: np.ndarray, n_heads: int = 32, n_kv: int = 8,
+                       stages: dict | None = None):
+    """The Llama-3.2 branch of run_layer (model.py:820-860), NPU path:
+    RMSNorm eps 1e-5 with weights (attn, ffn), no q/k norms, RoPE on 64-wide
+    heads (rope_cpu_llama), full attention scaled by 1/8, the attention and
+    FFN outputs added to the residual without a norm."""
+    H = x.shape[0]
+    q_size, k_size = n_heads * 64, n_kv * 64
+    st = {} if stages is None else stages
+    st["x_norm"] = x_norm = rmsnorm_cpu(x, w["attn"], eps=1e-5)
+    qkv = qkv_proj(x_norm)
+    q, k, v = qkv[:q_size], qkv[q_size:q_size + k_size], qkv[q_size + k_size:q_size + 2 * k_size]
+    st["q_rope"] = q_rope = rope_cpu_llama(q, cos_sin_row)
+    k_rope = rope_cpu_llama(k, cos_sin_row)
+    k_cache[:, pos, :] = k_rope.reshape(n_kv, 64)
+    v_cache[:, pos, :] = np.asarray(v, np.float32).reshape(n_kv, 64)
+    st["attn_out"] = attn_out = attention_host(q_rope, k_cache, v_cache, pos, n_heads, n_kv, 64,
+                                               1.0 / np.sqrt(64), 0)
+    st["attn_proj"] = attn_proj = o_proj(attn_out)[:H]
+    st["x_post"] = x_post = bf16_rne(x + attn_proj)
+    st["x_norm2"] = x_norm2 = rmsnorm_cpu(x_post, w["ffn"], eps=1e-5)
+    st["down"] = down = ffn(x_norm2)[:H]
+    st["y"] = y = bf16_rne(x_post + down)
     return y
 
 

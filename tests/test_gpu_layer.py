@@ -135,9 +135,9 @@ def test_qkv_post_bit_exact(dev, sliding, pos):
 
 # ---- attention (model.py:577-628) ---------------------------------------------------
 
-def _attn_check(q, kc, vc, pos, heads, kv, D, window, got_bits):
-    """fp64 softmax(K q) V with the float32 bound; returns the bf16 mismatch
-    count against numpy's own float32 evaluation."""
+def _attn_check(q, kc, vc, pos, heads, kv, D, window, got_bits, scale=1.0):
+    """fp64 softmax(scale K q) V with the float32 bound (scale a power of two);
+    returns the bf16 mismatch count against numpy's own float32 evaluation."""
     g = heads // kv
     seq = pos + 1
     st = max(0, seq - window) if window else 0
@@ -147,15 +147,15 @@ def _attn_check(q, kc, vc, pos, heads, kv, D, window, got_bits):
         k64 = kc[h // g, st:seq].astype(np.float64)
         v64 = vc[h // g, st:seq].astype(np.float64)
         qh = q[h * D:(h + 1) * D].astype(np.float64)
-        s = k64 @ qh
-        ds = (D + 2) * 2.0 ** -24 * (np.abs(k64) @ np.abs(qh))  # float32 score error
+        s = (k64 @ qh) * scale
+        ds = (D + 2) * 2.0 ** -24 * (np.abs(k64) @ np.abs(qh)) * scale  # float32 score error
         p = np.exp(s - s.max())
         p /= p.sum()
         ref[h * D:(h + 1) * D] = p @ v64
         # score errors move the weights by exp(+-2 ds); plus float32 sums over W and D
         bound[h * D:(h + 1) * D] = (np.expm1(2 * ds.max()) + (seq - st + 16) * 2.0 ** -23) * (p @ np.abs(v64)) + 1e-30
     parity.bf16_interval_check(got_bits, ref, bound, "attention")
-    npy = qn.attention_host(q, kc, vc, pos, heads, kv, D, 1.0, window)
+    npy = qn.attention_host(q, kc, vc, pos, heads, kv, D, scale, window)
     return int((parity.bits_bf16_f32(got_bits) != npy).sum())
 
 
@@ -394,6 +394,86 @@ def test_gemma4_layer_stagewise(orc, dev, sliding, fuse):
         assert np.array_equal(g["down"], qn.bf16_rne(y32))
         y_ref = qn.bf16_rne(qn.bf16_rne(x_post + qn.rmsnorm_cpu(g["down"], norms["post_ffw"])) * scale)
         assert np.array_equal(bf_np(y), y_ref)
+    L.close()
+
+
+@pytest.mark.parametrize("kind,sliding,fuse", [("gemma3", True, True), ("gemma3", False, False),
+                                               ("llama", False, True), ("llama", False, False)])
+def test_gemma3_llama_layer_stagewise(orc, dev, kind, sliding, fuse):
+    """The Gemma-3 (1B: H 1152, 4 q heads and 1 kv head of 256, FFN 6912
+    GeGLU) and Llama-3.2 (1B: H 2048, 32 q heads and 8 kv heads of 64, FFN
+    8192 SwiGLU) layers at their real shapes, every stage against the
+    reference's arithmetic as the oracle restates it
+    (gemma3_decode_layer, llama_decode_layer): norms, RoPE, cache insert and
+    the residual steps bit-exact; the projections within the GEMV bound;
+    attention within its fp64 bound; the FFN on the GPU's own input."""
+    from alveare_amd import layer
+
+    S = 96
+    if kind == "gemma3":
+        H, I, heads, kv, D = 1152, 6912, 4, 1, 256
+        eps, act = 1e-6, 0
+    else:
+        H, I, heads, kv, D = 2048, 8192, 32, 8, 64
+        eps, act = 1e-5, 1
+    q_size, k_size = heads * D, kv * D
+    n_qkv = q_size + 2 * k_size
+    _say(f"{kind} layer sliding={sliding} fuse={fuse} H={H} I={I}")
+    rng = np.random.default_rng(400 + sliding + 2 * fuse + (10 if kind == "llama" else 0))
+    base = 410 if kind == "gemma3" else 420
+    Wqkv = orc.synth_q4(n_qkv, H, base + 1)
+    Wo = orc.synth_q4(H, q_size, base + 2)
+    Wg, Wu, Wd = orc.synth_q4(I, H, base + 3), orc.synth_q4(I, H, base + 4), orc.synth_q4(H, I, base + 5)
+    names = ("attn", "q", "k", "post_attn", "ffn", "post_ffw") if kind == "gemma3" else ("attn", "ffn")
+    norms = {k: rng.uniform(0.5, 1.5, D if k in ("q", "k") else H).astype(np.float32) for k in names}
+    if kind == "gemma3":
+        L = layer.Gemma3DecodeLayer(qkv=Wqkv, o=Wo, gate=Wg, up=Wu, down=Wd, norms=norms, sliding=sliding,
+                                    max_seq=S, device=dev, fuse=fuse)
+        table = qn.cos_sin_table_gemma(10000.0 if sliding else 1e6, D, S, gemma4=False)
+        window = 512 if sliding else 0
+    else:
+        L = layer.LlamaDecodeLayer(qkv=Wqkv, o=Wo, gate=Wg, up=Wu, down=Wd, norms=norms, max_seq=S, device=dev,
+                                   fuse=fuse)
+        table = qn.cos_sin_table_llama(S)
+        window = 0
+    assert np.array_equal(bf_np(L.rope).reshape(S, -1), table)
+    kc = np.zeros((kv, S, D), np.float32)
+    vc = np.zeros((kv, S, D), np.float32)
+    for pos in (0, 1, 2, 40, 95):
+        x = rnd_bf16(rng, H, 1.0)
+        y = L.forward(bf_dev(x, dev), pos)
+        torch.cuda.synchronize()
+        g = {k: bf_np(getattr(L, k)) for k in ("x_norm", "qkv_out", "q_rope", "attn_out", "attn_proj", "x_post",
+                                                "down")}
+        assert np.array_equal(g["x_norm"], qn.rmsnorm_cpu(x, norms["attn"], eps=eps))
+        parity.gemv_bf16_check(orc, Wqkv, g["x_norm"], parity.bf16_bits(L.qkv_out), n_qkv, H)
+        qkv = g["qkv_out"]
+        q, k, v = qkv[:q_size], qkv[q_size:q_size + k_size], qkv[q_size + k_size:]
+        if kind == "gemma3":
+            q_n = np.concatenate([qn.rmsnorm_cpu(q[h * D:(h + 1) * D], norms["q"]) for h in range(heads)])
+            k_n = np.concatenate([qn.rmsnorm_cpu(k[h * D:(h + 1) * D], norms["k"]) for h in range(kv)])
+            q_r, k_r = qn.rope_cpu_gemma(q_n, table[pos], D), qn.rope_cpu_gemma(k_n, table[pos], D)
+        else:
+            q_r, k_r = qn.rope_cpu_llama(q, table[pos]), qn.rope_cpu_llama(k, table[pos])
+        assert np.array_equal(g["q_rope"], q_r)
+        kc[:, pos] = k_r.reshape(kv, D)
+        vc[:, pos] = v.reshape(kv, D)
+        assert np.array_equal(bf_np(L.kcache).reshape(kv, S, D), kc)
+        assert np.array_equal(bf_np(L.vcache).reshape(kv, S, D), vc)
+        _attn_check(g["q_rope"], kc, vc, pos, heads, kv, D, window, parity.bf16_bits(L.attn_out),
+                    scale=1.0 / np.sqrt(D))
+        parity.gemv_bf16_check(orc, Wo, g["attn_out"], parity.bf16_bits(L.attn_proj), H, q_size)
+        branch = qn.rmsnorm_cpu(g["attn_proj"], norms["post_attn"]) if kind == "gemma3" else g["attn_proj"]
+        x_post = qn.bf16_rne(x + branch)
+        assert np.array_equal(g["x_post"], x_post)
+        x_norm2 = qn.rmsnorm_cpu(x_post, norms["ffn"], eps=eps)
+        if not fuse:
+            assert np.array_equal(bf_np(L.x_norm2), x_norm2)
+        y32 = L.ffn(torch.from_numpy(x_norm2).to(dev)).cpu().numpy().reshape(-1)
+        parity.ffn_check(orc, Wg, Wu, Wd, x_norm2, H, I, act, y32, a_test=L.ffn.last_activation().cpu().numpy().reshape(-1))
+        assert np.array_equal(g["down"], qn.bf16_rne(y32))
+        down_b = qn.rmsnorm_cpu(g["down"], norms["post_ffw"]) if kind == "gemma3" else g["down"]
+        assert np.array_equal(bf_np(y), qn.bf16_rne(x_post + down_b))
     L.close()
 
 

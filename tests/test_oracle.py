@@ -485,6 +485,81 @@ def test_gemma4_layer_restatement_closed_form():
     assert np.any(kc[:, 3] != 0) and not np.any(kc[:, 4])
 
 
+def test_llama_rope_restatement_pins():
+    """cos_sin_table_llama against closed forms: position 0 is (cos 1, sin 0);
+    each row repeats its 32 cosines and 32 sines; the fastest angle (inverse
+    frequency 1, wavelength 2 pi below the high-frequency bound 2048) is the
+    position itself, the slowest (wavelength above 8192) is divided by the
+    factor 32, and a medium one follows the smoothing between the two. Then
+    rope_cpu_llama: identity at position 0, and on a made-up row whose
+    cosines are 0 and whose sines (values 64..95) are 1 the exact swap
+    y1 = -x2, y2 = x1 -- with values 32..63 set to a decoy that a reader of
+    the wrong offset would pick up."""
+    t = q4_numpy.cos_sin_table_llama(300)
+    assert np.all(t[0, :64] == 1.0) and np.all(t[0, 64:] == 0.0)
+    assert np.array_equal(t[:, 32:64], t[:, :32]) and np.array_equal(t[:, 96:], t[:, 64:96])
+    pos = np.arange(300, dtype=np.float64)
+    inv = 500000.0 ** (-np.arange(0, 64, 2) / 64.0)
+    wl = 2 * np.pi / inv
+    assert wl[0] < 2048 and wl[31] > 8192
+    assert np.all(np.abs(t[:, 0] - np.cos(pos)) <= 2.0 ** -8 + 1e-6)
+    assert np.all(np.abs(t[:, 64] - np.sin(pos)) <= 2.0 ** -8 + 1e-6)
+    assert np.all(np.abs(t[:, 31] - np.cos(pos * inv[31] / 32)) <= 2.0 ** -8 + 1e-6)
+    med = [i for i in range(32) if 2048 <= wl[i] <= 8192]
+    assert med
+    i = med[0]
+    sm = (8192 / wl[i] - 1.0) / 3.0
+    f = (1 - sm) * inv[i] / 32 + sm * inv[i]
+    assert np.all(np.abs(t[:, i] - np.cos(pos * f)) <= 2.0 ** -8 + 1e-5)
+    assert not np.allclose(t[:, i], np.cos(pos * inv[i]), atol=1e-2)  # not the unscaled angle
+    rng = np.random.default_rng(8)
+    x = q4_numpy.bf16_rne(rng.normal(0, 1, 8 * 64).astype(np.float32))
+    assert np.array_equal(q4_numpy.rope_cpu_llama(x, t[0]), x)
+    row = np.zeros(128, np.float32)
+    row[32:64] = 0.5  # decoy
+    row[64:96] = 1.0
+    y = q4_numpy.rope_cpu_llama(x, row).reshape(8, 64)
+    xr = x.reshape(8, 64)
+    assert np.array_equal(y[:, :32], -xr[:, 32:]) and np.array_equal(y[:, 32:], xr[:, :32])
+
+
+def test_gemma3_llama_layer_restatement_closed_forms():
+    """With the FFN's output zero and the O projection returning a fixed c,
+    a Llama layer is y = bf16(x + c) (no norm on the residual adds) and a
+    Gemma-3 layer y = bf16(x + rmsnorm(c) * w_post_attn) (the post-attention
+    norm, no output scale); with both zero, y = x. The caches receive the
+    rotated k (Gemma-3: after its norm) and the raw v at pos."""
+    rng = np.random.default_rng(9)
+    # Llama: H 256, 4 q heads and 2 kv heads of 64.
+    H = 256
+    x = q4_numpy.bf16_rne(rng.normal(0, 1, H).astype(np.float32))
+    c = q4_numpy.bf16_rne(rng.normal(0, 1, H).astype(np.float32))
+    w = {k: rng.uniform(0.5, 1.5, H).astype(np.float32) for k in ("attn", "ffn")}
+    qkv_val = q4_numpy.bf16_rne(rng.normal(0, 1, 8 * 64).astype(np.float32))
+    kc, vc = np.zeros((2, 16, 64), np.float32), np.zeros((2, 16, 64), np.float32)
+    t = q4_numpy.cos_sin_table_llama(16)
+    zero = lambda a: np.zeros(H, np.float32)  # noqa: E731
+    y = q4_numpy.llama_decode_layer(x, 5, w, lambda xn: qkv_val, lambda a: c, zero, kc, vc, t[5], 4, 2)
+    assert np.array_equal(y, q4_numpy.bf16_rne(x + c))
+    y0 = q4_numpy.llama_decode_layer(x, 6, w, lambda xn: qkv_val, zero, zero, kc, vc, t[6], 4, 2)
+    assert np.array_equal(y0, x)
+    assert np.array_equal(kc[:, 5].reshape(-1), q4_numpy.rope_cpu_llama(qkv_val[256:384], t[5]))
+    assert np.array_equal(vc[:, 5].reshape(-1), qkv_val[384:512])
+    # Gemma-3: H 256, 2 q heads and 1 kv head of 256.
+    wg = {k: rng.uniform(0.5, 1.5, 256).astype(np.float32) for k in ("attn", "q", "k", "post_attn", "ffn", "post_ffw")}
+    qkv3 = q4_numpy.bf16_rne(rng.normal(0, 1, 4 * 256).astype(np.float32))
+    kc3, vc3 = np.zeros((1, 16, 256), np.float32), np.zeros((1, 16, 256), np.float32)
+    tg = q4_numpy.cos_sin_table_gemma(10000.0, 256, 16)
+    y3 = q4_numpy.gemma3_decode_layer(x, 4, True, wg, lambda xn: qkv3, lambda a: c, zero, kc3, vc3, tg[4], 2, 1)
+    assert np.array_equal(y3, q4_numpy.bf16_rne(x + q4_numpy.rmsnorm_cpu(c, wg["post_attn"])))
+    assert not np.array_equal(y3, q4_numpy.bf16_rne(x + c))
+    y30 = q4_numpy.gemma3_decode_layer(x, 5, False, wg, lambda xn: qkv3, zero, zero, kc3, vc3, tg[5], 2, 1)
+    assert np.array_equal(y30, x)
+    k_n = q4_numpy.rmsnorm_cpu(qkv3[512:768], wg["k"])
+    assert np.array_equal(kc3[0, 4], q4_numpy.rope_cpu_gemma(k_n, tg[4], 256))
+    assert np.array_equal(vc3[0, 4], qkv3[768:1024])
+
+
 def test_ffn_check_batch_pins(orc):
     """The batched flip-aware FFN check (tests/parity.py::ffn_check_batch)
     accepts the float32 oracle's own outputs and rejects a planted mistake:

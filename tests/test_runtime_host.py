@@ -46,3 +46,17 @@ def test_lazy_layer_weights_refuses_pickles(tmp_path):
     np.save(tmp_path / "blk.0.attn_q.weight_packed.npy", np.array([{"x": 1}], dtype=object), allow_pickle=True)
     with pytest.raises(ValueError):
         LazyLayerWeights(tmp_path, 0, device="cpu")
+
+
+def test_rope_tables_match_the_oracle():
+    """The layers' RoPE tables (built on the host when a layer is created)
+    equal the oracle's restatements bit for bit: Llama-3.2's scaled table and
+    Gemma-3's 256-wide one."""
+    import parity
+    from alveare_amd import layer
+    from oracle import q4_numpy as qn
+
+    assert np.array_equal(layer.cos_sin_table_llama(300), parity.f32_bits_bf16(qn.cos_sin_table_llama(300)))
+    for base in (10000.0, 1e6):
+        assert np.array_equal(layer.cos_sin_table_gemma(base, 256, 64, gemma4=False),
+                              parity.f32_bits_bf16(qn.cos_sin_table_gemma(base, 256, 64, gemma4=False)))
