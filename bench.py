@@ -85,7 +85,7 @@ def _cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(threads: int) -> dict:
+def cpu_baseline(threads: int, host: dict | None = None) -> dict:
     """The oracle (a C restatement of the reference's CPU path) timed on this
     host: one 12B-class layer per call as the reference computes it (per call
     dequantize each matrix to fp32, fp32 matvec, the FFN's bf16 rounding
@@ -94,7 +94,8 @@ def cpu_baseline(threads: int) -> dict:
     and the 2048 x 2048 gemv_q the reference publishes a CPU time for
     (47.91 ms, tests/bench/gemv_q_bench.txt:3). Median of 10 after 2
     warm-ups (median of 3 after 1 for the one-thread layer, to bound the
-    sample to seconds)."""
+    sample to seconds). `host`: the GPU run's first layer and inputs
+    (build_layers), timed in place of seeded synthetic ones."""
     import ctypes
 
     import numpy as np
@@ -104,20 +105,25 @@ def cpu_baseline(threads: int) -> dict:
     L = oracle.lib()
     u8, f32 = ctypes.POINTER(ctypes.c_uint8), ctypes.POINTER(ctypes.c_float)
     ptr = lambda a, t: a.ctypes.data_as(t)  # noqa: E731
-    Wq = oracle.synth_q4(N_QKV, H, oracle.seed_for(3, 0))
-    Wo = oracle.synth_q4(H, K_O, oracle.seed_for(3, 1))
-    Wg = oracle.synth_q4(I_FF, H, oracle.seed_for(3, 2))
-    Wu = oracle.synth_q4(I_FF, H, oracle.seed_for(3, 3))
-    Wd = oracle.synth_q4(H, I_FF, oracle.seed_for(3, 4))
-    x = oracle.synth_normal(K_O, oracle.seed_for(3, 5))
+    if host:
+        Wq, Wo, Wg, Wu, Wd = (np.ascontiguousarray(host[k]) for k in ("Wq", "Wo", "Wg", "Wu", "Wd"))
+        xq, xo, xf = (np.ascontiguousarray(host[k], dtype=np.float32) for k in ("x_qkv", "x_o", "x_ffn"))
+    else:
+        Wq = oracle.synth_q4(N_QKV, H, oracle.seed_for(3, 0))
+        Wo = oracle.synth_q4(H, K_O, oracle.seed_for(3, 1))
+        Wg = oracle.synth_q4(I_FF, H, oracle.seed_for(3, 2))
+        Wu = oracle.synth_q4(I_FF, H, oracle.seed_for(3, 3))
+        Wd = oracle.synth_q4(H, I_FF, oracle.seed_for(3, 4))
+        xo = oracle.synth_normal(K_O, oracle.seed_for(3, 5))
+        xq = xf = xo[:H].copy()
     yq, yo, yf = np.empty(N_QKV, np.float32), np.empty(H, np.float32), np.empty(H, np.float32)
 
     def layer(th: int, pre: bool = False) -> float:
         g = L.orc_time_gemv_predequant if pre else L.orc_time_gemv_faithful
         f = L.orc_time_ffn_predequant if pre else L.orc_time_ffn_faithful
-        t = g(ptr(Wq, u8), ptr(x, f32), ptr(yq, f32), N_QKV, H, 1, th)
-        t += g(ptr(Wo, u8), ptr(x, f32), ptr(yo, f32), H, K_O, 1, th)
-        t += f(ptr(Wg, u8), ptr(Wu, u8), ptr(Wd, u8), ptr(x, f32), ptr(yf, f32), H, I_FF, 1, th)
+        t = g(ptr(Wq, u8), ptr(xq, f32), ptr(yq, f32), N_QKV, H, 1, th)
+        t += g(ptr(Wo, u8), ptr(xo, f32), ptr(yo, f32), H, K_O, 1, th)
+        t += f(ptr(Wg, u8), ptr(Wu, u8), ptr(Wd, u8), ptr(xf, f32), ptr(yf, f32), H, I_FF, 1, th)
         return t
 
     def med(fn, warm: int, n: int) -> float:
@@ -151,6 +157,7 @@ def cpu_baseline(threads: int) -> dict:
             "c1_gemv_2048x2048": {"ms_all_threads": round(c1_all * 1e3, 3), "ms_1_thread": round(c1_one * 1e3, 3),
                                   "reference_numpy_ms": 47.91},
         },
+        "inputs": "the GPU run's first layer and inputs" if host else "seeded synthetic (oracle.synth_q4)",
         "sample": (f"1 layer (QKV {N_QKV}x{H} + O {H}x{K_O} + FFN {H}x{I_FF}) through the oracle's "
                    f"restatement of the reference CPU path (per call: dequantize to an fp32 matrix, "
                    f"fp32 matvec; FFN bf16 rounding points), median of 10 after 2 warm-ups, {threads} "
@@ -159,22 +166,33 @@ def cpu_baseline(threads: int) -> dict:
     }
 
 
-def build_layers(torch, aa, nl, dev):
+def build_layers(torch, aa, nl, dev, host: dict | None = None):
+    """nl layers of synthetic registered weights and the ops' inputs. With
+    `host` (a dict), the first layer's combined-layout matrices and the
+    inputs are also copied into it as NumPy arrays (the CPU baseline's
+    inputs)."""
     gen = torch.Generator(device=dev)
     gen.manual_seed(0xA1E00300)
     layers = []
-    for _ in range(nl):
-        wq = aa.Q4Weight(synth_q4_dev(torch, N_QKV, H, gen, dev), N_QKV, H)
-        wo = aa.Q4Weight(synth_q4_dev(torch, H, K_O, gen, dev), H, K_O)
+    for i in range(nl):
+        mq = synth_q4_dev(torch, N_QKV, H, gen, dev)
+        mo = synth_q4_dev(torch, H, K_O, gen, dev)
         wg = synth_q4_dev(torch, I_FF, H, gen, dev)
         wu = synth_q4_dev(torch, I_FF, H, gen, dev)
         wd = synth_q4_dev(torch, H, I_FF, gen, dev)
+        if host is not None and i == 0:
+            for k, t in (("Wq", mq), ("Wo", mo), ("Wg", wg), ("Wu", wu), ("Wd", wd)):
+                host[k] = t.cpu().numpy().reshape(-1)
+        wq, wo = aa.Q4Weight(mq, N_QKV, H), aa.Q4Weight(mo, H, K_O)
         ffn = aa.FfnWeights(wg, wu, wd, H, I_FF, "gelu")
-        del wg, wu, wd
+        del mq, mo, wg, wu, wd
         layers.append((wq, wo, ffn))
     torch.cuda.empty_cache()
     xs = {k: torch.randn(n, device=dev, generator=gen) for k, n in (("qkv", H), ("o", K_O), ("ffn", H))}
     ys = {k: torch.empty(n, device=dev) for k, n in (("qkv", N_QKV), ("o", H), ("ffn", H))}
+    if host is not None:
+        for k in xs:
+            host["x_" + k] = xs[k].cpu().numpy()
     return layers, xs, ys
 
 
@@ -565,7 +583,8 @@ def main() -> int:
     nl = args.layers
     log(f"building {nl} synthetic layers on {torch.cuda.get_device_name(dev)}")
     t0 = time.time()
-    layers, xs, ys = build_layers(torch, aa, nl, dev)
+    host = {} if not args.no_cpu_baseline else None
+    layers, xs, ys = build_layers(torch, aa, nl, dev, host)
     torch.cuda.synchronize()
     log(f"layers ready in {time.time() - t0:.1f}s; {torch.cuda.memory_allocated() / 1e9:.2f} GB held by torch")
 
@@ -780,7 +799,7 @@ def main() -> int:
     if not args.no_cpu_baseline:
         threads = args.cpu_threads or int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
         try:
-            out["cpu_baseline"] = cpu_baseline(threads)
+            out["cpu_baseline"] = cpu_baseline(threads, host)
         except Exception as e:  # the baseline is reported, never required
             out["cpu_baseline"] = {"error": repr(e)}
     print(json.dumps(out), flush=True)
