@@ -28,10 +28,12 @@ _i64 = ctypes.c_int64
 
 
 def build(ref: bool = False) -> None:
-    """Compile the oracle (and, with ``ref``, the reference's bf16.cpp into _ref/)."""
+    """Compile the oracle (and, with ``ref``, the reference's bf16.cpp into _ref/
+    and the reference's C++ runtime against this build's NpuRegistry adapter)."""
     subprocess.run(["make", "-s", "-C", _HERE, "all"], check=True)
     if ref:
         subprocess.run(["make", "-s", "-C", _HERE, "ref"], check=True)
+        subprocess.run(["make", "-s", "-C", _HERE, "ref-runtime"], check=True)
 
 
 def lib() -> ctypes.CDLL:
