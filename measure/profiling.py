@@ -7,6 +7,9 @@
         the same run's Q4 dispatches grouped by launch shape (grid, LDS).
     python -m measure.profiling counters <dir>
         mean per dispatch of every counter of a ``--pmc`` run, per Q4 kernel.
+    python -m measure.profiling decode <dir>
+        per-op medians of a decode-step run (bench.py --decode-step under
+        ``--kernel-trace``), each launch named by its place in the step.
     python -m measure.profiling traffic <fetch_dir> <write_dir> <copy_bytes>
         HBM bytes per dispatch of every q4 kernel from one ``--pmc FETCH_SIZE``
         and one ``--pmc WRITE_SIZE`` run of ``bench.py --profile-pass``, each
@@ -105,6 +108,49 @@ def traffic(fetch_dir: str, write_dir: str, copy_bytes: int) -> str:
     return "\n".join(out)
 
 
+def decode(d: str) -> str:
+    """Median duration of each op of the decode step, the launches named by
+    their order: the streaming GEMV with 256 workgroups is the QKV launch, or
+    the LM head after the final residual step; with 240 workgroups it is O
+    after the attention merge or FFN down after the gate/up launch."""
+    with open(_find(d, "kernel_trace.csv")) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    out = defaultdict(list)
+    prev = None
+    for r in rows:
+        n = r["Kernel_Name"]
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+        wg = int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"]))
+        if "attn_partial" in n:
+            tag = "attention, global" if "512" in n else "attention, sliding"
+        elif "attn_merge" in n:
+            tag = "attention merge"
+        elif "head_fold" in n:
+            tag = "head fold"
+        elif "head_kernel" in n:
+            tag = "head softcap/argmax"
+        elif "embed_kernel" in n:
+            tag = "embedding"
+        elif "add_norm_kernel" in n:
+            tag = "final residual step + norm"
+        elif "rmsnorm_kernel" in n:
+            tag = "layer-0 input norm"
+        elif "q4_gemv1_kernel" in n and "true, true, 1," in n:
+            tag = "gate/up + residual step"
+        elif "q4_gemv1_kernel" in n and wg == 240:
+            tag = "FFN down" if prev == "gate/up + residual step" else "O"
+        elif "q4_gemv1_kernel" in n:
+            tag = "LM-head GEMV" if prev == "final residual step + norm" else "QKV + residual step"
+        else:
+            continue
+        out[tag].append(us)
+        prev = tag
+    lines = ["op | launches | median us | mean us"]
+    for tag, v in out.items():
+        lines.append(f"{tag} | {len(v)} | {statistics.median(v):.2f} | {statistics.mean(v):.2f}")
+    return "\n".join(lines)
+
+
 def counters(d: str) -> str:
     """Mean per dispatch of every counter of a --pmc run, per Q4 kernel, plus
     the ratios that matter here (LDS conflicts per access, MFMA and VALU busy
@@ -135,6 +181,9 @@ def main(argv) -> int:
         return 0
     if len(argv) >= 2 and argv[0] == "launches":
         print(launches(argv[1]))
+        return 0
+    if len(argv) >= 2 and argv[0] == "decode":
+        print(decode(argv[1]))
         return 0
     if len(argv) >= 2 and argv[0] == "counters":
         print(counters(argv[1]))
