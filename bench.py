@@ -226,6 +226,38 @@ def profile_pass(torch, aa, dev) -> int:
     return 0
 
 
+def vendor_gemm_us(torch, dev, M: int, H: int, I: int, nl: int) -> dict:
+    """µs per call of torch.matmul (the platform's hipBLASLt / rocBLAS bf16
+    GEMM) at the M-token FFN's two products, gate and up together (M x 2I x H)
+    and down (M x H x I), over nl distinct random bf16 weight sets: a yardstick
+    for the Q4 prefill kernels, which also dequantize and apply the GeGLU."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0xA1E00B1A)
+    x = torch.randn(M, H, device=dev, dtype=torch.bfloat16, generator=gen)
+    h = torch.randn(M, I, device=dev, dtype=torch.bfloat16, generator=gen)
+    wgu = [torch.randn(2 * I, H, device=dev, dtype=torch.bfloat16, generator=gen) for _ in range(nl)]
+    wd = [torch.randn(H, I, device=dev, dtype=torch.bfloat16, generator=gen) for _ in range(nl)]
+
+    def timed(fn, reps: int = 3) -> float:
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / (reps * nl)
+
+    gu = timed(lambda: [x @ w.t() for w in wgu])
+    dn = timed(lambda: [h @ w.t() for w in wd])
+    del wgu, wd
+    torch.cuda.empty_cache()
+    return {"gate_up_us": round(gu, 2), "down_us": round(dn, 2), "sum_us": round(gu + dn, 2),
+            "TFLOPs": round(2.0 * M * 3 * I * H / (gu + dn) / 1e6, 1),
+            "note": "torch.matmul bf16 on pre-dequantized weights, no GeGLU; scale reference only"}
+
+
 _CAPTURE_STREAM = None
 
 
@@ -656,6 +688,10 @@ def main() -> int:
         flops = 2.0 * Mp * 3 * I_FF * H
         extra["prefill_ffn_m512"] = {"us": round(us, 2), "TFLOPs": round(flops / us / 1e6, 1),
                                      "mfma_frac_bf16_dense": round(flops / us / 1e6 / 2500.0, 4)}
+        # For scale only (not the product path): the vendor bf16 GEMM
+        # (torch.matmul -> hipBLASLt) on already-dequantized bf16 weights of the
+        # same shapes, without the GeGLU between the two products.
+        extra["prefill_ffn_m512"]["vendor_bf16_gemm_reference"] = vendor_gemm_us(torch, dev, Mp, H, I_FF, npf)
 
         # Where the streaming kernel should hand over to the MFMA tiled kernel
         # (small-M decode against the 12B-class FFN): both kernels at M = 8 ... 128
