@@ -641,8 +641,14 @@ __device__ __forceinline__ void finish_rows(const Gemv1Args& a, const WgWork& wk
     if (tid == 0) __hip_atomic_store(&a.cnt[wk.tg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int NW, int P, int R, bool XB, bool GLU, int MT, bool TB, bool TL>
-__global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
+// ST: the workgroups compute their activation from a fused residual step
+// (a.pr_r set). Those launches run a kernel of their own
+// (q4_gemv1_step_kernel), so the one-token launches without a step (O, FFN
+// down, the LM head) carry none of its code: decode-step rocprof on one box,
+// O 5.84-5.92 against 6.00 µs, down 11.32-11.36 against 11.44, head
+// 104.6-105.3 against 107.0-107.3.
+template <int NW, int P, int R, bool XB, bool GLU, int MT, bool TB, bool TL, bool ST>
+__device__ __forceinline__ void gemv1_body(const Gemv1Args& a) {
     using Ph = PhaseT<R, XB, GLU, MT, TB>;
     constexpr int NT = Ph::NT, SR = Ph::SR, US = Ph::US;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -671,7 +677,7 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     // (issuing the first weight loads ahead of a fused residual step's
     // computation measured slower as well).
     bool fused = false;
-    if constexpr (XB && MT == 1) {
+    if constexpr (XB && MT == 1 && ST) {
         if (a.pr_r) {
             // The fused residual step's LDS follows the unit counter.
             float* red = reinterpret_cast<float*>(next + 4);
@@ -713,6 +719,16 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
     }
     lds_barrier();
     finish_rows<NW, R, GLU, MT, TB>(a, wk, part, U * US, next, tid);
+}
+
+template <int NW, int P, int R, bool XB, bool GLU, int MT, bool TB, bool TL>
+__global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
+    gemv1_body<NW, P, R, XB, GLU, MT, TB, TL, false>(a);
+}
+
+template <int NW, int P, int R, bool XB, bool GLU, int MT, bool TB, bool TL>
+__global__ void __launch_bounds__(64 * NW) q4_gemv1_step_kernel(Gemv1Args a) {
+    gemv1_body<NW, P, R, XB, GLU, MT, TB, TL, true>(a);
 }
 
 // The split-K sums of a launch made with a.fix, after it: workgroup b adds
@@ -810,9 +826,13 @@ inline hipError_t ensure_lds(const void* k, std::atomic<int> (&set)[64], size_t 
     return hipSuccess;
 }
 
-template <int P, int R, bool XB, bool GLU, int MT, bool TB = false, bool TL = true>
+template <int P, int R, bool XB, bool GLU, int MT, bool TB = false, bool TL = true, bool ST = false>
 hipError_t launch_k(const Gemv1Args& a, int groups, size_t lds, hipStream_t s) {
-    auto k = q4_gemv1_kernel<kNW, P, R, XB, GLU, MT, TB, TL>;
+    void (*k)(Gemv1Args);
+    if constexpr (ST)
+        k = q4_gemv1_step_kernel<kNW, P, R, XB, GLU, MT, TB, TL>;
+    else
+        k = q4_gemv1_kernel<kNW, P, R, XB, GLU, MT, TB, TL>;
     static std::atomic<int> set[64];
     if (const hipError_t e = ensure_lds(reinterpret_cast<const void*>(k), set, lds)) return e;
     hipLaunchKernelGGL(k, dim3(groups), dim3(64 * kNW), lds, s, a);
@@ -855,7 +875,9 @@ Shape shape_for(const GemvLaunch& L, int m) {
 hipError_t launch_shape(const Gemv1Args& a, const GemvLaunch& L, Shape sh, int groups, size_t lds, hipStream_t s) {
     if (L.Xb && L.glu) {
         switch (sh.mt) {
-            case 1: return launch_k<kP, 1, true, true, 1>(a, groups, lds, s);
+            case 1:
+                return a.pr_r ? launch_k<kP, 1, true, true, 1, false, true, true>(a, groups, lds, s)
+                              : launch_k<kP, 1, true, true, 1>(a, groups, lds, s);
             case 2: return launch_k<kP, 1, true, true, 2>(a, groups, lds, s);
             case 4: return launch_k<kP, 1, true, true, 4>(a, groups, lds, s);
             case 8: return launch_k<kPWide, 1, true, true, 8>(a, groups, lds, s);
@@ -864,7 +886,9 @@ hipError_t launch_shape(const Gemv1Args& a, const GemvLaunch& L, Shape sh, int g
     }
     if (L.Xb) {
         switch (sh.mt) {
-            case 1: return launch_k<kP, 1, true, false, 1>(a, groups, lds, s);
+            case 1:
+                return a.pr_r ? launch_k<kP, 1, true, false, 1, false, true, true>(a, groups, lds, s)
+                              : launch_k<kP, 1, true, false, 1>(a, groups, lds, s);
             case 2: return launch_k<kP, 1, true, false, 2>(a, groups, lds, s);
             case 4: return launch_k<kP, 1, true, false, 4>(a, groups, lds, s);
             case 8: return launch_k<kPWide, 1, true, false, 8>(a, groups, lds, s);

@@ -27,7 +27,7 @@ import statistics
 import sys
 from collections import defaultdict
 
-Q4_KERNELS = ("q4_gemv1_kernel", "gemm_q4_kernel", "tile_kernel", "rmsnorm_kernel", "qkv_post_kernel",
+Q4_KERNELS = ("q4_gemv1_kernel", "q4_gemv1_step_kernel", "gemm_q4_kernel", "tile_kernel", "rmsnorm_kernel", "qkv_post_kernel",
               "attn_partial_kernel", "attn_merge_kernel", "add_norm_kernel", "embed_kernel", "head_kernel",
               "head_fold_kernel", "quant_kernel", "split_x_kernel", "split_fix_kernel")
 CALIBRATION = "MulFunctor"  # the profile pass's copy: torch.mul(src, 1.0, out=dst)
@@ -110,9 +110,11 @@ def traffic(fetch_dir: str, write_dir: str, copy_bytes: int) -> str:
 
 def decode(d: str) -> str:
     """Median duration of each op of the decode step, the launches named by
-    their order: the streaming GEMV with 256 workgroups is the QKV launch, or
-    the LM head after the final residual step; with 240 workgroups it is O
-    after the attention merge or FFN down after the gate/up launch."""
+    their order: the streaming GEMV with a fused residual step is the QKV or
+    the gate/up launch (its instance: GLU or not); without one, with 256
+    workgroups it is the LM head after the final residual step (or layer 0's
+    QKV after the input norm), with 240 workgroups O after the attention
+    merge or FFN down after the gate/up launch."""
     with open(_find(d, "kernel_trace.csv")) as f:
         rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
     out = defaultdict(list)
@@ -135,12 +137,12 @@ def decode(d: str) -> str:
             tag = "final residual step + norm"
         elif "rmsnorm_kernel" in n:
             tag = "layer-0 input norm"
-        elif "q4_gemv1_kernel" in n and "true, true, 1," in n:
-            tag = "gate/up + residual step"
+        elif "q4_gemv1_step_kernel" in n:
+            tag = "gate/up + residual step" if "true, true, 1," in n else "QKV + residual step"
         elif "q4_gemv1_kernel" in n and wg == 240:
             tag = "FFN down" if prev == "gate/up + residual step" else "O"
         elif "q4_gemv1_kernel" in n:
-            tag = "LM-head GEMV" if prev == "final residual step + norm" else "QKV + residual step"
+            tag = "LM-head GEMV" if prev == "final residual step + norm" else "QKV, layer 0"
         else:
             continue
         out[tag].append(us)
