@@ -46,6 +46,8 @@ SIGNATURES: dict[str, tuple] = {
     "alv_weight_release": (None, [_vp]),
     "alv_lm_head": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _vp, _vp]),
     "alv_lm_head_bf16": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _vp, _vp, _i, _vp]),
+    "alv_lm_head_bf16_addnorm": (_i, [_vp, _vp, _vp, _vp, _i, ctypes.c_float, _i, _vp, _vp, ctypes.c_float, _i, _vp,
+                                      _i, ctypes.c_float, _vp, _vp, _i, _vp]),
     "alv_quantize_q4": (_i, [_vp, _i, _i, _i, _vp, _i, _i, _vp]),
     "alv_gemv_bf16": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "alv_ffn_fused_bf16": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),

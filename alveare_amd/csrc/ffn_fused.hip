@@ -288,7 +288,7 @@ extern "C" int alv_ffn_fused_bf16_addnorm(alv_ffn_t w, const uint16_t* resid, co
     GemvLaunch op[2];
     ffn_ops(w, w->a, nullptr, w->H, nullptr, w->H, 1, op);
     op[0].X = nullptr;
-    op[0].Xb = y;
+    op[0].Xb = y ? y : resid;
     op[0].parts = 1;
     op[0].step = &st;
     op[1].Y = nullptr;

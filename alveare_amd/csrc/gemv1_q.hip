@@ -78,6 +78,7 @@ struct Gemv1Args {
     uint16_t* pr_s;
     float pr_scale, pr_eps;
     int pr_norm_y, pr_mode;
+    int pr_k;  // width of the step's rows (K may differ: activation octets past both are zeros)
 };
 
 constexpr int kXO = 4;  // activation octets per thread and staging round
@@ -278,16 +279,21 @@ __device__ __forceinline__ void resid_octet_any(const Gemv1Args& a, float (&f)[8
     }
 }
 
+// The rows are pr_k wide; the matmul's K may differ (a head registered K
+// columns wider than the hidden size, or trimmed of all-zero columns):
+// activation octets at or past either width are zeros. Without y (pr_y null)
+// there is no residual step: s is resid as given (a first layer's input norm).
 template <int NW>
 __device__ void fused_resid_step(const Gemv1Args& a, const WgWork& wk, __bf16* xs, float* red, float* row, int tid) {
     constexpr int NT = 64 * NW;
-    const int K = a.K;
+    const int K = a.pr_k;
     const int v = tid;
     const bool in = 8 * v < K;
-    const uint4 yv = in ? reinterpret_cast<const uint4*>(a.pr_y)[v] : uint4{0u, 0u, 0u, 0u};
+    const bool has_y = a.pr_y != nullptr;
+    const uint4 yv = in && has_y ? reinterpret_cast<const uint4*>(a.pr_y)[v] : uint4{0u, 0u, 0u, 0u};
     const uint4 rv = in ? reinterpret_cast<const uint4*>(a.pr_r)[v] : uint4{0u, 0u, 0u, 0u};
     float wy[8], wx[8], f[8], rf[8];
-    load_w8(in && a.pr_norm_y ? a.pr_wy : nullptr, v, wy);
+    load_w8(in && has_y && a.pr_norm_y ? a.pr_wy : nullptr, v, wy);
     load_w8(in ? a.pr_wx : nullptr, v, wx);
     if (!a.pr_wx)  // t * 1 is t, bit for bit (NaN, signed zeros and subnormals included)
 #pragma unroll
@@ -296,7 +302,7 @@ __device__ void fused_resid_step(const Gemv1Args& a, const WgWork& wk, __bf16* x
     float inv = 1.0f;
     // Neither sum waits at its end: red is next written after the barrier
     // that follows the step, and nothing reads it after the second sum.
-    if (a.pr_norm_y) {
+    if (has_y && a.pr_norm_y) {
         if (in)
 #pragma unroll
             for (int e = 0; e < 8; ++e) row[8 * v + e] = f[e];
@@ -305,20 +311,28 @@ __device__ void fused_resid_step(const Gemv1Args& a, const WgWork& wk, __bf16* x
     }
     if (in) {  // waves wholly past K skip the step
         unpack8(rv, rf);
-        resid_octet_any(a, f, rf, wy, inv);
-        uint16_t b[8];
+        if (has_y) {
+            resid_octet_any(a, f, rf, wy, inv);
+            uint16_t b[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            b[e] = (uint16_t)(__builtin_bit_cast(uint32_t, f[e]) >> 16);  // f[e] holds a bf16 value
-            row[8 * v + e] = f[e];
+            for (int e = 0; e < 8; ++e) {
+                b[e] = (uint16_t)(__builtin_bit_cast(uint32_t, f[e]) >> 16);  // f[e] holds a bf16 value
+                row[8 * v + e] = f[e];
+            }
+            if (blockIdx.x == 0) reinterpret_cast<uint4*>(a.pr_s)[v] = pack8(b);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                f[e] = rf[e];
+                row[8 * v + e] = f[e];
+            }
         }
-        if (blockIdx.x == 0) reinterpret_cast<uint4*>(a.pr_s)[v] = pack8(b);
     }
     __syncthreads();
     const float inv2 = rms_inv<NT, false>(row, K, a.pr_eps, red, tid);
     if (v < wk.nsw * 64) {
         uint16_t xb[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (in)
+        if (in && 8 * v < a.K)
 #pragma unroll
             for (int e = 0; e < 8; ++e) xb[e] = bf16_rne_bits(mul_rn(mul_rn(f[e], inv2), wx[e]));
         const int sl = (v >> 6) * 64 + ((v & 15) << 2) + ((v >> 4) & 3);
@@ -1048,6 +1062,7 @@ int fill_args(const GemvLaunch& L, const Gemv1Plan& p, int m0, int m, hipStream_
         a.pr_eps = st->eps;
         a.pr_norm_y = st->norm_y;
         a.pr_mode = st->scale_mode;
+        a.pr_k = st->k ? st->k : L.K;
     }
     *out = a;
     return ALV_OK;
@@ -1080,7 +1095,11 @@ int launch_gemv_step(const GemvLaunch& L, hipStream_t s) {
         return fail(ALV_ERR_ARG, "a fused residual step takes one token of bf16 activations on registered weights");
     if (L.K % 8 || L.K > kResidStepMaxK)
         return fail(ALV_ERR_ARG, "a fused residual step takes K a multiple of 8 up to %d (got %d)", kResidStepMaxK, L.K);
-    if (!st.resid || !st.y || !st.sum_out) return fail(ALV_ERR_ARG, "null residual-step pointer");
+    const int rk = st.k ? st.k : L.K;  // the rows' width
+    if (rk < 8 || rk % 8 || rk > kResidStepMaxK)
+        return fail(ALV_ERR_ARG, "a fused residual step takes rows a multiple of 8 up to %d wide (got %d)",
+                    kResidStepMaxK, rk);
+    if (!st.resid || (st.y && !st.sum_out)) return fail(ALV_ERR_ARG, "null residual-step pointer");
     if (st.scale_mode < 0 || st.scale_mode > 2) return fail(ALV_ERR_ARG, "bad scale_mode %d", st.scale_mode);
     auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     if (!al(st.resid) || !al(st.y) || !al(st.sum_out) || !al(st.w_y) || !al(st.w_x))
@@ -1088,7 +1107,7 @@ int launch_gemv_step(const GemvLaunch& L, hipStream_t s) {
     Gemv1Plan p;
     if (!plan_gemv1(L, 1, &p)) return fail(ALV_ERR_RANGE, "streaming GEMV: no plan for N=%d K=%d", L.N, L.K);
     if (p.ks != 1) return fail(ALV_ERR_RANGE, "a fused residual step needs the whole of K in one workgroup (K=%d)", L.K);
-    p.lds += 128 * sizeof(float) + (size_t)L.K * sizeof(float);
+    p.lds += 128 * sizeof(float) + (size_t)rk * sizeof(float);
     if (p.lds > dev_info().lds) return fail(ALV_ERR_RANGE, "a fused residual step at K=%d exceeds the LDS", L.K);
     Gemv1Args a;
     if (int rc = fill_args(L, p, 0, 1, s, &a)) return rc;

@@ -124,7 +124,7 @@ using namespace alv;
 namespace {
 
 int lm_head(alv_weight_t w, const float* x, const uint16_t* xb, float* logits, int vocab, float softcap,
-            int32_t* argmax, int32_t* pos, int max_pos, void* stream) {
+            int32_t* argmax, int32_t* pos, int max_pos, void* stream, const ResidStep* step = nullptr) {
     if (!w || w->magic != kWeightMagic) return fail(ALV_ERR_HANDLE, "invalid weight handle");
     if ((!x && !xb) || !logits || !argmax) return fail(ALV_ERR_ARG, "null pointer");
     if (vocab < 1 || vocab > w->N) return fail(ALV_ERR_ARG, "vocab=%d outside the head's %d rows", vocab, w->N);
@@ -155,6 +155,7 @@ int lm_head(alv_weight_t w, const float* x, const uint16_t* xb, float* logits, i
     L.N = std::min(vocab, w->Ne);  // rows past the registered extent are zero logits
     L.Nz = vocab;
     L.parts = xb ? 1 : 3;
+    L.step = step;
     if (int rc = launch_gemv(L, s)) return rc;
     const int groups = std::min(kHeadGroups, (vocab + 63) / 64);
     hipLaunchKernelGGL(head_kernel, dim3(groups), dim3(kHeadThreads), 0, s, logits, vocab, softcap, pv, pi);
@@ -175,4 +176,26 @@ extern "C" int alv_lm_head_bf16(alv_weight_t w, const uint16_t* x, float* logits
                                 int32_t* argmax, int32_t* pos_dev, int max_pos, void* stream) {
     if (!x) return fail(ALV_ERR_ARG, "null pointer");
     return lm_head(w, nullptr, x, logits, vocab, softcap, argmax, pos_dev, max_pos, stream);
+}
+
+extern "C" int alv_lm_head_bf16_addnorm(alv_weight_t w, const uint16_t* resid, const uint16_t* y, const float* w_y,
+                                        int norm_y, float scale, int scale_mode, uint16_t* sum_out, const float* w_x,
+                                        float eps, int hidden, float* logits, int vocab, float softcap,
+                                        int32_t* argmax, int32_t* pos_dev, int max_pos, void* stream) {
+    if (!resid) return fail(ALV_ERR_ARG, "null pointer");
+    if (!w || w->magic != kWeightMagic) return fail(ALV_ERR_HANDLE, "invalid weight handle");
+    if (hidden < 8 || hidden > w->K)
+        return fail(ALV_ERR_ARG, "hidden=%d outside [8, the head's K=%d]", hidden, w->K);
+    ResidStep st;
+    st.resid = resid;
+    st.y = y;
+    st.w_y = w_y;
+    st.norm_y = norm_y;
+    st.scale = scale;
+    st.scale_mode = scale_mode;
+    st.sum_out = sum_out;
+    st.w_x = w_x;
+    st.eps = eps;
+    st.k = hidden;
+    return lm_head(w, nullptr, y ? y : resid, logits, vocab, softcap, argmax, pos_dev, max_pos, stream, &st);
 }

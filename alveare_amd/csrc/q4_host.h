@@ -71,6 +71,7 @@ struct SplitBuf {
 // workgroups compute the activation x = bf16(rmsnorm(s) [* w_x]) themselves
 // from s = resid_step(y, resid) (row_norm.h), workgroup 0 also writing s to
 // sum_out, so the separate alv_add_norm launch and its output round trip go.
+// y null: no step, s = resid (the input norm alone; sum_out is not written).
 struct ResidStep {
     const uint16_t* resid = nullptr;
     const uint16_t* y = nullptr;
@@ -81,6 +82,7 @@ struct ResidStep {
     uint16_t* sum_out = nullptr;
     const float* w_x = nullptr;  // null: the activation's norm has no weight
     float eps = 1e-6f;
+    int k = 0;  // width of resid / y / sum_out / w_x (0: the matmul's K); activation values past it are zeros
 };
 // Widest row a fused residual step takes (one octet per thread of the
 // 1024-thread workgroup, the float row in LDS).

@@ -291,7 +291,7 @@ extern "C" int alv_gemv_bf16_addnorm(alv_weight_t w, const uint16_t* resid, cons
     st.eps = eps;
     GemvLaunch L;
     weight_launch(w, L);
-    L.Xb = y;
+    L.Xb = y ? y : resid;
     L.ldx = w->K;
     L.Yb = Y;
     L.ldy = w->N;

@@ -229,7 +229,13 @@ def ffn_fused_bf16(F: FfnWeights, X: torch.Tensor, Y: torch.Tensor | None = None
 
 def _step_args(resid, y, K, w_y, norm_y, scale, scale_mode, sum_out, w_x, eps, dev):
     _bf16(resid, "resid", K)
+    if y is None:  # no residual step: the activation is the norm of resid
+        w_x = _f32(w_x, "w_x", K, dev)
+        return (resid.data_ptr(), None, None, 0, ctypes.c_float(1.0), 0, None, _ptr(w_x),
+                ctypes.c_float(eps)), (w_x,)
     _bf16(y, "y", K)
+    if sum_out is None:
+        raise ValueError("a residual step needs sum_out")
     _bf16(sum_out, "sum_out", K)
     if sum_out.data_ptr() in (resid.data_ptr(), y.data_ptr()):
         raise ValueError("sum_out must not alias resid or y")
@@ -239,19 +245,56 @@ def _step_args(resid, y, K, w_y, norm_y, scale, scale_mode, sum_out, w_x, eps, d
             sum_out.data_ptr(), _ptr(w_x), ctypes.c_float(eps)), (w_y, w_x)
 
 
-def gemv_bf16_addnorm(W: Q4Weight, resid: torch.Tensor, y: torch.Tensor, *, sum_out: torch.Tensor, w_y=None,
-                      norm_y: bool = True, scale: float = 1.0, scale_mode: int = 0, w_x=None, eps: float = _GEMMA_EPS,
+def gemv_bf16_addnorm(W: Q4Weight, resid: torch.Tensor, y: torch.Tensor | None, *,
+                      sum_out: torch.Tensor | None = None, w_y=None, norm_y: bool = True, scale: float = 1.0,
+                      scale_mode: int = 0, w_x=None, eps: float = _GEMMA_EPS,
                       Y: torch.Tensor | None = None) -> torch.Tensor:
     """add_norm(resid, y, ...) of one row (sum_out = s) and Y = gemv_bf16(W,
     rmsnorm(s) * w_x) in one launch: the matmul's workgroups compute the
-    normalised activation themselves, bit for bit as the two calls do."""
+    normalised activation themselves, bit for bit as the two calls do.
+    y None: no residual step, Y = gemv_bf16(W, rmsnorm(resid) * w_x) (the
+    first layer's input norm inside its QKV launch)."""
     args, keep = _step_args(resid, y, W.K, w_y, norm_y, scale, scale_mode, sum_out, w_x, eps, W.device)
     if Y is None:
         Y = torch.empty(W.N, dtype=torch.bfloat16, device=W.device)
     _bf16(Y, "Y", W.N)
     with torch.cuda.device(W.device):
-        check(lib().alv_gemv_bf16_addnorm(W.handle, *args, Y.data_ptr(), _stream(y)), "alv_gemv_bf16_addnorm")
+        check(lib().alv_gemv_bf16_addnorm(W.handle, *args, Y.data_ptr(), _stream(resid)), "alv_gemv_bf16_addnorm")
     return Y
+
+
+def lm_head_addnorm(W: Q4Weight, resid: torch.Tensor, y: torch.Tensor | None, *, hidden: int,
+                    sum_out: torch.Tensor | None = None, w_y=None, norm_y: bool = True, scale: float = 1.0,
+                    scale_mode: int = 0, w_x=None, eps: float = _GEMMA_EPS, vocab: int | None = None,
+                    softcap: float = 30.0, logits: torch.Tensor | None = None, token: torch.Tensor | None = None,
+                    pos: torch.Tensor | None = None, max_pos: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+    """add_norm(resid, y, ..., w_out=w_x, pad=W.K) of one `hidden`-wide row
+    and lm_head on its bf16 norm in the head GEMV's launch
+    (alv_lm_head_bf16_addnorm): the same sum_out, logits and token bits as
+    the two calls. y None: the head on rmsnorm(resid) * w_x."""
+    if not isinstance(W, Q4Weight):
+        raise TypeError("W must be a registered Q4Weight")
+    if not 8 <= hidden <= W.K or hidden % 8:
+        raise ValueError(f"hidden={hidden}: a multiple of 8 in [8, {W.K}]")
+    args, keep = _step_args(resid, y, hidden, w_y, norm_y, scale, scale_mode, sum_out, w_x, eps, W.device)
+    vocab = W.N if vocab is None else int(vocab)
+    if logits is None:
+        logits = torch.empty(vocab, dtype=torch.float32, device=W.device)
+    if logits.dtype != torch.float32 or not logits.is_contiguous() or logits.device != W.device:
+        raise TypeError("logits must be a contiguous float32 tensor on the weights' device")
+    if logits.numel() < vocab:
+        raise ValueError(f"logits holds {logits.numel()} values, vocab is {vocab}")
+    if token is None:
+        token = torch.empty(1, dtype=torch.int32, device=W.device)
+    if token.dtype != torch.int32 or token.device != W.device:
+        raise TypeError("token must be an int32 tensor on the weights' device")
+    if pos is not None and (pos.dtype != torch.int32 or pos.device != W.device or pos.numel() < 1):
+        raise TypeError("pos must be an int32 tensor on the weights' device")
+    with torch.cuda.device(W.device):
+        check(lib().alv_lm_head_bf16_addnorm(W.handle, *args, int(hidden), logits.data_ptr(), vocab, float(softcap),
+                                             token.data_ptr(), pos.data_ptr() if pos is not None else None,
+                                             int(max_pos), _stream(resid)), "alv_lm_head_bf16_addnorm")
+    return logits, token
 
 
 def ffn_fused_bf16_addnorm(F: FfnWeights, resid: torch.Tensor, y: torch.Tensor, *, sum_out: torch.Tensor, w_y=None,
@@ -265,7 +308,7 @@ def ffn_fused_bf16_addnorm(F: FfnWeights, resid: torch.Tensor, y: torch.Tensor, 
         Y = torch.empty(F.H, dtype=torch.bfloat16, device=F.device)
     _bf16(Y, "Y", F.H)
     with torch.cuda.device(F.device):
-        check(lib().alv_ffn_fused_bf16_addnorm(F.handle, *args, Y.data_ptr(), _stream(y)),
+        check(lib().alv_ffn_fused_bf16_addnorm(F.handle, *args, Y.data_ptr(), _stream(resid)),
               "alv_ffn_fused_bf16_addnorm")
     return Y
 
@@ -364,7 +407,7 @@ class Gemma4DecodeLayer:
         self.y = torch.empty(H, **bf)
 
     def enqueue(self, x: torch.Tensor, normed: bool = False, next_norm=None, step_in: dict | None = None,
-                defer: bool = False):
+                defer: bool = False, norm_in_qkv: bool = False):
         """The layer's launches for the position already in ``pos_dev``.
         ``normed``: ``x_norm`` already holds the input norm (written by the
         previous layer's last launch). ``next_norm`` = (weights, out, pad): the
@@ -373,15 +416,19 @@ class Gemma4DecodeLayer:
         ``defer`` result), run inside this layer's QKV launch, which computes
         the input norm itself (``x`` is that step's sum_out). ``defer``: leave
         this layer's last residual step to the next layer's QKV launch and
-        return (y, step) instead of y. With ``fuse`` the q/k/v norms, RoPE and
-        cache insert run inside the attention launch, and the post-attention
-        step inside the FFN's gate/up launch (``x_norm2`` is then not
-        written)."""
+        return (y, step) instead of y. ``norm_in_qkv`` (without ``step_in``
+        or ``normed``): the QKV launch computes the input norm of ``x``
+        itself (``x_norm`` is then not written). With ``fuse`` the q/k/v
+        norms, RoPE and cache insert run inside the attention launch, and the
+        post-attention step inside the FFN's gate/up launch (``x_norm2`` is
+        then not written)."""
         H, n = self.H, self.norms
         if step_in is not None:
             gemv_bf16_addnorm(self.w_qkv, step_in["resid"], step_in["y"], sum_out=step_in["sum_out"],
                               w_y=step_in["w_y"], scale=step_in["scale"], scale_mode=step_in["scale_mode"],
                               w_x=n["attn"], Y=self.qkv_out)
+        elif norm_in_qkv and not normed:
+            gemv_bf16_addnorm(self.w_qkv, x, None, w_x=n["attn"], Y=self.qkv_out)
         else:
             if not normed:
                 rmsnorm(x, n["attn"], K=H, out=self.x_norm)
@@ -629,24 +676,33 @@ class Gemma4Decoder:
         embed(self.table, self.token_dev, self.scale, out=self.x)
         h = self.x
         n = len(self.layers)
-        # fuse: each layer's last residual step runs inside the next layer's QKV
-        # launch (which computes its input norm itself); the last layer's
-        # writes the final norm, zero-padded to the head's K. Unfused: each
-        # layer's last launch writes the next layer's input norm.
+        # fuse: the first layer's QKV launch computes its input norm itself,
+        # each layer's last residual step runs inside the next layer's QKV
+        # launch (which computes its input norm too), and the last layer's
+        # inside the head's GEMV launch with the final norm, zero-padded to
+        # the head's K (x_norm is then not written). Unfused: each layer's
+        # last launch writes the next layer's input norm, the last layer's
+        # the final norm.
         step = None
         for i, L in enumerate(self.layers):
             nxt = self.layers[i + 1] if i + 1 < n else None
-            if self.fuse and nxt is not None:
-                h, step = L.enqueue(h, normed=i > 0 and step is None, step_in=step, defer=True)
+            if self.fuse:
+                h, step = L.enqueue(h, step_in=step, defer=True, norm_in_qkv=i == 0)
                 continue
             next_norm = ((nxt.norms["attn"], nxt.x_norm, self.H) if nxt is not None
                          else (self.final_norm, self.x_norm, self.head.K))
             h = L.enqueue(h, normed=i > 0 and step is None, next_norm=next_norm, step_in=step)
             step = None
-        if n == 0:
-            rmsnorm(h, self.final_norm, K=self.H, pad=self.head.K, out=self.x_norm)
         # The head on the bf16 final norm; its last launch also writes token -1
         # past the caches and advances pos_dev.
+        if step is not None:
+            lm_head_addnorm(self.head, step["resid"], step["y"], hidden=self.H, sum_out=step["sum_out"],
+                            w_y=step["w_y"], scale=step["scale"], scale_mode=step["scale_mode"], w_x=self.final_norm,
+                            vocab=self.vocab, softcap=self.softcap, logits=self.logits, token=self.token_dev,
+                            pos=self.pos_dev, max_pos=self.max_pos)
+            return
+        if n == 0:
+            rmsnorm(h, self.final_norm, K=self.H, pad=self.head.K, out=self.x_norm)
         lm_head(self.head, self.x_norm, self.vocab, self.softcap, self.logits, token=self.token_dev,
                 pos=self.pos_dev, max_pos=self.max_pos)
 

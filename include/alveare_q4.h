@@ -163,6 +163,21 @@ int alv_lm_head_bf16(alv_weight_t w, const uint16_t* x, float* logits, int vocab
                      int32_t* pos_dev, int max_pos, void* stream);
 
 /*
+ * alv_lm_head_bf16 on the final norm of the last layer's residual step, the
+ * step inside the head GEMV's launch (as alv_gemv_bf16_addnorm): s =
+ * resid_step(y, resid) -> sum_out, x = bf16(rmsnorm(s) * w_x) over the
+ * first `hidden` values, zero-padded to the head's K -- the same bits as
+ * alv_add_norm (pad = K) followed by alv_lm_head_bf16 on its norm_out
+ * (runtime/py/model.py:783-788, then :907-916 with the final norm;
+ * model.cpp:409-420 and generator.cpp:28-52). hidden <= K, a multiple of 8
+ * up to 8192; y may be NULL (no step: x is the norm of resid itself).
+ */
+int alv_lm_head_bf16_addnorm(alv_weight_t w, const uint16_t* resid, const uint16_t* y, const float* w_y, int norm_y,
+                             float scale, int scale_mode, uint16_t* sum_out, const float* w_x, float eps, int hidden,
+                             float* logits, int vocab, float softcap, int32_t* argmax, int32_t* pos_dev, int max_pos,
+                             void* stream);
+
+/*
  * Quantize float32 weights to the Q4 combined layout on the GPU:
  * quantize_to_q4_0 + pack_to_combined (tools/convert/gemv_q_convert.py:5-85)
  * with the zero padding of quantize_and_pack_tensor
@@ -366,7 +381,9 @@ int alv_add_norm(const uint16_t* resid, int ldr, const uint16_t* y, int ldy, con
  * (runtime/py/model.py:775-788 then :797-806; model.cpp:409-420 then the FFN)
  * and from the FFN into the next layer's QKV (:783-788 then :705-713).
  * K = the weight's K (the FFN's H), a multiple of 8 up to 8192; rows and
- * weights 16-byte aligned; sum_out must not alias resid or y.
+ * weights 16-byte aligned; sum_out must not alias resid or y. y NULL: no
+ * residual step, the activation is bf16(rmsnorm(resid) * w_x) as alv_rmsnorm
+ * writes it (a first layer's input norm) and sum_out is not written.
  */
 int alv_gemv_bf16_addnorm(alv_weight_t w, const uint16_t* resid, const uint16_t* y, const float* w_y, int norm_y,
                           float scale, int scale_mode, uint16_t* sum_out, const float* w_x, float eps, uint16_t* Y,

@@ -111,13 +111,15 @@ def traffic(fetch_dir: str, write_dir: str, copy_bytes: int) -> str:
 def decode(d: str) -> str:
     """Median duration of each op of the decode step, the launches named by
     their order: the streaming GEMV with a fused residual step is the QKV or
-    the gate/up launch (its instance: GLU or not); without one, with 256
-    workgroups it is the LM head after the final residual step (or layer 0's
-    QKV after the input norm), with 240 workgroups O after the attention
+    the gate/up launch (its instance: GLU or not), layer 0's QKV with the
+    input norm when it follows the embedding, the LM head with the final
+    residual step and norm when head_kernel follows it; without one, with
+    256 workgroups it is the LM head after the final residual step (or layer
+    0's QKV after the input norm), with 240 workgroups O after the attention
     merge or FFN down after the gate/up launch."""
     with open(_find(d, "kernel_trace.csv")) as f:
         rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
-    out = defaultdict(list)
+    seq = []  # (tag, us) in launch order
     prev = None
     for r in rows:
         n = r["Kernel_Name"]
@@ -138,15 +140,23 @@ def decode(d: str) -> str:
         elif "rmsnorm_kernel" in n:
             tag = "layer-0 input norm"
         elif "q4_gemv1_step_kernel" in n:
-            tag = "gate/up + residual step" if "true, true, 1," in n else "QKV + residual step"
+            if "true, true, 1," in n:
+                tag = "gate/up + residual step"
+            else:
+                tag = "QKV, layer 0 + input norm" if prev == "embedding" else "QKV + residual step"
         elif "q4_gemv1_kernel" in n and wg == 240:
             tag = "FFN down" if prev == "gate/up + residual step" else "O"
         elif "q4_gemv1_kernel" in n:
             tag = "LM-head GEMV" if prev == "final residual step + norm" else "QKV, layer 0"
         else:
             continue
-        out[tag].append(us)
+        if tag == "head softcap/argmax" and seq and seq[-1][0] == "QKV + residual step":
+            seq[-1] = ("LM-head GEMV + final residual step + norm", seq[-1][1])
+        seq.append((tag, us))
         prev = tag
+    out = defaultdict(list)
+    for tag, us in seq:
+        out[tag].append(us)
     lines = ["op | launches | median us | mean us"]
     for tag, v in out.items():
         lines.append(f"{tag} | {len(v)} | {statistics.median(v):.2f} | {statistics.mean(v):.2f}")

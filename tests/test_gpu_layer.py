@@ -484,7 +484,11 @@ def test_gemma4_decoder_step_and_graph(orc, dev):
     token entirely on the device: the embedding and final norm bit-exact, the
     head's bf16 logits within the GEMV bound, the token their np.argmax; a
     captured step replayed from the same state gives the eager steps' logits
-    and tokens bit for bit."""
+    and tokens bit for bit. The head is 64 columns wider than the hidden size
+    (the reference pads Gemma-4's K to 4096): the fused decoder computes the
+    final norm inside the head's launch, zero-padded, and the first layer's
+    input norm inside its QKV launch, with every bit of the unfused
+    decoder's launches."""
     import math
 
     import alveare_amd as aa
@@ -505,8 +509,9 @@ def test_gemma4_decoder_step_and_graph(orc, dev):
             scale=0.7, sliding=sliding, H=H, I=I, max_seq=S, device=dev, pos_dev=pos_dev))
     table_np = rng.normal(0, 0.05, (V, H)).astype(np.float16)
     fnorm = rng.uniform(0.5, 1.5, H).astype(np.float32)
-    Wh = orc.synth_q4(V, H, 408)
-    head = aa.Q4Weight(torch.from_numpy(Wh).to(dev), V, H)
+    KH = H + 64
+    Wh = orc.synth_q4(V, KH, 408)
+    head = aa.Q4Weight(torch.from_numpy(Wh).to(dev), V, KH)
     dec = layer.Gemma4Decoder(layers, torch.from_numpy(table_np).to(dev), fnorm, head, V, softcap=0.0)
     # The same layers unfused (separate residual-step launches): the fused
     # step must give every bit the unfused one gives.
@@ -533,6 +538,9 @@ def test_gemma4_decoder_step_and_graph(orc, dev):
     for step in range(4):
         tok = ref.step()
         torch.cuda.synchronize()
+        xn = bf_np(ref.x_norm)
+        assert np.array_equal(xn[:H], qn.rmsnorm_cpu(bf_np(layers[-1].y), fnorm))
+        assert not xn[H:].any()
         unfused.append((ref.logits.cpu().numpy().copy(), tok, [bf_np(L.y).copy() for L in layers]))
     for L in layers:
         L.fuse = True
@@ -550,10 +558,11 @@ def test_gemma4_decoder_step_and_graph(orc, dev):
             assert np.array_equal(bf_np(L.y), y_ref)
         x = (table_np[tok_in].astype(np.float32) * np.sqrt(H)).astype(np.float32)
         assert np.array_equal(bf_np(dec.x), qn.bf16_rne(x))
-        xn = bf_np(dec.x_norm)
-        assert np.array_equal(xn[:H], qn.rmsnorm_cpu(bf_np(layers[-1].y), fnorm))
+        # The final norm the head's launch computed (zero past H).
+        xn = np.zeros(KH, np.float32)
+        xn[:H] = qn.rmsnorm_cpu(bf_np(layers[-1].y), fnorm)
         logits = dec.logits.cpu().numpy()
-        parity.gemv_bf16_check(orc, Wh, xn, parity.f32_bits_bf16(logits), V, H)
+        parity.gemv_bf16_check(orc, Wh, xn, parity.f32_bits_bf16(logits), V, KH)
         assert tok == int(np.argmax(logits))
         eager.append((logits.copy(), tok))
     reset()
@@ -569,6 +578,68 @@ def test_gemma4_decoder_step_and_graph(orc, dev):
     del g
     for L in layers:
         L.close()
+    head.close()
+
+
+@pytest.mark.parametrize("H,KH,softcap", [(3840, 4096, 30.0), (512, 512, 0.0), (992, 1024, 30.0)])
+def test_fused_input_and_final_norms(orc, dev, H, KH, softcap):
+    """The norms a decode step folds into its matmul launches give the bits
+    of the separate launches: the first layer's input norm inside its QKV
+    launch (alv_gemv_bf16_addnorm without y) against alv_rmsnorm then
+    alv_gemv_bf16; the last residual step and the final norm inside the LM
+    head's launch (alv_lm_head_bf16_addnorm, rows H wide on a head K wide,
+    the norm zero-padded) against alv_add_norm(pad = K) then
+    alv_lm_head_bf16 -- sum_out, logits and token -- and the head on the
+    norm of a row alone (no y) against alv_rmsnorm(pad = K) then the head."""
+    import alveare_amd as aa
+    from alveare_amd import layer
+
+    _say(f"fused input/final norms H={H} KH={KH} softcap={softcap}")
+    rng = np.random.default_rng(600 + H)
+    V, NQ = 3000, 384
+    Wq = aa.Q4Weight(torch.from_numpy(orc.synth_q4(NQ, H, 601)).to(dev), NQ, H)
+    head = aa.Q4Weight(torch.from_numpy(orc.synth_q4(V, KH, 602)).to(dev), V, KH)
+    resid = bf_dev(rnd_bf16(rng, H, 2.0), dev)
+    y = bf_dev(rnd_bf16(rng, H, 0.5), dev)
+    w_x = rng.uniform(0.5, 1.5, H).astype(np.float32)
+    w_y = rng.uniform(0.5, 1.5, H).astype(np.float32)
+
+    # Input norm inside the QKV launch.
+    xn = layer.rmsnorm(resid, w_x, K=H)
+    ref_q = layer.gemv_bf16(Wq, xn)
+    got_q = layer.gemv_bf16_addnorm(Wq, resid, None, w_x=w_x)
+    torch.cuda.synchronize()
+    assert torch.equal(got_q.view(torch.int16), ref_q.view(torch.int16))
+    parity.gemv_bf16_check(orc, orc.synth_q4(NQ, H, 601), bf_np(xn), parity.bf16_bits(got_q), NQ, H)
+
+    # Last residual step + final norm inside the head's launch.
+    s_ref, n_ref = layer.add_norm(resid, y, K=H, w_y=w_y, scale=0.7, scale_mode=1, w_out=w_x, norm_out=True,
+                                  pad=KH)
+    lg_ref, tok_ref = aa.lm_head(head, n_ref, V, softcap)
+    lg_ref, tok_ref = lg_ref.clone(), tok_ref.clone()
+    s_got = torch.empty(H, dtype=torch.bfloat16, device=dev)
+    lg, tok = layer.lm_head_addnorm(head, resid, y, hidden=H, sum_out=s_got, w_y=w_y, scale=0.7, scale_mode=1,
+                                    w_x=w_x, vocab=V, softcap=softcap)
+    torch.cuda.synchronize()
+    assert torch.equal(s_got.view(torch.int16), s_ref.view(torch.int16))
+    assert torch.equal(lg.view(torch.int32), lg_ref.view(torch.int32))
+    assert int(tok.item()) == int(tok_ref.item())
+    assert not bf_np(n_ref)[H:].any()
+
+    # The head on the norm of a row alone.
+    n2 = layer.rmsnorm(resid, w_x, K=H, pad=KH)
+    lg2_ref, tok2_ref = aa.lm_head(head, n2, V, softcap)
+    lg2_ref, tok2_ref = lg2_ref.clone(), tok2_ref.clone()
+    lg2, tok2 = layer.lm_head_addnorm(head, resid, None, hidden=H, w_x=w_x, vocab=V, softcap=softcap)
+    torch.cuda.synchronize()
+    assert torch.equal(lg2.view(torch.int32), lg2_ref.view(torch.int32))
+    assert int(tok2.item()) == int(tok2_ref.item())
+
+    with pytest.raises(ValueError):
+        layer.lm_head_addnorm(head, resid, None, hidden=KH + 8, w_x=w_x)
+    with pytest.raises(ValueError):
+        layer.lm_head_addnorm(head, resid, y, hidden=H, w_x=w_x)  # a step needs sum_out
+    Wq.close()
     head.close()
 
 
