@@ -789,6 +789,41 @@ def test_lm_head_bf16_and_position(orc, dev):
     w.close()
 
 
+def test_lm_head_fold_group_counts(orc, dev):
+    """The token fold at every grid size the head takes (1 to 256
+    workgroups of logits), calls back to back on one stream: the token is
+    the np.argmax of the logits the call wrote, a tie of the largest logit
+    across workgroups (the lower index wins) and a NaN included."""
+    import alveare_amd as aa
+
+    N, K = 20000, 256
+    seed = orc.seed_for(6, 3)
+    W = orc.synth_q4(N, K, seed).reshape(N, K // 32 * 20)
+    w0 = aa.Q4Weight(to_dev(W, dev), N, K)
+    x = to_dev(orc.bf16_round(orc.synth_normal(K, seed + 1)), dev)
+    r = int(aa.lm_head(w0, x, N, 30.0)[1].item())
+    w0.close()
+    j = (r + 9000) % N
+    W[j] = W[r]  # the largest logit twice, in workgroups far apart: the lower index wins
+    w = aa.Q4Weight(to_dev(W, dev), N, K)
+    for vocab in (1, 2, 63, 64, 65, 1000, 12346, 16383, 16385, 20000, 7, 20000):
+        for softcap in (30.0, 0.0):
+            logits, tok = aa.lm_head(w, x, vocab, softcap)
+            lg = logits.cpu().numpy()
+            assert int(tok.item()) == int(np.argmax(lg)), (vocab, softcap)
+            if vocab == N:
+                assert int(tok.item()) == min(r, j)
+    Wn = W.copy()
+    Wn[15000, 16:18] = [0xC0, 0x7F]  # NaN scale: a NaN logit outranks every value
+    wn = aa.Q4Weight(to_dev(Wn, dev), N, K)
+    _, tok = aa.lm_head(wn, x, 20000, 30.0)
+    assert int(tok.item()) == 15000
+    _, tok = aa.lm_head(wn, x, 15000, 30.0)  # the NaN row past the vocabulary
+    assert int(tok.item()) == int(np.argmax(aa.lm_head(w, x, 15000, 30.0)[0].cpu().numpy()))
+    w.close()
+    wn.close()
+
+
 def test_lm_head_full_vocab(orc, dev):
     """The reference's head shape: 262144 x 4096 (671 MB of Q4 weights, the
     largest GEMV of a decode step), softcap 30, whole vocabulary; then through
