@@ -35,6 +35,7 @@ SIGNATURES: dict[str, tuple] = {
     "alv_ffn_fused_noalloc": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "alv_ffn_activation": (_i, [_vp, _vp, _i, _vp]),
     "alv_ffn_gate_up": (_i, [_vp, _vp, _i, _i, _vp]),
+    "alv_ffn_partials": (_i, [_vp, _vp, _vp, _vp, _vp]),
     "alv_ffn_shape": (_i, [_vp, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "alv_ffn_exec_shape": (_i, [_vp, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "alv_ffn_release": (None, [_vp]),

@@ -15,6 +15,7 @@
 // Prefill (from 17 bf16 / 33 fp32 tokens): the same two steps with the MFMA
 // tiled kernel (gemm_q.hip);
 // the M x I activation lives in the stream's prefill scratch (q4_host.h).
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -29,6 +30,36 @@ namespace {
 int check_handle(alv_ffn_t w) {
     if (!w || w->magic != alv::kFfnMagic) return alv::fail(ALV_ERR_HANDLE, "invalid FFN handle");
     return ALV_OK;
+}
+
+// Down slices of the one-token FFN launch (gemv1_q.hip, q4_ffn1_kernel): a
+// combined-layout matrix of G U 16 rows x 16 blocks whose row (u G + b) 16 + j
+// holds, as block vb, the block (row 128 u + 16 (vb >> 1) + j, column block
+// b + G (vb & 1)) of Wd (rows rs bytes apart). A byte permutation, like the
+// reference's own FFN repack (runtime/cpp/src/weights.cpp:94-190).
+__global__ void __launch_bounds__(256) ffn1_vdown_kernel(const uint8_t* Wd, uint32_t rs, int G, int U, uint32_t* out) {
+    const int64_t total = (int64_t)G * U * 16 * 16 * 5;  // dwords: 16 blocks of 5 per virtual row
+    for (int64_t d = (int64_t)blockIdx.x * 256 + threadIdx.x; d < total; d += (int64_t)gridDim.x * 256) {
+        const int64_t blk = d / 5;
+        const int e = (int)(d - blk * 5);
+        const int vb = (int)(blk & 15);
+        const int64_t vr = blk >> 4;
+        const int j = (int)(vr & 15);
+        const int64_t ub = vr >> 4;  // unit-major: tile u G + b
+        const int b = (int)(ub % G), u = (int)(ub / G);
+        const int row = 128 * u + 16 * (vb >> 1) + j;
+        const int cb = b + G * (vb & 1);
+        out[d] = *reinterpret_cast<const uint32_t*>(Wd + (size_t)row * rs + (size_t)cb * alv::kBlockBytes + 4 * e);
+    }
+}
+
+// Whether one-token calls take the one-launch FFN (when the handle has it):
+// the environment variable ALV_FFN_ONE (0 / 1), read at each call, overrides
+// the default (on).
+bool ffn1_on() {
+    const char* e = getenv("ALV_FFN_ONE");
+    if (e && *e) return atoi(e) != 0;
+    return true;
 }
 
 }  // namespace
@@ -116,10 +147,31 @@ extern "C" int alv_ffn_register(const uint8_t* Wg, const uint8_t* Wu, const uint
     if (!rc) rc = hip_check(hipMalloc(&h->a, h->a_cap * sizeof(uint16_t)), "hipMalloc(FFN activation)");
     if (!rc) rc = hip_check(hipMemsetAsync(h->a, 0, h->a_cap * sizeof(uint16_t), s), "hipMemsetAsync(FFN activation)");
     h->last_a = h->a;
+    // The one-token launch takes 64 intermediate rows per workgroup and down
+    // units of 128 rows: Ie a multiple of 64, He of 128.
+    uint8_t* vtmp = nullptr;
+    if (!rc && h->Ie % 64 == 0 && h->He % 128 == 0 && h->He > 512 && h->Ie / 64 <= 256) {
+        h->G1 = h->Ie / 64;
+        h->U1 = h->He / 128;
+        const int nv = h->G1 * h->U1 * 16;
+        h->vdown_bytes = tile_bytes(nv, 512);
+        rc = hip_check(hipMalloc(&vtmp, (size_t)nv * 16 * kBlockBytes), "hipMalloc(FFN down slices, staging)");
+        if (!rc) rc = hip_check(hipMalloc(&h->vdown, h->vdown_bytes), "hipMalloc(FFN down slices)");
+        if (!rc) rc = hip_check(hipMalloc(&h->part1, (size_t)h->G1 * h->He * sizeof(float)), "hipMalloc(FFN partials)");
+        if (!rc) {
+            hipLaunchKernelGGL(ffn1_vdown_kernel, dim3(4096), dim3(256), 0, s, Wd, rs_i, h->G1, h->U1,
+                               reinterpret_cast<uint32_t*>(vtmp));
+            rc = hip_check(hipGetLastError(), "ffn1_vdown_kernel launch");
+        }
+        if (!rc) rc = launch_tile(vtmp, h->vdown, nv, 512, s, 16 * kBlockBytes);
+    }
     if (!rc) rc = hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    if (vtmp) (void)hipFree(vtmp);
     if (rc) {
         if (h->w) (void)hipFree(h->w);
         if (h->a) (void)hipFree(h->a);
+        if (h->vdown) (void)hipFree(h->vdown);
+        if (h->part1) (void)hipFree(h->part1);
         h->magic = 0;
         delete h;
         return rc;
@@ -166,6 +218,15 @@ extern "C" int alv_ffn_fused(alv_ffn_t w, const float* X, float* Y, int M, int l
         w->a_rows = M;
         return ALV_OK;
     }
+    if (M == 1 && w->vdown && ffn1_on()) {
+        GemvLaunch op[2];
+        ffn_ops(w, w->a, X, ldx, Y, ldy, 1, op);
+        if (int rc = launch_ffn1(op[0], w->vdown, w->vdown_bytes, w->part1, w->a, w->G1, w->U1, w->H, Y, nullptr, s))
+            return rc;
+        w->last_a = w->a;
+        w->a_rows = 1;
+        return ALV_OK;
+    }
     for (int m0 = 0; m0 < M; m0 += kGemvMaxM) {
         const int mc = std::min(kGemvMaxM, M - m0);
         GemvLaunch op[2];
@@ -207,6 +268,16 @@ extern "C" int alv_ffn_fused_bf16(alv_ffn_t w, const uint16_t* X, uint16_t* Y, i
         if (int rc = launch_gemm_tiled(op[1], s)) return rc;
         w->last_a = static_cast<uint16_t*>(act);
         w->a_rows = M;
+        return ALV_OK;
+    }
+    if (M == 1 && w->vdown && ffn1_on()) {
+        GemvLaunch op[2];
+        ffn_ops(w, w->a, nullptr, ldx, nullptr, ldy, 1, op);
+        bf16_ends(op, X, Y);
+        if (int rc = launch_ffn1(op[0], w->vdown, w->vdown_bytes, w->part1, w->a, w->G1, w->U1, w->H, nullptr, Y, s))
+            return rc;
+        w->last_a = w->a;
+        w->a_rows = 1;
         return ALV_OK;
     }
     for (int m0 = 0; m0 < M; m0 += kGemvMaxM) {
@@ -293,6 +364,13 @@ extern "C" int alv_ffn_fused_bf16_addnorm(alv_ffn_t w, const uint16_t* resid, co
     op[0].step = &st;
     op[1].Y = nullptr;
     op[1].Yb = Y;
+    if (w->vdown && ffn1_on()) {
+        if (int rc = launch_ffn1(op[0], w->vdown, w->vdown_bytes, w->part1, w->a, w->G1, w->U1, w->H, nullptr, Y, s))
+            return rc;
+        w->last_a = w->a;
+        w->a_rows = 1;
+        return ALV_OK;
+    }
     if (int rc = launch_gemv(op[0], s)) return rc;
     if (int rc = launch_gemv(op[1], s)) return rc;
     w->last_a = w->a;
@@ -348,6 +426,28 @@ extern "C" int alv_ffn_gate_up(alv_ffn_t w, const float* X, int M, int ldx, void
     return ALV_OK;
 }
 
+extern "C" int alv_ffn_partials(alv_ffn_t w, const float* X, float* P, int* slices, void* stream) {
+    if (int rc = check_handle(w)) return rc;
+    if (!X) return fail(ALV_ERR_ARG, "null activation pointer");
+    if (reinterpret_cast<uintptr_t>(X) % 4 || reinterpret_cast<uintptr_t>(P) % 4)
+        return fail(ALV_ERR_ALIGN, "X and P need 4-byte alignment");
+    if (!w->vdown)
+        return fail(ALV_ERR_ARG, "this FFN (H=%d I=%d executed as %d x %d) has no one-launch form: it needs the "
+                    "executed I a multiple of 64 up to 16384 and H a multiple of 128 above 512", w->H, w->I, w->He, w->Ie);
+    int dev = -1;
+    if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+    if (dev != w->device) return fail(ALV_ERR_HANDLE, "FFN handle belongs to device %d, current device is %d", w->device, dev);
+    if (slices) *slices = w->G1;
+    GemvLaunch op[2];
+    ffn_ops(w, w->a, X, w->H, nullptr, w->H, 1, op);
+    if (int rc = launch_ffn1(op[0], w->vdown, w->vdown_bytes, P ? P : w->part1, w->a, w->G1, w->U1, w->H, nullptr,
+                             nullptr, (hipStream_t)stream, false))
+        return rc;
+    w->last_a = w->a;
+    w->a_rows = 1;
+    return ALV_OK;
+}
+
 namespace {
 
 __global__ void __launch_bounds__(256) bf16_to_f32_kernel(const uint16_t* in, float* out, int64_t n) {
@@ -375,6 +475,8 @@ extern "C" void alv_ffn_release(alv_ffn_t w) {
     (void)hipDeviceSynchronize();
     if (w->w) (void)hipFree(w->w);
     if (w->a) (void)hipFree(w->a);
+    if (w->vdown) (void)hipFree(w->vdown);
+    if (w->part1) (void)hipFree(w->part1);
     if (cur >= 0 && cur != w->device) (void)hipSetDevice(cur);
     w->magic = 0;
     delete w;

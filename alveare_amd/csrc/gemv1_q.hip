@@ -367,9 +367,11 @@ __device__ __forceinline__ void issue_unit(const Gemv1Args& a, const WgWork& wk,
 // read row AR - 1; their D rows are never used). A block past the row's end
 // (the last super-step: the next plane's bytes, or the next row's in the
 // combined layout) gets a zero scale, so its weights are zero.
-template <int R, bool GLU, int MT, bool TB, bool TL>
-__device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& wk, const u32x4 (&q)[5], int u,
-                                             const __bf16* xs, f32x4* part, int lane) {
+// Unit u of super-step ss (nb: 32-column blocks of the matrix; s0: the
+// workgroup's first super-step, whose activations sit first in xs).
+template <int R, bool GLU, int MT, bool TB>
+__device__ __forceinline__ void compute_unit_ss(int nb, int ss, int s0, const u32x4 (&q)[5], int u, const __bf16* xs,
+                                                f32x4* part, int lane) {
     using Ph = PhaseT<R, false, GLU, MT, TB>;
     constexpr int SR = Ph::SR, AR = Ph::AR, DL = Ph::DL, RM = Ph::RM;
     constexpr bool QUAD = Ph::QUAD;
@@ -377,9 +379,8 @@ __device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& w
     constexpr int ND = QUAD ? NB : 1;                 // D tiles
     const int j = lane & 15;
     const int g = lane >> 4;
-    const UnitPos p = unit_pos<Ph::NT, TL>(a, wk, u);
-    const int kb0 = p.ss * 16 + g * 4;
-    const __bf16* xu = xs + (size_t)g * SR * 8 + (size_t)(p.ss - wk.s0) * 16 * 4 * SR * 8;
+    const int kb0 = ss * 16 + g * 4;
+    const __bf16* xu = xs + (size_t)g * SR * 8 + (size_t)(ss - s0) * 16 * 4 * SR * 8;
     // This lane's A row in each block (rows >= AR read row AR - 1; their D rows
     // are never used; a token quad's fourth row reads the zero row).
     int arow[NB];
@@ -393,7 +394,7 @@ __device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& w
 #pragma unroll
     for (int bl = 0; bl < 4; ++bl) {
         const int w4 = 5 * bl + 4;
-        const uint32_t sd = kb0 + bl < a.nb ? (uint32_t)q[w4 >> 2][w4 & 3] : 0u;
+        const uint32_t sd = kb0 + bl < nb ? (uint32_t)q[w4 >> 2][w4 & 3] : 0u;
         const Scale2 sc = make_scale2(scale_of(sd));
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -421,6 +422,13 @@ __device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& w
     } else {
         if (lane < DL) part[(size_t)u * DL + lane] = t0[0] + t1[0];
     }
+}
+
+template <int R, bool GLU, int MT, bool TB, bool TL>
+__device__ __forceinline__ void compute_unit(const Gemv1Args& a, const WgWork& wk, const u32x4 (&q)[5], int u,
+                                             const __bf16* xs, f32x4* part, int lane) {
+    const UnitPos p = unit_pos<PhaseT<R, false, GLU, MT, TB>::NT, TL>(a, wk, u);
+    compute_unit_ss<R, GLU, MT, TB>(a.nb, p.ss, wk.s0, q, u, xs, part, lane);
 }
 
 __device__ __forceinline__ void ystore(const Gemv1Args& a, int m, int row, float out) {
@@ -743,6 +751,230 @@ __global__ void __launch_bounds__(64 * NW) q4_gemv1_kernel(Gemv1Args a) {
 template <int NW, int P, int R, bool XB, bool GLU, int MT, bool TB, bool TL>
 __global__ void __launch_bounds__(64 * NW) q4_gemv1_step_kernel(Gemv1Args a) {
     gemv1_body<NW, P, R, XB, GLU, MT, TB, TL, true>(a);
+}
+
+// ---- One-token FFN in one launch (q4_ffn1_kernel) ------------------------------------
+// The reference's NPU dataflow (kernels/ffn_fused/ffn_fused.py:28-328: each
+// core owns a slice of the intermediate rows, computes gate, up and the
+// activation for them and multiplies the slice's columns of the down matrix
+// into a partial output; the host sums the partials, runtime/cpp/src/npu.cpp:
+// 360-377), planned for the GPU. Workgroup b owns the 64 intermediate rows of
+// row-tile pairs b and b + G (rows 32 b .. 32 b + 31 and 32 (b + G) .. + 31):
+//   A. the gate/up units of its four row tiles against the staged activation,
+//      then the GLU epilogue of those 64 rows into LDS (bf16 values, the
+//      reference's rounding points) and into the handle's activation buffer;
+//   B. the down units of its slice: the 64 down columns of those rows, from
+//      a registration-time layout (ffn1_vdown_kernel) in which down unit u of
+//      workgroup b (tile u G + b) is an ordinary 16-row x 512-column tile whose block
+//      4 g + bl is the real block (row 128 u + 16 ((4 g + bl) >> 1) + j,
+//      column block b + G ((4 g + bl) & 1)). Its A operand holds eight rows,
+//      one per real row tile: row t carries the slice's activations in the
+//      two blocks of tile t and zeros elsewhere, so D row t of the unit is
+//      the partial output of rows 128 u + 16 t .. + 15 -- the eight-token
+//      bf16 instance of compute_unit as it stands;
+//   C. the 128 U partial outputs to part[b][.], summed over the workgroups
+//      in a fixed order by ffn1_sum_kernel.
+// No workgroup waits for another: the down weights of a slice stream behind
+// its gate/up units in the same ring, and a wave that takes its first down
+// unit issues the loads before the GLU epilogue runs.
+struct Ffn1Args {
+    Gemv1Args gu;       // the gate/up launch at one token (tiled gate W0 and up W1, X, act, nss, nb)
+    const uint8_t* Wv;  // down slices, tiled layout of the (G U 16) x 512 matrix above
+    uint32_t vbytes;
+    float* part;   // G x He partial outputs
+    uint16_t* act; // the bf16 activation of the I rows (token 0)
+    int G, U, He;
+};
+
+constexpr int kFfn1Rows = 64;  // intermediate rows per workgroup
+
+// Unit u of workgroup b: u < UA a gate/up unit, (local tile tl * nss + ss) * 2
+// + matrix, local tile tl being row tile 2 (b + G (tl >> 1)) + (tl & 1);
+// UA <= u < UE down unit u - UA; past UE nothing (loads past the range read
+// zeros). Offsets and the descriptor are wave-uniform.
+__device__ __forceinline__ void ffn1_issue(const Ffn1Args& f, int b, int UA, int UE, __amdgpu_buffer_rsrc_t r0,
+                                           __amdgpu_buffer_rsrc_t r1, __amdgpu_buffer_rsrc_t rv, uint32_t voff,
+                                           u32x4 (&d)[5], int u) {
+    const int nss = f.gu.nss;
+    uint32_t off = f.gu.wbytes, step = 1024u;
+    int sel = 0;
+    if (u < UA) {
+        const int t = u >> 1, tl = t / nss, ss = t - tl * nss;
+        const int rt = 2 * (b + f.G * (tl >> 1)) + (tl & 1);
+        off = (uint32_t)rt * f.gu.rtb + (uint32_t)ss * 5120u;
+        step = ss == nss - 1 ? 256u * (uint32_t)f.gu.ng_last : 1024u;
+        sel = u & 1;
+    } else if (u < UE) {
+        off = (uint32_t)((u - UA) * f.G + b) * 5120u;  // unit-major: the workgroups' units u are neighbours
+        sel = 2;
+    }
+    off = __builtin_amdgcn_readfirstlane(off);
+    step = __builtin_amdgcn_readfirstlane(step);
+    sel = __builtin_amdgcn_readfirstlane(sel);
+    const __amdgpu_buffer_rsrc_t r = sel == 2 ? rv : (sel ? r1 : r0);
+#pragma unroll
+    for (int i = 0; i < 5; ++i) d[i] = buf_load16_so<true>(r, voff, off + step * i);
+}
+
+// ST: the activation comes from a fused residual step (a.pr_r set; bf16, one
+// token), computed in phase B's LDS before that region is used.
+template <int NW, int R, bool XB, bool ST>
+__global__ void __launch_bounds__(64 * NW) q4_ffn1_kernel(Ffn1Args f) {
+    using PA = PhaseT<R, XB, true, 1, false>;
+    using PB = PhaseT<1, true, false, 8, false>;
+    const Gemv1Args& a = f.gu;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int b = blockIdx.x;
+    const int nss = a.nss;
+    const int UA = 4 * nss * 2;
+    const int UE = UA + f.U;
+    __bf16* xsA = reinterpret_cast<__bf16*>(smem);
+    f32x4* partA = reinterpret_cast<f32x4*>(smem + (size_t)nss * 1024 * PA::SR);
+    int* next = reinterpret_cast<int*>(partA + (size_t)UA * PA::US);
+    float* aval = reinterpret_cast<float*>(next + 4);
+    unsigned char* xsB_bytes = reinterpret_cast<unsigned char*>(aval + kFfn1Rows);
+    __bf16* xsB = reinterpret_cast<__bf16*>(xsB_bytes);
+    f32x4* partB = reinterpret_cast<f32x4*>(xsB_bytes + 1024 * PB::SR);
+
+    WgWork wk;
+    wk.tg = 0;
+    wk.kq = 0;
+    wk.ntg = 1;
+    wk.nt = 4;
+    wk.s0 = 0;
+    wk.nsw = nss;
+    bool fused = false;
+    if constexpr (ST) {
+        if (a.pr_r) {
+            float* red = reinterpret_cast<float*>(xsB_bytes);  // 128 + K floats, free until the GLU epilogue
+            fused_resid_step<NW>(a, wk, xsA, red, red + 128, tid);
+            fused = true;
+        }
+    }
+    if (!fused) stage_acts<NW, R, XB, 1, false>(a, wk, xsA, tid);
+    if (tid == 0) *next = NW;
+    lds_barrier();
+
+    const __amdgpu_buffer_rsrc_t r0 = make_rsrc(a.W0, a.wbytes);
+    const __amdgpu_buffer_rsrc_t r1 = make_rsrc(a.W1, a.wbytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(f.Wv, f.vbytes);
+    const uint32_t voff = 16u * (uint32_t)lane;
+    u32x4 q[5];
+    int uk = w;
+    ffn1_issue(f, b, UA, UE, r0, r1, rv, voff, q, uk);
+
+    // ---- A: gate/up units; a wave leaves holding the loads of its first down unit
+    for (;;) {
+        int un = 0;
+        if (lane == 0) un = __hip_atomic_fetch_add(next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        un = __builtin_amdgcn_readfirstlane(un);
+        const int t = uk >> 1;
+        compute_unit_ss<R, true, 1, false>(a.nb, t % nss, 0, q, uk, xsA, partA, lane);
+        ffn1_issue(f, b, UA, UE, r0, r1, rv, voff, q, un);
+        uk = un;
+        if (un >= UA) break;
+    }
+    lds_barrier();
+
+    // GLU of local tile w (waves 0..3), as finish_tile sums and rounds it.
+    if (w < 4) {
+        const int c = lane & 3, jj = lane >> 2;
+        float y[2] = {0.0f, 0.0f};
+        for (int ss = c; ss < nss; ss += 4) {
+#pragma unroll
+            for (int n = 0; n < 2; ++n) {
+                const f32x4* sl = partA + ((size_t)(w * nss + ss) * 2 + n) * PA::US + jj;
+                float v = 0.0f;
+#pragma unroll
+                for (int p = 0; p < R; ++p) v += sl[(p >> 2) * 16][p & 3];
+                y[n] += v;
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            y[n] += dpp_f<0xB1>(y[n]);
+            y[n] += dpp_f<0x4E>(y[n]);
+        }
+        if (c == 0) {
+            const float out = glu_out<1>(y[0], y[1], a.act);
+            aval[16 * w + jj] = out;
+            const int row = 16 * (2 * (b + f.G * (w >> 1)) + (w & 1)) + jj;
+            f.act[row] = (uint16_t)(__builtin_bit_cast(uint32_t, out) >> 16);  // out holds a bf16 value
+        }
+    }
+    lds_barrier();
+    // The down units' A operand: slot (bl 4 + t) 4 + g of virtual block
+    // vb = 4 g + bl, octet t; its row rr holds the slice's octet when the block
+    // belongs to real row tile rr (vb >> 1 == rr), zeros otherwise.
+    for (int e = tid; e < 64 * PB::SR; e += 64 * NW) {
+        const int sl = e / PB::SR, rr = e - sl * PB::SR;
+        const int g = sl & 3, bt = sl >> 2, bl = bt >> 2, t = bt & 3;
+        const int vb = 4 * g + bl;
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
+        if ((vb >> 1) == rr) {
+            const float* src = aval + 32 * (vb & 1) + 8 * t;
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+                v[h] = (__builtin_bit_cast(uint32_t, src[2 * h]) >> 16) | (__builtin_bit_cast(uint32_t, src[2 * h + 1]) & 0xFFFF0000u);
+        }
+        *reinterpret_cast<u32x4*>(xsB + (size_t)e * 8) = v;
+    }
+    lds_barrier();
+
+    // ---- B: down units -------------------------------------------------------------
+    while (uk < UE) {
+        int un = 0;
+        if (lane == 0) un = __hip_atomic_fetch_add(next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        un = __builtin_amdgcn_readfirstlane(un);
+        compute_unit_ss<1, false, 8, false>(16, 0, 0, q, uk - UA, xsB, partB, lane);
+        ffn1_issue(f, b, UA, UE, r0, r1, rv, voff, q, un);
+        uk = un;
+    }
+    lds_barrier();
+
+    // ---- C: this slice's partial outputs -------------------------------------------
+    // D of down unit u: lane 16 g + j, element e = rows 128 u + 16 (4 g + e) + j.
+    const float* pb = reinterpret_cast<const float*>(partB);
+    for (int i = tid; i < f.U * 128; i += 64 * NW) {
+        const int u = i >> 7, r = i & 127, tt = r >> 4, j = r & 15;
+        f.part[(size_t)b * f.He + i] = pb[((size_t)u * 32 + (tt >> 2) * 16 + j) * 4 + (tt & 3)];
+    }
+}
+
+// Output row r = the G partials in a fixed order: thread group q (of 32)
+// adds workgroups q, q + 32, ... (its loads issued together), then the 32
+// sums in order; rows [He, H) are zeros (trimmed all-zero rows).
+constexpr int kFfn1SumRows = 32, kFfn1SumGroups = 32, kFfn1SumLoads = 8;  // G <= 256
+
+__global__ void __launch_bounds__(kFfn1SumRows * kFfn1SumGroups) ffn1_sum_kernel(const float* part, int G, int He,
+                                                                                 int H, float* Y, uint16_t* Yb) {
+    __shared__ float red[kFfn1SumGroups][kFfn1SumRows + 1];
+    const int r = threadIdx.x % kFfn1SumRows, qg = threadIdx.x / kFfn1SumRows;
+    const int row = blockIdx.x * kFfn1SumRows + r;
+    float v[kFfn1SumLoads];
+#pragma unroll
+    for (int i = 0; i < kFfn1SumLoads; ++i) {
+        const int b = qg + i * kFfn1SumGroups;
+        v[i] = row < He && b < G ? part[(size_t)b * He + row] : 0.0f;
+    }
+    float sacc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kFfn1SumLoads; ++i) sacc += v[i];
+    red[qg][r] = sacc;
+    __syncthreads();
+    if (qg == 0 && row < H) {
+        float y = 0.0f;
+        if (row < He)
+#pragma unroll
+            for (int i = 0; i < kFfn1SumGroups; ++i) y += red[i][r];
+        if (Yb)
+            Yb[row] = __builtin_bit_cast(uint16_t, (__bf16)y);
+        else
+            Y[row] = y;
+    }
 }
 
 // The split-K sums of a launch made with a.fix, after it: workgroup b adds
@@ -1089,7 +1321,10 @@ int64_t gemv_split_bytes(const GemvLaunch& L) {
 // A one-token launch whose workgroups compute their bf16 activation from a
 // fused residual step (fused_resid_step): one K split, the float row and the
 // pairwise-sum scratch after the unit counter.
-int launch_gemv_step(const GemvLaunch& L, hipStream_t s) {
+namespace {
+
+// The argument checks of a launch with a fused residual step.
+int check_step(const GemvLaunch& L) {
     const ResidStep& st = *L.step;
     if (L.M != 1 || !L.Xb || !L.tiled || L.parts != 1)
         return fail(ALV_ERR_ARG, "a fused residual step takes one token of bf16 activations on registered weights");
@@ -1104,6 +1339,15 @@ int launch_gemv_step(const GemvLaunch& L, hipStream_t s) {
     auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     if (!al(st.resid) || !al(st.y) || !al(st.sum_out) || !al(st.w_y) || !al(st.w_x))
         return fail(ALV_ERR_ALIGN, "residual-step rows and weights need 16-byte alignment");
+    return ALV_OK;
+}
+
+}  // namespace
+
+int launch_gemv_step(const GemvLaunch& L, hipStream_t s) {
+    if (int rc = check_step(L)) return rc;
+    const ResidStep& st = *L.step;
+    const int rk = st.k ? st.k : L.K;
     Gemv1Plan p;
     if (!plan_gemv1(L, 1, &p)) return fail(ALV_ERR_RANGE, "streaming GEMV: no plan for N=%d K=%d", L.N, L.K);
     if (p.ks != 1) return fail(ALV_ERR_RANGE, "a fused residual step needs the whole of K in one workgroup (K=%d)", L.K);
@@ -1138,4 +1382,46 @@ int launch_gemv(const GemvLaunch& L, hipStream_t s) {
     return ALV_OK;
 }
 
+
+// LDS bytes of q4_ffn1_kernel at nss super-steps of the hidden size.
+size_t ffn1_lds(int nss, int U, bool xb) {
+    const int SRA = xb ? 1 : 3, USA = 16, SRB = 8, USB = 32;
+    return (size_t)nss * 1024 * SRA + (size_t)8 * nss * USA * 16 + 16 + kFfn1Rows * 4 + 1024 * SRB +
+           (size_t)U * USB * 16;
+}
+
+int launch_ffn1(const GemvLaunch& up, const uint8_t* Wv, uint64_t vbytes, float* part, uint16_t* act, int G, int U,
+                int H, float* Y, uint16_t* Yb, hipStream_t s, bool sum) {
+    if (up.step)
+        if (int rc = check_step(up)) return rc;
+    Gemv1Plan p;
+    if (!plan_gemv1(up, 1, &p) || p.ks != 1) return fail(ALV_ERR_RANGE, "one-launch FFN: no one-token plan");
+    Ffn1Args f{};
+    if (int rc = fill_args(up, p, 0, 1, s, &f.gu)) return rc;
+    const bool xb = up.Xb != nullptr;
+    const size_t lds = ffn1_lds(f.gu.nss, U, xb);
+    if (lds > dev_info().lds || 8 * f.gu.nss < 16 || vbytes >= 0xFFFFE000ull || G > kFfn1SumGroups * kFfn1SumLoads)
+        return fail(ALV_ERR_RANGE, "one-launch FFN: shape outside the kernel's limits");
+    f.Wv = Wv;
+    f.vbytes = (uint32_t)vbytes;
+    f.part = part;
+    f.act = act;
+    f.G = G;
+    f.U = U;
+    f.He = 128 * U;
+    // The step's rows (128 + K floats) take phase B's region: 4 (128 + 128 U)
+    // <= 8192 + 512 U bytes for every U, so the LDS size does not change.
+    const int ki = up.step ? 2 : (xb ? 1 : 0);
+    void (*k)(Ffn1Args) = ki == 2 ? q4_ffn1_kernel<kNW, 1, true, true>
+                                  : (ki == 1 ? q4_ffn1_kernel<kNW, 1, true, false> : q4_ffn1_kernel<kNW, 3, false, false>);
+    static std::atomic<int> set[3][64];
+    if (int rc = hip_check(ensure_lds(reinterpret_cast<const void*>(k), set[ki], lds), "q4_ffn1_kernel LDS"))
+        return rc;
+    hipLaunchKernelGGL(k, dim3(G), dim3(64 * kNW), lds, s, f);
+    if (int rc = hip_check(hipGetLastError(), "q4_ffn1_kernel launch")) return rc;
+    if (!sum) return ALV_OK;
+    hipLaunchKernelGGL(ffn1_sum_kernel, dim3((H + kFfn1SumRows - 1) / kFfn1SumRows), dim3(kFfn1SumRows * kFfn1SumGroups),
+                       0, s, part, G, f.He, H, Y, Yb);
+    return hip_check(hipGetLastError(), "ffn1_sum_kernel launch");
+}
 }  // namespace alv

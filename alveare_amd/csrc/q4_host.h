@@ -165,6 +165,14 @@ int device_cus();
 // the GLU epilogue into the bf16 activation `act`, then down from it.
 void ffn_ops(alv_ffn_t w, uint16_t* act, const float* X, int ldx, float* Y, int ldy, int M, GemvLaunch (&op)[2]);
 
+// The one-token FFN in one launch (gemv1_q.hip, q4_ffn1_kernel, then the
+// partials' sum): `up` is the gate/up launch of ffn_ops at M = 1; Wv the
+// down slices (vbytes), part G x 128 U floats, act the handle's activation;
+// the output (Y fp32 or Yb bf16) has H rows, zeros past 128 U. sum = false:
+// the partials only (alv_ffn_partials).
+int launch_ffn1(const GemvLaunch& up, const uint8_t* Wv, uint64_t vbytes, float* part, uint16_t* act, int G, int U,
+                int H, float* Y, uint16_t* Yb, hipStream_t s, bool sum = true);
+
 // The launch of registered matrix w (tile_q.hip): weights, executed shape and
 // the zero rows up to its logical N; the caller adds activations and M.
 void weight_launch(const struct alv_weight* w, GemvLaunch& L);
@@ -204,5 +212,11 @@ struct alv_ffn {
     size_t a_cap;
     const uint16_t* last_a;  // activation of the last call: `a`, or the stream's prefill scratch
     int a_rows;              // tokens held at last_a after the last call
+    // One-token FFN in one launch (q4_ffn1_kernel; null vdown: the shape does
+    // not take it): the down matrix again in slice order, and G x He partials.
+    uint8_t* vdown;
+    uint64_t vdown_bytes;
+    float* part1;
+    int G1, U1;
 };
 

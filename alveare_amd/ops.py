@@ -338,6 +338,20 @@ class FfnWeights:
         with torch.cuda.device(self.device):
             check(lib().alv_ffn_gate_up(self.handle, x.data_ptr(), M, self.H, _stream(x)), "alv_ffn_gate_up")
 
+    def partials(self, X: torch.Tensor, P: torch.Tensor | None = None) -> int:
+        """Only the first launch of a one-token call (alv_ffn_partials): the
+        activation of every intermediate row and each 64-row slice's partial
+        output, G = I / 64 rows of H' floats into P (None: the handle's
+        buffer). Returns G."""
+        x = _act_in(X, self.H, "X")
+        if x.device != self.device:
+            raise ValueError(f"X on {x.device}, weights on {self.device}")
+        g = ctypes.c_int(0)
+        with torch.cuda.device(self.device):
+            check(lib().alv_ffn_partials(self.handle, x.data_ptr(), P.data_ptr() if P is not None else None,
+                                         ctypes.byref(g), _stream(x)), "alv_ffn_partials")
+        return g.value
+
     def __call__(self, X: torch.Tensor, Y: torch.Tensor | None = None, M: int = 1) -> torch.Tensor:
         x = _act_in(X, M * self.H, "X")
         if x.device != self.device:

@@ -288,7 +288,22 @@ int alv_ffn_activation(alv_ffn_t w, float* out, int M, void* stream);
  */
 int alv_ffn_gate_up(alv_ffn_t w, const float* X, int M, int ldx, void* stream);
 
-/* Shape of a registered FFN (any output pointer may be NULL). */
+/*
+ * The first of the one-token FFN's two launches alone (alv_ffn_fused at M = 1
+ * runs it, then sums): each of the G = I / 64 workgroups computes gate, up
+ * and the activation of its 64 intermediate rows and multiplies the matching
+ * 64 columns of the down matrix into a partial output, P[b * H' + r] for
+ * b < G, r < H' (H' = the executed hidden size, alv_ffn_exec_shape; P NULL:
+ * the handle's buffer). Replaces the reference's ffn_fused_npu with its
+ * Y_partial output of one row per core (kernels/ffn_fused/ffn_fused.py:28-328),
+ * which the reference's host sums (runtime/cpp/src/npu.cpp:360-377). *slices
+ * (if not NULL) receives G. One fp32 token; ALV_ERR_ARG for a registration
+ * without the one-launch form (I not a multiple of 64, H not a multiple of
+ * 128 above 512). The activation is readable with alv_ffn_activation.
+ */
+int alv_ffn_partials(alv_ffn_t w, const float* X, float* P, int* slices, void* stream);
+
+/* Shape of a registered FFN (any output pointer may be NULL). *//* Shape of a registered FFN (any output pointer may be NULL). */
 int alv_ffn_shape(alv_ffn_t w, int* H, int* I, int* act);
 
 /* Free a handle from alv_ffn_register (NULL is a no-op). Synchronises the

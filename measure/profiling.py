@@ -29,7 +29,8 @@ from collections import defaultdict
 
 Q4_KERNELS = ("q4_gemv1_kernel", "q4_gemv1_step_kernel", "gemm_q4_kernel", "tile_kernel", "rmsnorm_kernel", "qkv_post_kernel",
               "attn_partial_kernel", "attn_merge_kernel", "add_norm_kernel", "embed_kernel", "head_kernel",
-              "head_fold_kernel", "quant_kernel", "split_x_kernel", "split_fix_kernel")
+              "head_fold_kernel", "quant_kernel", "split_x_kernel", "split_fix_kernel", "q4_ffn1_kernel",
+              "ffn1_sum_kernel", "ffn1_vdown_kernel")
 CALIBRATION = "MulFunctor"  # the profile pass's copy: torch.mul(src, 1.0, out=dst)
 
 
@@ -139,6 +140,10 @@ def decode(d: str) -> str:
             tag = "final residual step + norm"
         elif "rmsnorm_kernel" in n:
             tag = "layer-0 input norm"
+        elif "q4_ffn1_kernel" in n:
+            tag = "FFN one launch + residual step" if "true, true>" in n else "FFN one launch"
+        elif "ffn1_sum_kernel" in n:
+            tag = "FFN partial sum"
         elif "q4_gemv1_step_kernel" in n:
             if "true, true, 1," in n:
                 tag = "gate/up + residual step"

@@ -600,6 +600,51 @@ def test_ffn_deterministic(orc, dev):
     ffn.close()
 
 
+@pytest.mark.parametrize("H,I", [(3840, 15360), (1152, 6912), (1024, 2048)])
+def test_ffn_one_token_both_forms(orc, dev, monkeypatch, H, I):
+    """The one-token FFN in one launch (q4_ffn1_kernel: 64 intermediate rows per
+    workgroup, the down slice's partial outputs summed in a fixed order by a
+    second launch) and in two (gate/up, then down) both meet the oracle, with
+    the same activation bit for bit; the one-launch form is deterministic."""
+    import alveare_amd as aa
+
+    _say(f"ffn one-token forms H={H} I={I}")
+    seed = orc.seed_for(2, 7) + H
+    Wg, Wu, Wd = orc.synth_q4(I, H, seed), orc.synth_q4(I, H, seed + 1), orc.synth_q4(H, I, seed + 2)
+    ffn = aa.pack_ffn_fused_weights(to_dev(Wg, dev), to_dev(Wu, dev), to_dev(Wd, dev), H, I)
+    x = orc.synth_normal(H, seed + 3)
+    acts = {}
+    for form in ("1", "0"):
+        monkeypatch.setenv("ALV_FFN_ONE", form)
+        Y = torch.empty((1, H), dtype=torch.float32, device=dev)
+        ffn(to_dev(x[None, :], dev), Y, 1)
+        acts[form] = ffn.last_activation(1).cpu().numpy()[0]
+        st = parity.ffn_check(orc, Wg, Wu, Wd, x, H, I, 0, Y.cpu().numpy()[0], acts[form])
+        _say(f"  ALV_FFN_ONE={form}: {st}")
+        if form == "1":
+            Y2 = torch.empty_like(Y)
+            ffn(to_dev(x[None, :], dev), Y2, 1)
+            assert torch.equal(Y, Y2)
+            # The first launch alone (alv_ffn_partials): one partial output per
+            # 64-row slice; the output is their sum in the summing launch's
+            # order (group q of 32 adds slices q, q + 32, ..., then the groups
+            # in order), bit for bit.
+            P = torch.empty((I // 64) * H, dtype=torch.float32, device=dev)
+            G = ffn.partials(to_dev(x, dev), P)
+            assert G == I // 64
+            Pn = P.cpu().numpy().reshape(G, H)
+            grp = [np.zeros(H, np.float32) for _ in range(32)]
+            for q in range(32):
+                for b in range(q, G, 32):
+                    grp[q] = (grp[q] + Pn[b]).astype(np.float32)
+            want = np.zeros(H, np.float32)
+            for q in range(32):
+                want = (want + grp[q]).astype(np.float32)
+            assert np.array_equal(want, Y.cpu().numpy()[0])
+    assert np.array_equal(acts["1"], acts["0"])
+    ffn.close()
+
+
 # ---- runtime/py dispatch -------------------------------------------------------------
 
 def test_dispatch_entry_points(orc, dev):
