@@ -61,7 +61,7 @@ def layer_bytes() -> dict:
 # partial; one fp32 token, registered weights): the layer's dominant kernel.
 ROOFLINE_KERNEL = "q4_ffn1_kernel<16, 3, false, false>"
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                            "q4_gemv1_traffic_gemma12b_decode.txt")
+                            "q4_ffn1_traffic_gemma12b_decode.txt")
 CALIBRATION_BYTES = 256 << 20
 
 
