@@ -391,6 +391,16 @@ extern "C" int alv_ffn_fused_noalloc(alv_ffn_t w, const float* X, float* Y, int 
     if (dev != w->device) return fail(ALV_ERR_HANDLE, "FFN handle belongs to device %d, current device is %d", w->device, dev);
     GemvLaunch op[2];
     ffn_ops(w, w->a, X, ldx, Y, ldy, M, op);
+    if (M == 1 && w->vdown && ffn1_on()) {
+        // The one-launch form, as alv_ffn_fused takes it: its partials live in
+        // the handle (allocated at registration), so the call allocates nothing.
+        if (int rc = launch_ffn1(op[0], w->vdown, w->vdown_bytes, w->part1, w->a, w->G1, w->U1, w->H, Y, nullptr,
+                                 (hipStream_t)stream))
+            return rc;
+        w->last_a = w->a;
+        w->a_rows = 1;
+        return ALV_OK;
+    }
     for (const GemvLaunch& L : op) {
         const int64_t need = gemv_split_bytes(L);
         if (need < 0) return fail(ALV_ERR_RANGE, "no launch plan for M=%d H=%d I=%d", M, w->H, w->I);

@@ -34,7 +34,7 @@ def test_ffn_noalloc_matches_allocating_entry_point(orc, dev):
     Wg, Wu, Wd = orc.synth_q4(I, H, seed), orc.synth_q4(I, H, seed + 1), orc.synth_q4(H, I, seed + 2)
     ffn = aa.pack_ffn_fused_weights(to_dev(Wg, dev), to_dev(Wu, dev), to_dev(Wd, dev), H, I)
     st = torch.cuda.current_stream().cuda_stream
-    for M in (16, 3):  # 16 tokens split K in gate/up and down; the second call is smaller
+    for M in (16, 3, 1):  # 16 tokens split K in gate/up and down; then smaller calls (1: the one-launch form)
         _say(f"ffn noalloc M={M}")
         X = orc.synth_normal(M * H, seed + 10 + M).reshape(M, H)
         Xd = to_dev(X, dev)
