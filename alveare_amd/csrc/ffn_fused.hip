@@ -1,7 +1,13 @@
 // Fused FFN (gate/up projection, GLU activation, down projection) on gfx950:
 // alv_ffn_register / alv_ffn_fused / alv_ffn_shape / alv_ffn_release.
 //
-// Decode (M <= 16): two launches of the streaming kernel (gemv1_q.hip).
+// One token (when the registration has the slice-ordered down matrix): one
+// streaming launch plus a summing launch (gemv1_q.hip, q4_ffn1_kernel): each
+// workgroup computes gate, up and the activation of 64 intermediate rows and
+// multiplies their 64 down columns into a partial output, as the reference's
+// NPU cores do with their slices (kernels/ffn_fused/ffn_fused.py:28-328); the
+// partials are summed in a fixed order on the device.
+// Decode (M <= 16) otherwise: two launches of the streaming kernel (gemv1_q.hip).
 //   1. gate and up tiles of the same rows are streamed by the same workgroup
 //      against the same activation operands; the epilogue rounds both to
 //      bf16, applies the GLU and rounds the activation to bf16 -- the
